@@ -1,0 +1,99 @@
+"""ctypes binding of the C ABI in include/flagsparse_hip.h.
+
+The library is loaded after ``import torch`` so that its libamdhip64.so.7 dependency
+resolves to the HIP runtime torch already loaded (same SONAME): device pointers and
+``hipStream_t`` handles from torch are then valid in the library.  A missing library is an
+error - there is no fallback compute path.
+"""
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the HIP runtime first; see module docstring)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libflagsparse_hip.so")
+
+FSP_F32 = 0
+FSP_F64 = 1
+ABI_VERSION = 1
+
+_lib = None
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes); kept in the order of include/flagsparse_hip.h.
+SIGNATURES = {
+    "fsp_last_error": (ctypes.c_char_p, []),
+    "fsp_abi_version": (_i32, []),
+    "fsp_spmv_stream_nnz_cap": (_i64, []),
+    "fsp_spmv_stream_rows_cap": (_i64, []),
+    "fsp_spmv_chunk_nnz_cap": (_i64, []),
+    "fsp_spmm_block_nnz_cap": (_i64, []),
+    "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
+                            _i64, _p, _p, _i32, _p]),
+    "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
+    "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
+                            _i64, _i64, _i32, _i32, _p, _p, _i32, _p]),
+}
+
+
+class HipLibraryError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def lib():
+    """The loaded library (loaded on first use)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"flagsparse_amd HIP library not found at {LIB_PATH}; build it with "
+                "`python -m flagsparse_amd._build` (there is no CPU fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        version = handle.fsp_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libflagsparse_hip.so ABI {version}, expected {ABI_VERSION}; rebuild")
+        _lib = handle
+    return _lib
+
+
+def check(status, what):
+    if status != 0:
+        msg = lib().fsp_last_error().decode(errors="replace")
+        raise HipLibraryError(f"{what} failed (status {status}): {msg}")
+
+
+def dtype_code(dtype):
+    if dtype == torch.float32:
+        return FSP_F32
+    if dtype == torch.float64:
+        return FSP_F64
+    raise TypeError(f"no gfx950 kernel for value dtype {dtype}")
+
+
+def ptr(t):
+    """Device (or host) address of a tensor's first element; None for absent tensors."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device):
+    """hipStream_t of torch's current stream on ``device``."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def caps():
+    """Kernel capacities compiled into the library."""
+    L = lib()
+    return {
+        "spmv_stream_nnz": int(L.fsp_spmv_stream_nnz_cap()),
+        "spmv_stream_rows": int(L.fsp_spmv_stream_rows_cap()),
+        "spmv_chunk_nnz": int(L.fsp_spmv_chunk_nnz_cap()),
+        "spmm_block_nnz": int(L.fsp_spmm_block_nnz_cap()),
+    }

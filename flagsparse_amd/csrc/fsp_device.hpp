@@ -1,0 +1,142 @@
+// Device-side building blocks shared by the SpMV / SpMM kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fsp {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;               // threads per workgroup (4 waves)
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+
+// Streaming loads: the matrix arrays are read exactly once per call, so they are fetched
+// with the non-temporal hint and do not displace x / B lines from L2 and the MALL.
+template <bool NT, typename V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
+// Four consecutive matrix entries ("a quad"): values converted to the accumulator type.
+// base is a multiple of 4, so the 16-byte vector loads are aligned when the array base is.
+// Entries outside [lo, hi) are returned with val = 0 and col = -1.
+template <bool NT, typename T>
+struct QuadLoader;
+
+template <bool NT>
+struct QuadLoader<NT, float> {
+  template <typename P>
+  __device__ __forceinline__ static void load(const float* __restrict__ vals,
+                                              const int* __restrict__ cols, P base, P lo,
+                                              P hi, P nnz_total, float (&v)[4], int (&c)[4]) {
+    if (base + 4 <= nnz_total) {
+      f32x4 vv = ld_stream<NT>(reinterpret_cast<const f32x4*>(vals + base));
+      i32x4 cc = ld_stream<NT>(reinterpret_cast<const i32x4*>(cols + base));
+      v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
+      c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = base + j < nnz_total;
+        v[j] = ok ? vals[base + j] : 0.0f;
+        c[j] = ok ? cols[base + j] : -1;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = (base + j >= lo) && (base + j < hi);
+      if (!in) { v[j] = 0.0f; c[j] = -1; }
+    }
+  }
+};
+
+template <bool NT>
+struct QuadLoader<NT, double> {
+  template <typename P>
+  __device__ __forceinline__ static void load(const double* __restrict__ vals,
+                                              const int* __restrict__ cols, P base, P lo,
+                                              P hi, P nnz_total, double (&v)[4], int (&c)[4]) {
+    if (base + 4 <= nnz_total) {
+      f64x2 v01 = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + base));
+      f64x2 v23 = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + base + 2));
+      i32x4 cc = ld_stream<NT>(reinterpret_cast<const i32x4*>(cols + base));
+      v[0] = v01.x; v[1] = v01.y; v[2] = v23.x; v[3] = v23.y;
+      c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = base + j < nnz_total;
+        v[j] = ok ? vals[base + j] : 0.0;
+        c[j] = ok ? cols[base + j] : -1;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = (base + j >= lo) && (base + j < hi);
+      if (!in) { v[j] = 0.0; c[j] = -1; }
+    }
+  }
+};
+
+// Butterfly sum over aligned groups of g lanes (g a power of two, g <= 64).  Every lane of
+// the group ends with the same value; the pairing order is fixed, so the result is
+// deterministic.  All lanes of a group must be active.
+template <typename A>
+__device__ __forceinline__ A group_sum(A v, int g) {
+  for (int off = 1; off < g; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <typename A>
+__device__ __forceinline__ A wave_sum(A v) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Workgroup sum in a fixed order: butterfly inside each wave, then waves 0..3 in order.
+// Result valid in every thread.  red must hold kWavesPerBlock entries.
+template <typename A>
+__device__ __forceinline__ A block_sum(A v, A* red) {
+  v = wave_sum(v);
+  const int tid = threadIdx.x;
+  __syncthreads();  // red may still be read by a previous call
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
+  __syncthreads();
+  A t = red[0];
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) t += red[w];
+  return t;
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup i runs on XCD i % 8).
+// Remap so that XCD k processes one contiguous range of logical blocks: neighbouring rows
+// (which share x / B lines) then meet in the same L2.  Bijective for any n.
+__device__ __forceinline__ int xcd_logical_block(int i, int n) {
+  constexpr int kXcd = 8;
+  const int q = n / kXcd, r = n % kXcd;
+  const int x = i % kXcd, j = i / kXcd;
+  return (x < r) ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+}
+
+// Agent-scope accesses for the cross-workgroup partial sums: the XCD L2s are not coherent
+// with each other, so partials and tickets go through these.
+template <typename A>
+__device__ __forceinline__ void store_agent(A* p, A v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename A>
+__device__ __forceinline__ A load_agent(const A* p) {
+  return __hip_atomic_load(const_cast<A*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace fsp

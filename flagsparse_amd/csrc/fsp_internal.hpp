@@ -1,0 +1,25 @@
+// Host-side helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "flagsparse_hip.h"
+
+namespace fsp {
+
+// Kernel capacities (see the kernels for why each value is what it is).
+constexpr int64_t kSpmvStreamSlots = 2048;               // LDS product slots per short-row block
+constexpr int64_t kSpmvStreamNnzCap = kSpmvStreamSlots - 3;
+constexpr int64_t kSpmvStreamRowsCap = 1024;
+constexpr int64_t kSpmvChunkUnitsPerThread = 4;
+constexpr int64_t kSpmvChunkCap = kSpmvChunkUnitsPerThread * 4 * 256 - 3;
+constexpr int64_t kSpmmSlots = 2048;                     // LDS (col, val) slots per SpMM block
+constexpr int64_t kSpmmNnzCap = kSpmmSlots - 3;
+
+int set_error(int code, const std::string& msg);
+int check_hip(hipError_t e, const char* what);
+
+}  // namespace fsp

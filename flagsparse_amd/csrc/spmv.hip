@@ -1,0 +1,288 @@
+// CSR / COO-run SpMV for gfx950: one fused launch over a row-block descriptor table.
+//
+// Reference behaviour followed (src/flagsparse/sparse_operations/):
+//   spmv_csr.py:94-120    base kernel: y[row] = sum over the row's nnz, fp32 summed in fp64
+//                         (spmv_csr.py:498-536 casts to fp64 and back)
+//   spmv_csr.py:161-279   opt kernels: native-precision accumulation (use_opt=True)
+//   spmv_coo.py:51-108    row-run kernel: one output row per run, rows without a run are 0
+//   spmv_coo.py:111-150   atomic kernel for unsorted COO
+//
+// Work decomposition (MI355X-first, not the reference's bucket launches):
+//   * short-row block  {r0, r1, 0, 0}: the block's contiguous nnz range (<= 2045 entries) is
+//     read with 16-byte loads, one quad of entries per thread and step; products go to LDS;
+//     then each row is summed by a group of G lanes (G = 256 / next_pow2(rows), <= 64) with a
+//     butterfly shuffle reduction.
+//   * long-row chunk   {row, k, nch, part}: 256 threads sum <= 4093 entries of one row in
+//     registers, reduce across the workgroup; with nch > 1 the chunk sum goes to partials[]
+//     and the last-arriving workgroup (ticket counter) adds partials[part .. part+nch) in
+//     index order, so the result does not depend on arrival order.
+#include "fsp_device.hpp"
+#include "fsp_internal.hpp"
+
+namespace fsp {
+namespace {
+
+constexpr int kStreamSlots = (int)kSpmvStreamSlots;
+constexpr int kStreamRows = (int)kSpmvStreamRowsCap;
+constexpr int kStreamUPT = kStreamSlots / (4 * kBlock);  // quads per thread in a short-row block
+constexpr int kChunkUPT = (int)kSpmvChunkUnitsPerThread;
+static_assert(kStreamUPT * 4 * kBlock == kStreamSlots, "stream slots must be whole quads per thread");
+
+template <typename T, typename A, typename P, bool NT>
+__global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
+    const T* __restrict__ vals, const int* __restrict__ cols, const P* __restrict__ rowptr,
+    P nnz_total, const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
+    const i32x4* __restrict__ desc, int n_desc, P chunk, A* __restrict__ partials,
+    unsigned* __restrict__ tickets, int xcd_remap) {
+  __shared__ A s_prod[kStreamSlots];
+  __shared__ P s_ptr[kStreamRows + 1];
+  __shared__ A s_red[kWavesPerBlock];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  int b = blockIdx.x;
+  if (xcd_remap) b = xcd_logical_block(b, n_desc);
+  const i32x4 d = desc[b];
+
+  if (d.z == 0) {
+    // ---------------- short-row block: rows [r0, r0 + R) ----------------
+    const int r0 = d.x, R = d.y - d.x;
+    if (R <= 0 || R > kStreamRows) return;  // not a planner descriptor; uniform per block
+    for (int i = tid; i <= R; i += kBlock) s_ptr[i] = rowptr[r0 + i];
+    __syncthreads();
+    const P lo = s_ptr[0], hi = s_ptr[R];
+    if (hi - lo > P(kSpmvStreamNnzCap)) return;  // uniform per block
+    const P s0 = lo & ~P(3);
+
+    T v[kStreamUPT][4];
+    int c[kStreamUPT][4];
+#pragma unroll
+    for (int u = 0; u < kStreamUPT; ++u) {
+      const P base = s0 + P(4) * (tid + u * kBlock);
+      if (base < hi) {
+        QuadLoader<NT, T>::load(vals, cols, base, lo, hi, nnz_total, v[u], c[u]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { v[u][j] = T(0); c[u][j] = -1; }
+      }
+    }
+    T xv[kStreamUPT][4];
+#pragma unroll
+    for (int u = 0; u < kStreamUPT; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[u][j] = c[u][j] >= 0 ? x[c[u][j]] : T(0);
+#pragma unroll
+    for (int u = 0; u < kStreamUPT; ++u) {
+      const P base = s0 + P(4) * (tid + u * kBlock);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c[u][j] >= 0) s_prod[(int)(base + j - lo)] = A(v[u][j]) * A(xv[u][j]);
+    }
+    __syncthreads();
+
+    // Lanes per row: the largest power of two G <= 64 with G * next_pow2(R) <= 256.
+    int lg = 0;
+    if (R < kBlock) {
+      int p2 = 1, lp = 0;
+      while (p2 < R) { p2 <<= 1; ++lp; }
+      lg = 8 - lp;  // log2(256 / p2)
+      if (lg > 6) lg = 6;
+    }
+    const int G = 1 << lg;
+    const int ngrp = kBlock >> lg;
+    const int grp = tid >> lg, lane = tid & (G - 1);
+    // With G > 1, ngrp >= R, so each group runs at most one iteration and its lanes stay
+    // converged for the shuffles.
+    for (int r = grp; r < R; r += ngrp) {
+      const int a = (int)(s_ptr[r] - lo), e = (int)(s_ptr[r + 1] - lo);
+      A acc = A(0);
+      for (int i = a + lane; i < e; i += G) acc += s_prod[i];
+      if (G > 1) acc = group_sum(acc, G);
+      if (lane == 0) {
+        const int row = r0 + r;
+        y[row_map ? row_map[row] : row] = T(acc);
+      }
+    }
+    return;
+  }
+
+  // ---------------- long-row chunk ----------------
+  const int row = d.x, k = d.y, nch = d.z, part = d.w;
+  const P rs = rowptr[row], re = rowptr[row + 1];
+  const P lo = rs + P(k) * chunk;
+  const P hi = (lo + chunk < re) ? lo + chunk : re;
+  const P s0 = lo & ~P(3);
+
+  T v[kChunkUPT][4];
+  int c[kChunkUPT][4];
+#pragma unroll
+  for (int u = 0; u < kChunkUPT; ++u) {
+    const P base = s0 + P(4) * (tid + u * kBlock);
+    if (base < hi) {
+      QuadLoader<NT, T>::load(vals, cols, base, lo, hi, nnz_total, v[u], c[u]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { v[u][j] = T(0); c[u][j] = -1; }
+    }
+  }
+  T xv[kChunkUPT][4];
+#pragma unroll
+  for (int u = 0; u < kChunkUPT; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[u][j] = c[u][j] >= 0 ? x[c[u][j]] : T(0);
+  A acc = A(0);
+#pragma unroll
+  for (int u = 0; u < kChunkUPT; ++u)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += A(v[u][j]) * A(xv[u][j]);
+
+  const A total = block_sum(acc, s_red);
+  const int out_row = row_map ? row_map[row] : row;
+  if (nch == 1) {
+    if (tid == 0) y[out_row] = T(total);
+    return;
+  }
+  if (tid == 0) {
+    store_agent(&partials[part + k], total);
+    __threadfence();
+    const unsigned t = atomicAdd(&tickets[part], 1u);
+    __threadfence();
+    s_last = (t == unsigned(nch - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  A a = A(0);
+  for (int i = tid; i < nch; i += kBlock) a += load_agent(&partials[part + i]);
+  const A fin = block_sum(a, s_red);
+  if (tid == 0) {
+    y[out_row] = T(fin);
+    store_agent(&tickets[part], 0u);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_zero_kernel(T* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) y[i] = T(0);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void spmv_coo_atomic_kernel(
+    const T* __restrict__ vals, const int* __restrict__ rows, const int* __restrict__ cols,
+    int64_t nnz, const T* __restrict__ x, T* __restrict__ y, int64_t per_block) {
+  const int64_t begin = (int64_t)blockIdx.x * per_block;
+  int64_t end = begin + per_block;
+  if (end > nnz) end = nnz;
+  for (int64_t i = begin + threadIdx.x; i < end; i += kBlock)
+    atomicAdd(&y[rows[i]], vals[i] * x[cols[i]]);
+}
+
+template <typename T>
+int launch_fill(T* y, int64_t n, hipStream_t st) {
+  if (n <= 0) return FSP_OK;
+  int64_t blocks = (n + kBlock - 1) / kBlock;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_zero_kernel<T>, dim3((unsigned)blocks), dim3(kBlock), 0, st, y, n);
+  return check_hip(hipGetLastError(), "fill_zero_kernel launch");
+}
+
+template <typename T, typename A, typename P>
+int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
+                const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                uint32_t* tickets, int xcd_remap, hipStream_t st) {
+  if (row_map) {
+    int rc = launch_fill<T>(static_cast<T*>(y), n_out, st);
+    if (rc) return rc;
+  }
+  if (n_desc == 0) return FSP_OK;
+  hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, true>), dim3((unsigned)n_desc), dim3(kBlock),
+                     0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
+                     (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
+                     reinterpret_cast<const i32x4*>(desc), (int)n_desc, (P)chunk,
+                     static_cast<A*>(partials), tickets, xcd_remap);
+  return check_hip(hipGetLastError(), "spmv_rowblock_kernel launch");
+}
+
+template <typename T, typename A>
+int dispatch_ptr(int rowptr_bits, const void* vals, const int32_t* cols, const void* rowptr,
+                 int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                 uint32_t* tickets, int xcd_remap, hipStream_t st) {
+  if (rowptr_bits == 32)
+    return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
+                                  chunk, partials, tickets, xcd_remap, st);
+  return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
+                                    chunk, partials, tickets, xcd_remap, st);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace fsp
+
+using namespace fsp;
+
+extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
+                            const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
+                            const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                            const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                            uint32_t* tickets, int xcd_remap, void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_csr: dtype");
+  if (rowptr_bits != 32 && rowptr_bits != 64)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: rowptr_bits must be 32 or 64");
+  if (n_rows < 0 || nnz < 0 || n_desc < 0 || n_out < 0)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: negative size");
+  if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: more than 2^31-1 rows or descriptors");
+  if (rowptr_bits == 32 && nnz > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: nnz exceeds int32 rowptr range");
+  if (chunk < 1 || chunk > kSpmvChunkCap)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: chunk outside [1, fsp_spmv_chunk_nnz_cap()]");
+  if (n_desc > 0 && (!rowptr || !y || !desc))
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
+  if (nnz > 0 && (!vals || !cols || !x)) return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
+  if (!aligned16(vals) || !aligned16(cols) || !aligned16(desc))
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: vals, cols and desc must be 16-byte aligned");
+  if (row_map && !y) return set_error(FSP_EINVAL, "fsp_spmv_csr: null y");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FSP_F32) {
+    if (acc_f64)
+      return dispatch_ptr<float, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
+                                         desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+    return dispatch_ptr<float, float>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
+                                      desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+  }
+  return dispatch_ptr<double, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
+                                      desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+}
+
+extern "C" int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows,
+                                   const int32_t* cols, int64_t nnz, const void* x, void* y,
+                                   int64_t n_rows, int64_t nnz_per_block, void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64)
+    return set_error(FSP_ENOTSUP, "fsp_spmv_coo_atomic: dtype");
+  if (nnz < 0 || n_rows < 0 || nnz_per_block < 1)
+    return set_error(FSP_EINVAL, "fsp_spmv_coo_atomic: bad size");
+  if (n_rows > 0 && !y) return set_error(FSP_EINVAL, "fsp_spmv_coo_atomic: null y");
+  if (nnz > 0 && (!vals || !rows || !cols || !x))
+    return set_error(FSP_EINVAL, "fsp_spmv_coo_atomic: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t blocks = (nnz + nnz_per_block - 1) / nnz_per_block;
+  if (blocks > 0x7fffffffLL) return set_error(FSP_EINVAL, "fsp_spmv_coo_atomic: grid too large");
+  if (dtype == FSP_F32) {
+    int rc = launch_fill<float>(static_cast<float*>(y), n_rows, st);
+    if (rc || nnz == 0) return rc;
+    hipLaunchKernelGGL(spmv_coo_atomic_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                       static_cast<const float*>(vals), rows, cols, nnz,
+                       static_cast<const float*>(x), static_cast<float*>(y), nnz_per_block);
+  } else {
+    int rc = launch_fill<double>(static_cast<double*>(y), n_rows, st);
+    if (rc || nnz == 0) return rc;
+    hipLaunchKernelGGL(spmv_coo_atomic_kernel<double>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                       static_cast<const double*>(vals), rows, cols, nnz,
+                       static_cast<const double*>(x), static_cast<double*>(y), nnz_per_block);
+  }
+  return check_hip(hipGetLastError(), "spmv_coo_atomic_kernel launch");
+}

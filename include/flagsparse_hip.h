@@ -1,0 +1,121 @@
+/*
+ * flagsparse_hip.h - C ABI of the MI355X (gfx950) CSR/COO SpMV and CSR SpMM library.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed as void*.
+ * Nothing here allocates device memory: workspaces (partials, tickets, descriptor tables)
+ * are owned by the caller, which sizes them from the plan functions below.
+ * Every function returns 0 on success or a negative fsp_status; fsp_last_error() then
+ * holds a message for the calling thread.  No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (paths relative to the FlagSparse source tree,
+ * src/flagsparse/sparse_operations/):
+ *   fsp_plan_row_blocks  - bucket/split planning of spmv_csr.py:281-327 (_build_spmv_opt_buckets)
+ *                          and spmm_csr.py:417-477 (_build_spmm_opt_split_metadata,
+ *                          _build_spmm_opt_buckets); one descriptor table replaces the
+ *                          per-bucket row lists.
+ *   fsp_spmv_csr         - the Triton launches of spmv_csr.py:329-376
+ *                          (_triton_spmv_csr_impl_opt_prepared, use_opt=True) and
+ *                          spmv_csr.py:510-536 (_triton_spmv_csr_impl_prepared, default
+ *                          path, fp32 accumulated in fp64); with row_map != NULL it also
+ *                          replaces the row-run launch of spmv_coo.py:254-268 (_spmv_coo_seg_*).
+ *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
+ *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
+ *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
+ *                          long-row split).
+ */
+#ifndef FLAGSPARSE_HIP_H
+#define FLAGSPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Value type of data / x / y / B / C. */
+enum fsp_dtype { FSP_F32 = 0, FSP_F64 = 1 };
+
+enum fsp_status {
+  FSP_OK = 0,
+  FSP_EINVAL = -1,   /* bad argument (sizes, null pointers, alignment, unsupported combo) */
+  FSP_EHIP = -2,     /* a HIP runtime call failed */
+  FSP_ENOTSUP = -3   /* dtype / index width not built */
+};
+
+/* Message for the last failing call made by this thread ("" if none). */
+const char* fsp_last_error(void);
+
+/* ABI revision of this header (bumped on any signature change). */
+int fsp_abi_version(void);
+
+/* Kernel capacities the planner must respect (fixed at build time). */
+int64_t fsp_spmv_stream_nnz_cap(void);   /* max nnz of one short-row block            */
+int64_t fsp_spmv_stream_rows_cap(void);  /* max rows of one short-row block           */
+int64_t fsp_spmv_chunk_nnz_cap(void);    /* max nnz of one long-row chunk             */
+int64_t fsp_spmm_block_nnz_cap(void);    /* max nnz of one SpMM row block / row part  */
+
+/*
+ * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
+ * COO run offsets).  Rows are packed greedily, in row order, into descriptors of 4 int32:
+ *   short-row block : {row_begin, row_end, 0, 0}      rows with len <= long_threshold,
+ *                                                      block nnz <= nnz_cap, rows <= rows_cap
+ *   long-row chunk  : {row, k, nchunks, part_base}    row split into ceil(len/chunk) chunks;
+ *                                                      part_base = -1 when nchunks == 1
+ * Pass desc_out == NULL to only count.  Outputs: number of descriptors, number of partial
+ * slots (sum of nchunks over rows with nchunks > 1) and number of split rows.
+ * Requires 1 <= long_threshold <= nnz_cap, rows_cap >= 1, chunk >= 1.
+ */
+int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
+                        int64_t rows_cap, int64_t long_threshold, int64_t chunk,
+                        int32_t* desc_out, int64_t* n_desc, int64_t* n_parts,
+                        int64_t* n_split_rows);
+
+/*
+ * y = A @ x for CSR A (or COO row runs when row_map != NULL).
+ *   dtype      FSP_F32 / FSP_F64 (vals, x, y)
+ *   acc_f64    1: accumulate in fp64 (reference default path for fp32), 0: native type
+ *   vals,cols  nnz entries; cols int32; both 16-byte aligned
+ *   rowptr     n_rows+1 offsets, int32 (rowptr_bits=32) or int64 (64)
+ *   row_map    NULL: output row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
+ *   desc       n_desc descriptors from fsp_plan_row_blocks with the caps above
+ *   partials   >= n_parts slots of 8 bytes; tickets >= n_parts uint32, all zero on entry
+ *              (the kernel leaves them zero again).  Calls sharing a workspace must not overlap.
+ *   chunk      the chunk size the plan was built with (<= fsp_spmv_chunk_nnz_cap())
+ *   xcd_remap  1: place consecutive descriptors on the same XCD (L2 locality of x)
+ */
+int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
+                 const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
+                 const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                 uint32_t* tickets, int xcd_remap, void* stream);
+
+/*
+ * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)
+ * is zeroed first.  Accumulation order, and so the last bits of y, are not deterministic.
+ * nnz_per_block: entries per 256-thread workgroup (reference block_size knob).
+ */
+int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows, const int32_t* cols,
+                        int64_t nnz, const void* x, void* y, int64_t n_rows,
+                        int64_t nnz_per_block, void* stream);
+
+/*
+ * C[n_rows, N] = A @ B for CSR A and row-major B[n_cols, ldb] (N columns used).
+ *   lanes_per_row  G in {1,2,4,...,64}: lanes sharing one B row; the plan must have been
+ *                  built with rows_cap <= 256/G and nnz_cap <= fsp_spmm_block_nnz_cap()
+ *   vec            elements per lane per load: 4 (fp32) / 2 (fp64) for 16-byte loads, or 1;
+ *                  vec > 1 requires ldb, ldc, N multiples of vec and 16-byte aligned B, C
+ *   partials       >= n_parts * N slots of 8 bytes; tickets >= n_parts * n_tiles uint32 zeroed,
+ *                  n_tiles = ceil(N / (G*vec)).  Calls sharing a workspace must not overlap.
+ */
+int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
+                 const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
+                 const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc,
+                 const int32_t* desc, int64_t n_desc, int64_t chunk, int lanes_per_row,
+                 int vec, void* partials, uint32_t* tickets, int xcd_remap, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLAGSPARSE_HIP_H */

@@ -120,6 +120,77 @@ def spmm_csr(indptr, indices, data, B):
     return C
 
 
+def time_spmv_csr(indptr, indices, data, x, min_seconds=10.0, max_passes=1000):
+    """Time the fp64 oracle SpMV on one core: full passes until ``min_seconds`` elapsed.
+
+    Inputs are converted once, outside the timing.  Returns (passes, seconds).  Used only as
+    bench.py's reported CPU baseline.
+    """
+    import time
+
+    ip = _np(indptr, np.int64)
+    ix = _np(indices, np.int64)
+    dv = _np(data, np.float64)
+    xv = _np(x, np.float64)
+    n_rows = ip.size - 1
+    y = np.zeros(n_rows, dtype=np.float64)
+    fn = _load().oracle_spmv_csr_f64
+    args = (n_rows, _ptr(ip), _ptr(ix), _ptr(dv), _ptr(xv), None, _ptr(y))
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        fn(*args)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= min_seconds or passes >= max_passes:
+            return passes, elapsed
+
+
+def time_spmm_csr(indptr, indices, data, B, min_seconds=10.0, max_passes=1000, row_limit=None):
+    """Time the fp64 oracle SpMM on one core over the first ``row_limit`` rows (all by
+    default).  Returns (passes, seconds, rows, nnz_in_rows)."""
+    import time
+
+    ip = _np(indptr, np.int64)
+    n_rows = ip.size - 1 if row_limit is None else min(int(row_limit), ip.size - 1)
+    ix = _np(indices, np.int64)
+    dv = _np(data, np.float64)
+    Bv = _np(B, np.float64)
+    N = Bv.shape[1]
+    C = np.zeros((n_rows, N), dtype=np.float64)
+    fn = _load().oracle_spmm_csr_f64
+    args = (n_rows, _ptr(ip), _ptr(ix), _ptr(dv), _ptr(Bv), N, N, _ptr(C), N)
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        fn(*args)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= min_seconds or passes >= max_passes:
+            return passes, elapsed, n_rows, int(ip[n_rows] - ip[0])
+
+
+def time_spmv_coo(row, col, data, x, n_rows, min_seconds=10.0, max_passes=1000):
+    """Time the fp64 oracle COO SpMV on one core.  Returns (passes, seconds)."""
+    import time
+
+    r = _np(row, np.int64)
+    c = _np(col, np.int64)
+    dv = _np(data, np.float64)
+    xv = _np(x, np.float64)
+    y = np.zeros(n_rows, dtype=np.float64)
+    fn = _load().oracle_spmv_coo_f64
+    args = (r.size, _ptr(r), _ptr(c), _ptr(dv), _ptr(xv), n_rows, _ptr(y))
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        fn(*args)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= min_seconds or passes >= max_passes:
+            return passes, elapsed
+
+
 # ----------------------------------------------------------------------------------------
 # SpMV planning semantics
 # ----------------------------------------------------------------------------------------

@@ -1,0 +1,142 @@
+"""C-ABI library checks that need no GPU: it loads, exports every function declared in
+include/flagsparse_hip.h, reports its capacities, and its host-side row-block planner
+(fsp_plan_row_blocks) produces tables with the invariants the kernels rely on.  Argument
+checks of the kernel entry points are exercised where they reject a call before any HIP
+runtime call is made."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import flagsparse_amd as fs
+from flagsparse_amd import _abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flagsparse_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fsp_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_abi.LIB_PATH)
+    names = _declared_functions()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes table covers exactly the declared functions
+    assert sorted(_abi.SIGNATURES) == names
+
+
+def test_abi_version_and_caps():
+    L = _abi.lib()
+    assert L.fsp_abi_version() == _abi.ABI_VERSION
+    caps = _abi.caps()
+    assert caps["spmv_stream_nnz"] >= 1 and caps["spmv_chunk_nnz"] >= caps["spmv_stream_nnz"]
+    assert caps["spmv_stream_rows"] >= 1 and caps["spmm_block_nnz"] >= 1
+    assert L.fsp_last_error() is not None
+
+
+def _plan(rowptr, nnz_cap, rows_cap, thr, chunk):
+    L = _abi.lib()
+    rp = np.ascontiguousarray(rowptr, dtype=np.int64)
+    nd, npart, nsplit = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    args = (rp.ctypes.data_as(ctypes.c_void_p), rp.size - 1, nnz_cap, rows_cap, thr, chunk)
+    rc = L.fsp_plan_row_blocks(*args, None, ctypes.byref(nd), ctypes.byref(npart),
+                               ctypes.byref(nsplit))
+    if rc != 0:
+        return rc, L.fsp_last_error().decode(), None, None, None
+    desc = np.zeros((nd.value, 4), dtype=np.int32)
+    rc = L.fsp_plan_row_blocks(*args, desc.ctypes.data_as(ctypes.c_void_p), ctypes.byref(nd),
+                               ctypes.byref(npart), ctypes.byref(nsplit))
+    return rc, desc, npart.value, nsplit.value, None
+
+
+def _check_plan(lengths, nnz_cap, rows_cap, thr, chunk):
+    rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    rc, desc, n_parts, n_split, _ = _plan(rowptr, nnz_cap, rows_cap, thr, chunk)
+    assert rc == 0, desc
+    n = len(lengths)
+    next_row = 0
+    part_cursor = 0
+    split_rows = 0
+    i = 0
+    while i < desc.shape[0]:
+        a, b, c, d = (int(v) for v in desc[i])
+        if c == 0:  # short-row block [a, b)
+            assert a == next_row and b > a
+            assert b - a <= rows_cap
+            blk = lengths[a:b]
+            assert np.all(blk <= thr) and blk.sum() <= nnz_cap
+            # greedy: the block stops only where the next row breaks a cap
+            if b < n:
+                nxt = lengths[b]
+                assert b - a == rows_cap or nxt > thr or blk.sum() + nxt > nnz_cap
+            next_row = b
+            i += 1
+        else:  # chunks of a long row
+            row, nch = a, c
+            assert row == next_row and lengths[row] > thr
+            assert nch == -(-lengths[row] // chunk)
+            for k in range(nch):
+                assert tuple(int(v) for v in desc[i + k][:3]) == (row, k, nch)
+                assert int(desc[i + k][3]) == (part_cursor if nch > 1 else -1)
+            if nch > 1:
+                part_cursor += nch
+                split_rows += 1
+            next_row = row + 1
+            i += nch
+    assert next_row == n
+    assert n_parts == part_cursor and n_split == split_rows
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_planner_invariants_random(seed):
+    rng = np.random.default_rng(seed)
+    lengths = rng.zipf(1.7, 3000).clip(max=20000) - 1 + (rng.random(3000) < 0.2)
+    lengths[rng.integers(0, 3000, 50)] = 0
+    for nnz_cap, rows_cap, thr, chunk in ((2045, 1024, 2045, 4093), (2045, 16, 128, 512),
+                                         (100, 7, 50, 33), (1, 1, 1, 1)):
+        _check_plan(lengths.astype(np.int64), nnz_cap, rows_cap, thr, chunk)
+
+
+def test_planner_edges():
+    _check_plan(np.zeros(0, dtype=np.int64), 10, 4, 5, 5)
+    _check_plan(np.zeros(5000, dtype=np.int64), 2045, 1024, 2045, 4093)
+    _check_plan(np.array([2045, 2046, 4093, 4094, 1, 0]), 2045, 1024, 2045, 4093)
+
+
+def test_planner_rejects_bad_arguments():
+    rp = np.array([0, 3, 2], dtype=np.int64)
+    rc, msg, *_ = _plan(rp, 10, 4, 5, 5)
+    assert rc == -1 and "non-decreasing" in msg  # FSP_EINVAL
+    rc, msg, *_ = _plan(np.array([0, 1]), 10, 4, 11, 5)  # long_threshold > nnz_cap
+    assert rc == -1 and "long_threshold" in msg
+    rc, msg, *_ = _plan(np.array([0, 1]), 10, 0, 5, 5)
+    assert rc == -1
+
+
+def test_kernel_entry_points_reject_before_any_hip_call():
+    L = _abi.lib()
+    # unsupported dtype code
+    assert L.fsp_spmv_csr(7, 0, None, None, None, 32, 0, 0, None, None, None, 0, None, 0, 1,
+                          None, None, 0, None) == -3
+    assert b"dtype" in L.fsp_last_error()
+    # bad rowptr width
+    assert L.fsp_spmv_csr(0, 0, None, None, None, 16, 0, 0, None, None, None, 0, None, 0, 1,
+                          None, None, 0, None) == -1
+    # chunk beyond the compiled capacity
+    assert L.fsp_spmv_csr(0, 0, None, None, None, 32, 0, 0, None, None, None, 0, None, 0,
+                          10**9, None, None, 0, None) == -1
+    # SpMM: lanes_per_row not a power of two, vec not allowed
+    assert L.fsp_spmm_csr(0, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0, 1, 3,
+                          1, None, None, 0, None) == -1
+    assert L.fsp_spmm_csr(1, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0, 1, 4,
+                          4, None, None, 0, None) == -1
+    assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1

@@ -1,0 +1,366 @@
+"""Pins the CPU oracle (oracle/oracle.py, oracle/fsp_oracle.c) before it is trusted as the checker.
+
+The reference ships no golden vectors for this path (its tests draw unseeded inputs and compare
+against fp64 torch.sparse / cuSPARSE), so every oracle function is pinned here by something
+other than a retyped formula:
+
+  spmv_csr, spmv_coo, spmm_csr     scipy.sparse (an independent CSR/COO implementation), exact
+                                   integer arithmetic, Poisson closed forms, unit vectors
+  spmv_csr(row_cap=...)            a loop-by-loop emulation of the reference's tile loops
+                                   (spmv_csr.py:106-118, 176-190, 240-250) on a dense copy
+  spmv_prepare_knobs               brute-force search over block_nnz doublings + known answers
+  spmv_opt_buckets / spmm_opt_*    per-row linear scans over the threshold tables
+  spmm_alg1_config                 known answers of the reference's ALG1 coverage table
+                                   (tests/test_spmm.py:47-54) and its overflow case (:721-724)
+  coo_sort_lex / coo_seg_starts    Python's stable sorted() and itertools.groupby
+  coo_to_csr                       scipy's COO -> CSR structure (indptr) and a stable sort
+  rel_l2 / allclose_ratio          hand-computed cases
+Each check is chosen so that a plausible slip (an off-by-one loop bound, a row/column swap, a
+dropped duplicate, a wrong threshold comparison) fails it.
+"""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+from oracle import oracle
+
+
+def _random_csr(rng, n_rows, n_cols, nnz, dtype=np.float64, sorted_cols=False):
+    """CSR with empty rows, unsorted and repeated columns (the reference generator's shape,
+    sparse_operations/_common.py:166-181)."""
+    rows = np.sort(rng.integers(0, n_rows, nnz))
+    indptr = np.zeros(n_rows + 1, dtype=np.int64)
+    indptr[1:] = np.cumsum(np.bincount(rows, minlength=n_rows))
+    cols = rng.integers(0, n_cols, nnz).astype(np.int64)
+    if sorted_cols:
+        for r in range(n_rows):
+            cols[indptr[r]:indptr[r + 1]].sort()
+    vals = rng.standard_normal(nnz).astype(dtype)
+    return indptr, cols, vals
+
+
+def _scipy_csr(indptr, cols, vals, shape):
+    # scipy keeps duplicates of a non-canonical CSR and sums them in the product
+    return sp.csr_matrix((vals.astype(np.float64), cols, indptr), shape=shape)
+
+
+# ------------------------------------------------------------------------------------------
+# fp64 arithmetic
+# ------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_spmv_csr_matches_scipy(seed):
+    rng = np.random.default_rng(seed)
+    n_rows, n_cols = 700, 530
+    indptr, cols, vals = _random_csr(rng, n_rows, n_cols, 1500)
+    assert np.any(np.diff(indptr) == 0)  # empty rows present
+    x = rng.standard_normal(n_cols)
+    ref = _scipy_csr(indptr, cols, vals, (n_rows, n_cols)) @ x
+    y = oracle.spmv_csr(indptr, cols, vals, x)
+    np.testing.assert_allclose(y, ref, rtol=1e-13, atol=1e-13)
+
+
+def test_spmv_csr_exact_on_integers():
+    """Small integers: every product and partial sum is exact in fp64, so the oracle must equal
+    the exact integer matrix-vector product."""
+    rng = np.random.default_rng(7)
+    n_rows, n_cols = 200, 150
+    indptr, cols, _ = _random_csr(rng, n_rows, n_cols, 3000)
+    vals = rng.integers(-50, 51, cols.size)
+    x = rng.integers(-50, 51, n_cols)
+    exact = [sum(int(vals[i]) * int(x[cols[i]]) for i in range(indptr[r], indptr[r + 1]))
+             for r in range(n_rows)]
+    y = oracle.spmv_csr(indptr, cols, vals.astype(np.float64), x.astype(np.float64))
+    assert y.tolist() == [float(v) for v in exact]
+
+
+def _poisson(grid):
+    n = grid * grid
+    indptr = [0]
+    cols, vals = [], []
+    for i in range(n):
+        r, c = divmod(i, grid)
+        for off, ok in ((-grid, r > 0), (-1, c > 0), (0, True), (1, c < grid - 1),
+                        (grid, r < grid - 1)):
+            if ok:
+                cols.append(i + off)
+                vals.append(4.0 if off == 0 else -1.0)
+        indptr.append(len(cols))
+    return np.array(indptr), np.array(cols), np.array(vals)
+
+
+def test_spmv_csr_poisson_closed_forms():
+    grid = 9
+    indptr, cols, vals = _poisson(grid)
+    n = grid * grid
+    # A @ 1 = 4 - (number of neighbours): 2 at corners, 1 on edges, 0 inside
+    y = oracle.spmv_csr(indptr, cols, vals, np.ones(n))
+    for i in range(n):
+        r, c = divmod(i, grid)
+        boundary = (r in (0, grid - 1)) + (c in (0, grid - 1))
+        assert y[i] == float(boundary)
+    # A @ e_j = column j of A (symmetric: equals row j)
+    for j in (0, 5, 40, n - 1):
+        e = np.zeros(n)
+        e[j] = 1.0
+        col = oracle.spmv_csr(indptr, cols, vals, e)
+        dense_row = np.zeros(n)
+        dense_row[cols[indptr[j]:indptr[j + 1]]] = vals[indptr[j]:indptr[j + 1]]
+        assert np.array_equal(col, dense_row)
+
+
+def _emulate_tile_loop(indptr, block, max_segs):
+    """Entries of each row visited by `for seg in range(MAX_SEGS): offs = start + seg*BLOCK +
+    arange(BLOCK); mask = offs < end` (spmv_csr.py:106-118): counted one offset at a time."""
+    visited = []
+    for r in range(indptr.size - 1):
+        start, end = int(indptr[r]), int(indptr[r + 1])
+        count = 0
+        for seg in range(max_segs):
+            for lane in range(block):
+                if start + seg * block + lane < end:
+                    count += 1
+        visited.append(count)
+    return np.array(visited)
+
+
+def test_spmv_csr_row_cap_matches_tile_loop_emulation():
+    rng = np.random.default_rng(3)
+    lengths = np.array([0, 1, 5, 31, 32, 33, 64, 65, 100, 129, 300])
+    indptr = np.concatenate([[0], np.cumsum(lengths)])
+    n_cols = 400
+    cols = rng.integers(0, n_cols, indptr[-1])
+    vals = rng.standard_normal(indptr[-1])
+    x = rng.standard_normal(n_cols)
+    for block, max_segs in ((32, 1), (32, 2), (16, 3), (64, 1)):
+        visited = _emulate_tile_loop(indptr, block, max_segs)
+        caps = oracle.spmv_row_caps(lengths, use_opt=False, fp64=False, block_nnz=block,
+                                    max_segments=max_segs, user_max_segments=max_segs)
+        assert caps.tolist() == visited.tolist()
+        # result = product with the truncated rows, built densely
+        dense = np.zeros((lengths.size, n_cols))
+        for r in range(lengths.size):
+            for i in range(indptr[r], indptr[r] + visited[r]):
+                dense[r, cols[i]] += vals[i]
+        y = oracle.spmv_csr(indptr, cols, vals, x, row_cap=caps)
+        np.testing.assert_allclose(y, dense @ x, rtol=1e-13, atol=1e-13)
+
+
+def test_spmv_coo_matches_scipy_with_duplicates():
+    rng = np.random.default_rng(11)
+    n_rows, n_cols, nnz = 300, 250, 5000
+    row = rng.integers(0, n_rows, nnz)
+    col = rng.integers(0, n_cols, nnz)
+    row[:50] = row[50:100]  # force repeated (row, col) pairs
+    col[:50] = col[50:100]
+    vals = rng.standard_normal(nnz)
+    x = rng.standard_normal(n_cols)
+    ref = sp.coo_matrix((vals, (row, col)), shape=(n_rows, n_cols)) @ x
+    y = oracle.spmv_coo(row, col, vals, x, n_rows)
+    np.testing.assert_allclose(y, ref, rtol=1e-13, atol=1e-13)
+    empty_rows = np.setdiff1d(np.arange(n_rows), row)
+    assert np.all(y[empty_rows] == 0.0)
+
+
+@pytest.mark.parametrize("N", [1, 3, 16, 33])
+def test_spmm_csr_matches_scipy(N):
+    rng = np.random.default_rng(N)
+    n_rows, n_cols = 180, 140
+    indptr, cols, vals = _random_csr(rng, n_rows, n_cols, 2500)
+    B = rng.standard_normal((n_cols, N))
+    ref = _scipy_csr(indptr, cols, vals, (n_rows, n_cols)) @ B
+    C = oracle.spmm_csr(indptr, cols, vals, B)
+    np.testing.assert_allclose(C, ref, rtol=1e-13, atol=1e-13)
+
+
+def test_spmm_csr_edge_shapes():
+    indptr = np.zeros(3, dtype=np.int64)
+    assert oracle.spmm_csr(indptr, np.zeros(0), np.zeros(0), np.ones((2, 4))).tolist() == \
+        [[0.0] * 4] * 2
+    C = oracle.spmm_csr(np.array([0, 2, 3]), np.array([0, 1, 1]), np.array([1.0, 2.0, 3.0]),
+                        np.empty((2, 0)))
+    assert C.shape == (2, 0)
+
+
+# ------------------------------------------------------------------------------------------
+# planning semantics
+# ------------------------------------------------------------------------------------------
+
+
+def _knobs_brute(max_row, block_nnz):
+    """Smallest doubling of block_nnz (stopping at 65536) whose tile count is <= 2048."""
+    b = block_nnz
+    while True:
+        segs = max(-(-max_row // b), 1)
+        if segs <= 2048 or b >= 65536:
+            return b, segs
+        b *= 2
+
+
+@pytest.mark.parametrize("max_row", [0, 1, 255, 256, 257, 524288, 524289, 600000, 200000,
+                                     10**8, 2**31 - 1])
+@pytest.mark.parametrize("block_nnz", [1, 32, 256, 1000])
+def test_spmv_prepare_knobs_brute_force(max_row, block_nnz):
+    assert oracle.spmv_prepare_knobs(max_row, block_nnz) == _knobs_brute(max_row, block_nnz)
+
+
+def test_spmv_prepare_knobs_known_answers():
+    assert oracle.spmv_prepare_knobs(200000) == (256, 782)       # no doubling needed
+    assert oracle.spmv_prepare_knobs(600000) == (512, 1172)      # one doubling
+    assert oracle.spmv_prepare_knobs(10**9) == (65536, 15259)    # capped at 65536
+    assert oracle.spmv_prepare_knobs(0) == (256, 1)
+    assert oracle.spmv_prepare_knobs(999, 256, max_segments=2) == (256, 2)  # user value kept
+
+
+def _bucket_of(length, uppers):
+    for k, u in enumerate(uppers):
+        if u is None or length <= u:
+            return k
+    raise AssertionError
+
+
+@pytest.mark.parametrize("fp64", [False, True])
+def test_spmv_opt_buckets_brute_force(fp64):
+    lengths = np.array([0, 1, 64, 65, 256, 257, 512, 513, 2048, 2049, 4096, 4097, 8192, 8193,
+                        30000, 3, 0, 700])
+    specs = oracle.SPMV_OPT_BUCKETS_FP64 if fp64 else oracle.SPMV_OPT_BUCKETS_FP32
+    uppers = [s[0] for s in specs]
+    want = {}
+    for r, length in enumerate(lengths):
+        want.setdefault(_bucket_of(length, uppers), []).append(r)
+    got = oracle.spmv_opt_buckets(lengths, int(lengths.max()), fp64)
+    assert [b["rows"].tolist() for b in got] == [want[k] for k in sorted(want)]
+    for b, k in zip(got, sorted(want)):
+        upper, bs, batch = specs[k]
+        assert (b["block_size"], b["batch_rows"]) == (bs, batch)
+        bucket_max = int(lengths.max()) if upper is None else upper
+        assert b["max_segs"] * bs >= bucket_max > (b["max_segs"] - 1) * bs
+    # every row exactly once
+    assert sorted(itertools.chain(*[b["rows"].tolist() for b in got])) == list(range(lengths.size))
+
+
+def test_spmv_row_caps_opt_path_emulation():
+    lengths = np.array([0, 5, 64, 65, 200, 300, 513, 700, 1100, 4097, 9000])
+    indptr = np.concatenate([[0], np.cumsum(lengths)])
+    for fp64 in (False, True):
+        for user_segs in (1, 2, 3):
+            caps = oracle.spmv_row_caps(lengths, True, fp64, 256, user_segs, user_segs)
+            for b in oracle.spmv_opt_buckets(lengths, int(lengths.max()), fp64, user_segs):
+                sub = np.concatenate([[0], np.cumsum(lengths[b["rows"]])])
+                vis = _emulate_tile_loop(sub, b["block_size"], b["max_segs"])
+                assert caps[b["rows"]].tolist() == vis.tolist()
+        # without a caller max_segments the opt path covers every row
+        assert oracle.spmv_row_caps(lengths, True, fp64, 256, 36, None).tolist() == \
+            lengths.tolist()
+    del indptr
+
+
+@pytest.mark.parametrize("N,block_n,block_nnz", [(4, 4, 4), (5, 8, 8), (12, 16, 16),
+                                                  (24, 32, 32), (48, 64, 32), (96, 128, 32),
+                                                  (1, 4, 4), (8, 8, 8), (16, 16, 16),
+                                                  (32, 32, 32), (64, 64, 32), (256, 128, 32)])
+def test_spmm_alg1_known_answers(N, block_n, block_nnz):
+    cfg = oracle.spmm_alg1_config(N, 100)
+    assert (cfg["block_n"], cfg["block_nnz"]) == (block_n, block_nnz)
+    assert cfg["required_segments"] == -(-100 // block_nnz)
+
+
+def test_spmm_alg1_errors():
+    # tests/test_spmm.py:721-724: a 1536-nnz row, block_nnz=128, max_segments=4 -> 12 > 4
+    with pytest.raises(ValueError):
+        oracle.spmm_alg1_config(4, 1536, block_nnz=128, max_segments=4)
+    assert oracle.spmm_alg1_config(4, 1536, block_nnz=128, max_segments=12)["max_segments"] == 12
+    for kw in ({"block_n": 0}, {"block_nnz": 0}, {"max_segments": 0}):
+        with pytest.raises(ValueError):
+            oracle.spmm_alg1_config(4, 10, **kw)
+    assert oracle.spmm_alg1_config(4, 0)["required_segments"] == 0
+
+
+@pytest.mark.parametrize("N,want", [(1, 8), (8, 8), (9, 16), (16, 16), (17, 32), (32, 32),
+                                    (33, 64), (64, 64), (65, 128), (256, 128)])
+def test_spmm_opt_block_n(N, want):
+    assert oracle.spmm_opt_block_n(N) == want
+
+
+def test_spmm_opt_buckets_and_split_parts():
+    lengths = np.array([0, 32, 33, 128, 129, 512, 513, 2048, 2049, 3000, 1, 5000])
+    uppers = [s[0] for s in oracle.SPMM_OPT_BUCKETS]
+    buckets, long_rows = oracle.spmm_opt_buckets(lengths)
+    want = {}
+    for r, length in enumerate(lengths):
+        want.setdefault(_bucket_of(length, uppers), []).append(r)
+    assert [b["rows"].tolist() for b in buckets] == [want[k] for k in sorted(want)]
+    assert long_rows.tolist() == [8, 9, 11]
+    indptr = np.concatenate([[0], np.cumsum(lengths)])
+    rows, starts, ends, ptr = oracle.spmm_opt_split_metadata(indptr, long_rows)
+    for j, r in enumerate(long_rows):
+        seg = slice(ptr[j], ptr[j + 1])
+        assert np.all(rows[seg] == r)
+        assert starts[seg][0] == indptr[r] and ends[seg][-1] == indptr[r + 1]
+        assert np.all(starts[seg][1:] == ends[seg][:-1])          # contiguous cover
+        assert np.all(ends[seg] - starts[seg] <= 256)
+        assert ptr[j + 1] - ptr[j] == -(-lengths[r] // 256)
+    assert ends[ptr[1] - 1] - starts[ptr[1] - 1] == 2049 - 8 * 256  # a 1-entry last part
+
+
+# ------------------------------------------------------------------------------------------
+# COO semantics
+# ------------------------------------------------------------------------------------------
+
+
+def test_coo_sort_and_runs_brute_force():
+    rng = np.random.default_rng(5)
+    n_rows, n_cols, nnz = 40, 30, 600
+    row = rng.integers(0, n_rows, nnz)
+    col = rng.integers(0, n_cols, nnz)
+    data = np.arange(nnz, dtype=np.float64)  # identifies each entry
+    d, r, c = oracle.coo_sort_lex(data, row, col, n_cols)
+    want = sorted(zip(row.tolist(), col.tolist(), data.tolist()), key=lambda t: (t[0], t[1]))
+    assert list(zip(r.tolist(), c.tolist(), d.tolist())) == want
+    starts = oracle.coo_seg_starts(r)
+    runs = [len(list(g)) for _, g in itertools.groupby(r.tolist())]
+    assert starts.tolist() == [0] + np.cumsum(runs).tolist()
+    assert oracle.coo_seg_starts(np.zeros(0)) is None
+
+
+def test_coo_to_csr_structure():
+    rng = np.random.default_rng(9)
+    n_rows, n_cols, nnz = 50, 45, 700
+    row = rng.integers(0, n_rows, nnz)
+    col = rng.integers(0, n_cols, nnz)
+    data = rng.standard_normal(nnz)
+    d, c, indptr = oracle.coo_to_csr(data, row, col, n_rows, n_cols)
+    ref = sp.coo_matrix((data, (row, col)), shape=(n_rows, n_cols)).tocsr()
+    # scipy's tocsr sums duplicates; its row counts of distinct pairs differ, so compare the
+    # structure against the raw per-row counts and the values against the summed matrix
+    counts = np.bincount(row, minlength=n_rows)
+    assert indptr.tolist() == [0] + np.cumsum(counts).tolist()
+    dense = np.zeros((n_rows, n_cols))
+    for rr in range(n_rows):
+        for i in range(indptr[rr], indptr[rr + 1]):
+            dense[rr, c[i]] += d[i]
+    np.testing.assert_allclose(dense, ref.toarray(), rtol=1e-13, atol=1e-13)
+    # already-sorted input keeps its order
+    order = np.lexsort((col, row))
+    d2, c2, _ = oracle.coo_to_csr(data[order], row[order], col[order], n_rows, n_cols)
+    assert np.array_equal(d2, data[order]) and np.array_equal(c2, col[order])
+
+
+# ------------------------------------------------------------------------------------------
+# metrics
+# ------------------------------------------------------------------------------------------
+
+
+def test_metrics_hand_computed():
+    assert oracle.rel_l2([3.0, 4.0], [3.0, 4.0]) == 0.0
+    assert math.isclose(oracle.rel_l2([3.0, 5.0], [3.0, 4.0]), 1.0 / 5.0)
+    assert oracle.rel_l2([0.0], [0.0]) == 0.0
+    assert oracle.rel_l2([1e-30], [0.0]) == math.inf
+    assert math.isclose(oracle.allclose_ratio([1.1], [1.0], 0.0, 0.1), 1.0)
+    assert math.isclose(oracle.allclose_ratio([0.0, 2.0], [0.0, 1.0], 1.0, 0.0), 1.0)
+    assert oracle.allclose_ratio([], [], 1.0, 1.0) == 0.0

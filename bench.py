@@ -1,19 +1,27 @@
 """Benchmark of the flagsparse_amd hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2] [--no-targets]
 
-Prints ONE JSON line.  A step is one call of the public API over the workload's matrix
-(inputs already resident in HBM, the prepare step outside the timed region, as the
-reference's harness does: sparse_operations/benchmarks.py:249-262).  The default workload is
-BASELINE.json configs[1] (CSR SpMV, float64, 2D 5-point Poisson on a 2048 x 2048 grid); the
-others are selectable with --workload for measurement runs.
+Prints ONE JSON line.  A step is one call of the public API over the workload's matrix with
+the inputs already resident in HBM and the prepare step outside the timed region, as the
+reference's harness does (sparse_operations/benchmarks.py:249-262).  The default workload is
+BASELINE.json configs[1] (CSR SpMV, float64, 5-point Poisson on a 2048 x 2048 grid, the
+reference's default use_opt=False path); --workload selects the others.
 
-value        = algorithmic bytes per step / measured time per step (whole-job GB/s)
-roofline     = the same bytes over the kernel's average duration from HIP events on the launch
-               stream, against the 8 TB/s HBM3E peak; ``traffic`` is read from the committed
-               rocprofv3 PMC summary of the workload when one exists
-cpu_baseline = the C oracle (fp64 restatement, one core) on the same arrays, timed for about
-               10 s of full passes (rank 0, N=1 only)
+value        algorithmic bytes per step / time per step (HIP events around the K steps)
+roofline     the same bytes / the dominant kernel's average duration, timed with HIP events
+             around K back-to-back launches on the stream the kernel runs on, against the
+             8 TB/s HBM3E peak.  ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the
+             committed rocprofv3 PMC summary (profiles/<kernel tag>_traffic.txt), or null.
+cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
+             (a bounded row sample for SpMM), reported only, never a target
+targets      north_star's two targets measured in the same run (kernel time only): CSR SpMV
+             fp32 on the 8M power-law matrix (>= 70% of HBM peak) and CSR SpMM fp32 N=64
+             (>= 60%); omitted with --no-targets
+
+Algorithmic bytes count each array once at the width the kernel reads:
+  SpMV  nnz*(v + i) + (n_rows + 1)*p + n_cols*v + n_rows*v
+  SpMM  nnz*(v + i) + (n_rows + 1)*p + n_cols*N*v + n_rows*N*v
 """
 
 import argparse
@@ -55,8 +63,10 @@ def _parse():
     ap.add_argument("--opt", action="store_true",
                     help="SpMV: use_opt=True (native accumulation) instead of the default path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="CPU baseline: seconds of oracle passes (0 disables)")
+                    help="CPU baseline: seconds of oracle passes")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-targets", action="store_true",
+                    help="skip the north_star target measurements")
     return ap.parse_args()
 
 
@@ -70,162 +80,226 @@ def _traffic_from_profile(tag):
     return float(m.group(1)) if m else None
 
 
-def _time_steps(step, steps, warmup, torch):
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+def _event_loop(fn, count, torch):
+    """Average milliseconds of ``fn`` over ``count`` back-to-back calls, measured with HIP
+    events on torch's current stream (the stream every flagsparse_amd launch uses)."""
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
+    torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(steps):
-        step()
+    for _ in range(count):
+        fn()
     end.record(stream)
     torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(end)
-    return gpu_ms / steps, wall_s * 1000.0 / steps
+    return start.elapsed_time(end) / count
+
+
+def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
+    if name == "cfg1":
+        data, idx, ptr, x, shape = synthetic.csr_uniform_rows(device=dev)
+    elif name == "cfg2":
+        data, idx, ptr, x, shape = synthetic.csr_poisson2d(2048, device=dev)
+    else:
+        data, idx, ptr, x, shape = synthetic.csr_powerlaw(device=dev)
+    from flagsparse_amd import spmv_csr as mod
+
+    prepared = fs.prepare_spmv_csr(data, idx, ptr, shape)
+    use_opt = bool(opt and prepared.supports_opt)
+    y = torch.empty(shape[0], dtype=data.dtype, device=dev)
+    kc = prepared._kernel(use_opt)
+    v = data.element_size()
+    p_k = prepared.kernel_indptr.element_size()
+    nnz = int(data.numel())
+    nbytes = nnz * (v + 4) + (shape[0] + 1) * p_k + shape[1] * v + shape[0] * v
+    info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz,
+            "index_supplied": str(idx.dtype).replace("torch.", ""), "index_kernel": "int32",
+            "rowptr_kernel": f"int{8 * p_k}",
+            "path": "use_opt=True" if use_opt else "default (use_opt=False)",
+            "bytes_as_supplied": nnz * (v + idx.element_size()) +
+            (shape[0] + 1) * ptr.element_size() + shape[1] * v + shape[0] * v,
+            "plan": kc.describe()}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        passes, secs = oracle.time_spmv_csr(ptr, idx, data, x, min_seconds=seconds)
+        return {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{passes} full passes of the fp64 C oracle (oracle/fsp_oracle.c) over "
+                          f"the same matrix in {secs:.1f} s",
+                "gflops": round(2 * nnz * passes / secs / 1e9, 3)}
+
+    return {
+        "step": lambda: fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y),
+        "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
+        "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
+        "dtype": "f64" if data.dtype == torch.float64 else "f32",
+        "kernel": kc.kernel_name(), "tag": f"{kc.kernel_name()}_{name}",
+    }
+
+
+def _spmv_coo_workload(dev, torch, fs, synthetic):
+    from flagsparse_amd import spmv_coo as mod
+
+    data, row, col, x, shape = synthetic.coo_uniform(device=dev)
+    prepared = fs.prepare_spmv_coo(data, row, col, shape)
+    y = torch.empty(shape[0], dtype=data.dtype, device=dev)
+    v = data.element_size()
+    nnz = int(data.numel())
+    runs = prepared.n_segs
+    nbytes = nnz * (v + 4) + (runs + 1) * 4 + shape[1] * v + shape[0] * v
+    if prepared._run_rows is not None:
+        nbytes += runs * 4 + shape[0] * v
+    info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "row_runs": runs,
+            "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * v + shape[0] * v,
+            "plan": prepared._kernel_plan_description()}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        passes, secs = oracle.time_spmv_coo(row, col, data, x, shape[0], min_seconds=seconds)
+        return {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{passes} full passes of the fp64 C oracle COO SpMV in {secs:.1f} s",
+                "gflops": round(2 * nnz * passes / secs / 1e9, 3)}
+
+    return {
+        "step": lambda: fs.flagsparse_spmv_coo(x=x, prepared=prepared, out=y),
+        "launch": lambda: mod._run_spmv_coo(prepared, x, y, 256),
+        "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu, "dtype": "f32",
+        "kernel": prepared._kernel_name(), "tag": f"{prepared._kernel_name()}_cfg4",
+    }
+
+
+def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
+    from flagsparse_amd import spmm_csr as mod
+
+    vdt = torch.float64 if dtype_name == "f64" else torch.float32
+    data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
+    B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
+    prepared = fs.prepare_spmm_csr_opt(data, idx, ptr, shape)
+    C = torch.empty((shape[0], N), dtype=vdt, device=dev)
+    kc = prepared._kernel_csr()
+    v = data.element_size()
+    nnz = int(data.numel())
+    p_k = 4 if kc.rowptr_bits == 32 else 8
+    nbytes = nnz * (v + 4) + (shape[0] + 1) * p_k + shape[1] * N * v + shape[0] * N * v
+    info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
+            "path": "flagsparse_spmm_csr_opt (native accumulation)",
+            "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * p_k +
+            shape[0] * N * v}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        rows = max(1, min(shape[0], int(20e6 // max(1, 32 * N))))
+        passes, secs, r, nz = oracle.time_spmm_csr(ptr, idx, data, B, min_seconds=seconds,
+                                                   row_limit=rows)
+        frac = r / shape[0]
+        return {"value": round(nbytes * frac * passes / secs / 1e9, 3), "unit": "GB/s",
+                "cores": 1, "kind": "port",
+                "sample": f"{passes} passes of the fp64 C oracle SpMM over the first {r} rows "
+                          f"({nz} nnz) in {secs:.1f} s; bytes scaled by the row fraction",
+                "gflops": round(2 * nz * N * passes / secs / 1e9, 3)}
+
+    return {
+        "step": lambda: fs.flagsparse_spmm_csr_opt(B=B, prepared=prepared, out=C),
+        "launch": lambda: mod._run_spmm(kc, B, C, acc_f64=vdt == torch.float64),
+        "nbytes": nbytes, "flops": 2 * nnz * N, "info": info, "cpu": cpu,
+        "dtype": dtype_name, "kernel": kc.kernel_name(),
+        "tag": f"{kc.kernel_name()}_cfg5_{dtype_name}_n{N}",
+    }
+
+
+def _copy_workload(dev, torch):
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+
+    def step():
+        dst.copy_(src)
+
+    return {"step": step, "launch": step, "nbytes": 2 * n * 4, "flops": 0,
+            "info": {"bytes_read": n * 4, "bytes_written": n * 4}, "cpu": None, "dtype": "f32",
+            "kernel": "copy", "tag": "copy_1gib"}
+
+
+def _build(name, args, dev, torch):
+    import flagsparse_amd as fs
+    from flagsparse_amd import synthetic
+
+    if name in ("cfg1", "cfg2", "cfg3"):
+        return _spmv_csr_workload(name, dev, args.opt, torch, fs, synthetic)
+    if name == "cfg4":
+        return _spmv_coo_workload(dev, torch, fs, synthetic)
+    if name == "cfg5":
+        return _spmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
+    return _copy_workload(dev, torch)
+
+
+def _measure(w, steps, warmup, torch):
+    for _ in range(warmup):
+        w["step"]()
+    t0 = time.perf_counter()
+    ms_step = _event_loop(w["step"], steps, torch)
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
+    for _ in range(max(1, warmup // 2)):
+        w["launch"]()
+    ms_kernel = _event_loop(w["launch"], steps, torch)
+    return ms_step, wall_ms, ms_kernel
+
+
+def _target(name, args, dev, torch, steps):
+    class A:
+        pass
+
+    a = A()
+    a.opt, a.dtype, a.n = False, "f32", 64
+    w = _build(name, a, dev, torch)
+    _, _, ms_kernel = _measure(w, steps, 5, torch)
+    achieved = w["nbytes"] / (ms_kernel * 1e-3) / 1e9
+    out = {"workload": name if name != "cfg5" else "cfg5 (f32, N=64)", "kernel": w["kernel"],
+           "kernel_ms": round(ms_kernel, 6), "achieved_GBs": round(achieved, 2),
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": int(w["nbytes"]),
+           "gflops": round(w["flops"] / (ms_kernel * 1e-3) / 1e9, 2)}
+    del w
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
     args = _parse()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU row-slab design is described but not built)", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the "
+              "multi-GPU row-slab design is described in DESIGN.md but not built)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
 
-    import flagsparse_amd as fs
-    from flagsparse_amd import synthetic
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    w = args.workload
-    info = {"workload": f"{w}: {WORKLOADS[w]}"}
+    w = _build(args.workload, args, dev, torch)
+    ms_step, wall_ms, ms_kernel = _measure(w, args.steps, args.warmup, torch)
+    nbytes, flops = w["nbytes"], w["flops"]
+    value = nbytes / (ms_step * 1e-3) / 1e9
+    achieved = nbytes / (ms_kernel * 1e-3) / 1e9
     cpu = None
-
-    if w in ("cfg1", "cfg2", "cfg3"):
-        if w == "cfg1":
-            data, idx, ptr, x, shape = synthetic.csr_uniform_rows(device=dev)
-        elif w == "cfg2":
-            data, idx, ptr, x, shape = synthetic.csr_poisson2d(2048, device=dev)
-        else:
-            data, idx, ptr, x, shape = synthetic.csr_powerlaw(device=dev)
-        prepared = fs.prepare_spmv_csr(data, idx, ptr, shape)
-        use_opt = bool(args.opt)
-        y = torch.empty(shape[0], dtype=data.dtype, device=dev)
-
-        def step():
-            fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y)
-
-        v = data.element_size()
-        kc = prepared._kernel(use_opt and prepared.supports_opt)
-        p_k = 4 if kc.rowptr_bits == 32 else 8
-        nnz = int(data.numel())
-        nbytes = nnz * (v + 4) + (shape[0] + 1) * p_k + shape[1] * v + shape[0] * v
-        flops = 2 * nnz
-        info.update({"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz,
-                     "index_supplied": str(idx.dtype).replace("torch.", ""),
-                     "index_kernel": "int32", "rowptr_kernel": f"int{kc.rowptr_bits}",
-                     "path": "use_opt=True" if use_opt else "default (use_opt=False)",
-                     "bytes_as_supplied": nnz * (v + idx.element_size()) +
-                     (shape[0] + 1) * ptr.element_size() + shape[1] * v + shape[0] * v,
-                     "descriptors": kc.plan.n_desc, "split_rows": kc.plan.n_split_rows})
-        dtype_name = "f64" if data.dtype == torch.float64 else "f32"
-        kernel_tag = f"spmv_rowblock_{w}"
-        if not args.no_cpu and args.cpu_seconds > 0:
-            from oracle import oracle
-
-            passes, secs = oracle.time_spmv_csr(ptr, idx, data, x, min_seconds=args.cpu_seconds)
-            cpu = {"value": nbytes * passes / secs / 1e9, "unit": "GB/s", "cores": 1,
-                   "kind": "port",
-                   "sample": f"{passes} full passes of the fp64 C oracle (oracle/fsp_oracle.c) "
-                             f"over the same matrix in {secs:.1f} s",
-                   "gflops": flops * passes / secs / 1e9}
-    elif w == "cfg4":
-        data, row, col, x, shape = synthetic.coo_uniform(device=dev)
-        prepared = fs.prepare_spmv_coo(data, row, col, shape)
-        y = torch.empty(shape[0], dtype=data.dtype, device=dev)
-
-        def step():
-            fs.flagsparse_spmv_coo(x=x, prepared=prepared, out=y)
-
-        v = data.element_size()
-        nnz = int(data.numel())
-        runs = prepared.n_segs
-        nbytes = nnz * (v + 4) + (runs + 1) * 4 + shape[1] * v + shape[0] * v
-        if prepared._run_rows is not None:
-            nbytes += runs * 4 + shape[0] * v
-        flops = 2 * nnz
-        info.update({"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "row_runs": runs,
-                     "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * v + shape[0] * v})
-        dtype_name = "f64" if data.dtype == torch.float64 else "f32"
-        kernel_tag = "spmv_rowblock_cfg4"
-        if not args.no_cpu and args.cpu_seconds > 0:
-            from oracle import oracle
-
-            passes, secs = oracle.time_spmv_coo(row, col, data, x, shape[0],
-                                                min_seconds=args.cpu_seconds)
-            cpu = {"value": nbytes * passes / secs / 1e9, "unit": "GB/s", "cores": 1,
-                   "kind": "port",
-                   "sample": f"{passes} full passes of the fp64 C oracle COO SpMV in {secs:.1f} s",
-                   "gflops": flops * passes / secs / 1e9}
-    elif w == "cfg5":
-        vdt = torch.float64 if args.dtype == "f64" else torch.float32
-        N = int(args.n)
-        data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
-        B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
-        prepared = fs.prepare_spmm_csr_opt(data, idx, ptr, shape)
-        C = torch.empty((shape[0], N), dtype=vdt, device=dev)
-
-        def step():
-            fs.flagsparse_spmm_csr_opt(B=B, prepared=prepared, out=C)
-
-        v = data.element_size()
-        nnz = int(data.numel())
-        nbytes = nnz * (v + 4) + (shape[0] + 1) * 4 + shape[1] * N * v + shape[0] * N * v
-        flops = 2 * nnz * N
-        info.update({"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
-                     "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * 4 +
-                     shape[0] * N * v})
-        dtype_name = "f64" if vdt == torch.float64 else "f32"
-        kernel_tag = f"spmm_rowblock_cfg5_{dtype_name}_n{N}"
-        info["workload"] = f"cfg5 ({dtype_name}, N={N}): {WORKLOADS[w]}"
-        if not args.no_cpu and args.cpu_seconds > 0:
-            from oracle import oracle
-
-            rows = max(1, min(shape[0], int(20e6 // max(1, 32 * N))))
-            passes, secs, r, nz = oracle.time_spmm_csr(ptr, idx, data, B,
-                                                       min_seconds=args.cpu_seconds,
-                                                       row_limit=rows)
-            frac = r / shape[0]  # per-step bytes scaled by the sampled row fraction
-            cpu = {"value": nbytes * frac * passes / secs / 1e9, "unit": "GB/s", "cores": 1,
-                   "kind": "port",
-                   "sample": f"{passes} passes of the fp64 C oracle SpMM over the first {r} rows "
-                             f"({nz} nnz) in {secs:.1f} s; bytes scaled by the row fraction",
-                   "gflops": 2 * nz * N * passes / secs / 1e9}
-    else:  # copy calibration
-        n = (1 << 30) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-
-        def step():
-            dst.copy_(src)
-
-        nbytes = 2 * n * 4
-        flops = 0
-        dtype_name = "f32"
-        kernel_tag = "copy_1gib"
-        info.update({"bytes_read": n * 4, "bytes_written": n * 4})
-
-    ms_step, wall_ms = _time_steps(step, args.steps, args.warmup, torch)
-    achieved = nbytes / (ms_step * 1e-3) / 1e9
-    traffic = _traffic_from_profile(kernel_tag)
+    if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
+        cpu = w["cpu"](args.cpu_seconds)
+    workload = f"{args.workload}: {WORKLOADS[args.workload]}"
+    if args.workload == "cfg5":
+        workload = f"cfg5 ({w['dtype']}, N={args.n}): {WORKLOADS['cfg5']}"
+    info, dtype, kernel, tag = dict(w["info"]), w["dtype"], w["kernel"], w["tag"]
+    del w
+    torch.cuda.empty_cache()
+    targets = None
+    if not args.no_targets:
+        targets = [_target("cfg3", args, dev, torch, 20), _target("cfg5", args, dev, torch, 20)]
     out = {
         "metric": METRIC,
-        "value": round(achieved, 2),
+        "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -234,15 +308,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dtype_name,
+        "dtype": dtype,
         "data": "synthetic (seeded SplitMix64 generators, flagsparse_amd/synthetic.py)",
-        "config": dict(info, bytes_per_step=int(nbytes), flops_per_step=int(flops),
+        "config": dict({"workload": workload}, **info, bytes_per_step=int(nbytes),
+                       flops_per_step=int(flops),
                        gflops=round(flops / (ms_step * 1e-3) / 1e9, 2),
                        host_wall_ms_per_step=round(wall_ms, 6)),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": kernel_tag},
+                     "traffic": _traffic_from_profile(tag), "kernel": kernel,
+                     "kernel_ms": round(ms_kernel, 6), "profile_tag": tag},
         "cpu_baseline": cpu,
+        "targets": targets,
     }
     print(json.dumps(out), flush=True)
 

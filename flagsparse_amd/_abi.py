@@ -31,12 +31,16 @@ SIGNATURES = {
     "fsp_spmv_stream_rows_cap": (_i64, []),
     "fsp_spmv_chunk_nnz_cap": (_i64, []),
     "fsp_spmm_block_nnz_cap": (_i64, []),
+    "fsp_xcs_item_cap": (_i64, []),
+    "fsp_xcs_rows_cap": (_i64, []),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
-                            _i64, _p, _p, _i32, _p]),
+                            _i64, _p, _p, _p, _p, _i64, _i32, _p]),
+    "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _p, _i32, _p, _p, _p, _i64, _p, _i64, _p,
+                            _p, _p, _p, _p, _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
     "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
-                            _i64, _i64, _i32, _i32, _p, _p, _i32, _p]),
+                            _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),
 }
 
 
@@ -96,4 +100,6 @@ def caps():
         "spmv_stream_rows": int(L.fsp_spmv_stream_rows_cap()),
         "spmv_chunk_nnz": int(L.fsp_spmv_chunk_nnz_cap()),
         "spmm_block_nnz": int(L.fsp_spmm_block_nnz_cap()),
+        "xcs_item": int(L.fsp_xcs_item_cap()),
+        "xcs_rows": int(L.fsp_xcs_rows_cap()),
     }

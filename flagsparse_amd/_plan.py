@@ -18,13 +18,15 @@ from . import _abi
 
 
 class RowBlockPlan:
-    """A descriptor table on the device plus the zeroed workspace its split rows need."""
+    """A descriptor table on the device plus the partial-sum workspace its split rows need."""
 
-    __slots__ = ("desc", "n_desc", "n_parts", "n_split_rows", "chunk", "rows_cap", "nnz_cap",
-                 "long_threshold", "_workspaces")
+    __slots__ = ("desc", "desc_host", "n_desc", "n_parts", "n_split_rows", "chunk", "rows_cap",
+                 "nnz_cap", "long_threshold", "_workspaces", "_groups")
 
-    def __init__(self, desc, n_parts, n_split_rows, chunk, rows_cap, nnz_cap, long_threshold):
+    def __init__(self, desc, n_parts, n_split_rows, chunk, rows_cap, nnz_cap, long_threshold,
+                 desc_host=None):
         self.desc = desc
+        self.desc_host = desc_host
         self.n_desc = int(desc.shape[0])
         self.n_parts = int(n_parts)
         self.n_split_rows = int(n_split_rows)
@@ -33,23 +35,36 @@ class RowBlockPlan:
         self.nnz_cap = int(nnz_cap)
         self.long_threshold = int(long_threshold)
         self._workspaces = {}
+        self._groups = None
 
-    def workspace(self, width=1, tiles=1):
-        """(partials, tickets) for ``width`` values per part and ``tiles`` tickets per part.
-
-        Kept on the plan and reused by every call: the kernels leave the tickets at zero.
-        Calls that share a plan must therefore not run concurrently on different streams.
-        """
-        key = (int(width), int(tiles))
-        ws = self._workspaces.get(key)
+    def workspace(self, width=1):
+        """Partial-sum buffer for ``width`` values per row part, kept on the plan and reused by
+        every call.  Calls that share a plan must not run concurrently on different streams."""
+        ws = self._workspaces.get(int(width))
         if ws is None:
-            device = self.desc.device
             n = max(self.n_parts, 1)
-            partials = torch.empty(n * max(int(width), 1), dtype=torch.float64, device=device)
-            tickets = torch.zeros(n * max(int(tiles), 1), dtype=torch.int32, device=device)
-            ws = (partials, tickets)
-            self._workspaces[key] = ws
+            ws = torch.empty(n * max(int(width), 1), dtype=torch.float64, device=self.desc.device)
+            self._workspaces[int(width)] = ws
         return ws
+
+    def split_groups(self):
+        """(groups int32[g, 4], group_base int64[g], split_rows int32[g]) on the device for the
+        second-pass combine of rows cut into several chunks: group {g, 1, nch, 0} adds
+        partials[part .. part + nch) into that row."""
+        if self._groups is None:
+            d = self.desc_host
+            first = (d[:, 2] > 1) & (d[:, 1] == 0)
+            rows = np.ascontiguousarray(d[first, 0], dtype=np.int32)
+            base = np.ascontiguousarray(d[first, 3], dtype=np.int64)
+            g = rows.size
+            groups = np.zeros((g, 4), dtype=np.int32)
+            groups[:, 0] = np.arange(g, dtype=np.int32)
+            groups[:, 1] = 1
+            groups[:, 2] = d[first, 2]
+            device = self.desc.device
+            self._groups = (torch.from_numpy(groups).to(device), torch.from_numpy(base).to(device),
+                            torch.from_numpy(rows).to(device))
+        return self._groups
 
 
 def rowptr_to_host(rowptr):
@@ -75,7 +90,7 @@ def build_row_block_plan(rowptr_host, device, nnz_cap, rows_cap, long_threshold,
     if device is not None and torch.device(device).type != "cpu":
         desc_t = desc_t.to(device)
     return RowBlockPlan(desc_t, npart.value, nsplit.value, chunk, rows_cap, nnz_cap,
-                        long_threshold)
+                        long_threshold, desc_host=desc)
 
 
 def truncate_rows(data, indices, indptr, caps):

@@ -1,0 +1,325 @@
+"""Kernel-facing layouts of a CSR matrix for SpMV (CSR SpMV and COO row runs).
+
+Two layouts, chosen once per matrix at prepare time:
+
+``RowBlockLayout`` (csrc/spmv.hip, ``spmv_rowblock_kernel``)
+    The CSR arrays as given plus a descriptor table: short-row blocks of <= 2045 entries and
+    <= 1024 rows, and long rows cut into chunks of <= 4093 entries whose sums are added in
+    chunk order.  Right when the x entries a block gathers lie close together (banded,
+    stencil, locally clustered columns) or x fits in one XCD's L2.
+
+``XcsLayout`` (csrc/spmv_xcs.hip, ``spmv_xcs_kernel``)
+    Columns split into eight panels of about equal nnz, one per XCD; entries regrouped by
+    (row tile, panel) so that every workgroup gathers from one panel only, and that panel is
+    resident in its XCD's L2.  Right when columns are spread over an x larger than an L2
+    (uniform random columns, power-law graphs).  Rows whose entries fall in several workgroups
+    are summed through partials in a fixed order (deterministic).
+
+Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produce the same
+row sums up to floating-point summation order.
+"""
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _abi
+from ._common import _INDEX_LIMIT_INT32, _aligned
+from ._plan import build_row_block_plan, rowptr_to_host
+
+XCD_COUNT = 8
+L2_BYTES = 4 << 20
+# A column counts as "near" its row when within this many columns of the row's position on
+# the diagonal; the row-block layout is kept when most entries are near (x reuse in L2).
+NEAR_COLUMNS = 1 << 16
+SAMPLE = 1 << 20
+
+# Test hook: None (choose per matrix), "rowblock" or "xcs".
+FORCE = None
+
+
+def _host_rowptr(rowptr):
+    return rowptr_to_host(rowptr)
+
+
+class RowBlockLayout:
+    """CSR arrays (16-byte aligned) and the row-block descriptor plan."""
+
+    kind = "rowblock"
+
+    def __init__(self, data, cols, rowptr, rowptr_host=None):
+        self.data = _aligned(data)
+        self.cols = _aligned(cols)
+        nnz = int(data.numel())
+        if rowptr.dtype == torch.int32 or nnz <= _INDEX_LIMIT_INT32:
+            self.rowptr, self.rowptr_bits = rowptr.to(torch.int32).contiguous(), 32
+        else:
+            self.rowptr, self.rowptr_bits = rowptr.to(torch.int64).contiguous(), 64
+        self.nnz = nnz
+        self.n_rows = int(rowptr.numel()) - 1
+        caps = _abi.caps()
+        host = _host_rowptr(rowptr) if rowptr_host is None else rowptr_host
+        self.plan = build_row_block_plan(host, data.device, caps["spmv_stream_nnz"],
+                                         caps["spmv_stream_rows"], caps["spmv_stream_nnz"],
+                                         caps["spmv_chunk_nnz"])
+
+    def kernel_name(self):
+        return "spmv_rowblock_kernel"
+
+    def describe(self):
+        return {"layout": self.kind, "descriptors": self.plan.n_desc,
+                "split_rows": self.plan.n_split_rows, "partials": self.plan.n_parts}
+
+    def launch(self, x, y, acc_f64, row_map=None, n_out=0):
+        plan = self.plan
+        partials = plan.workspace()
+        groups, group_base, split_rows = plan.split_groups()
+        L = _abi.lib()
+        _abi.check(
+            L.fsp_spmv_csr(_abi.dtype_code(self.data.dtype), int(acc_f64), _abi.ptr(self.data),
+                           _abi.ptr(self.cols), _abi.ptr(self.rowptr), self.rowptr_bits,
+                           self.n_rows, self.nnz, _abi.ptr(x), _abi.ptr(y), _abi.ptr(row_map),
+                           n_out, _abi.ptr(plan.desc), plan.n_desc, plan.chunk,
+                           _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
+                           _abi.ptr(split_rows), int(groups.shape[0]), 1,
+                           _abi.stream_handle(y.device)),
+            "fsp_spmv_csr")
+        return y
+
+
+def _ceil_log2(v):
+    return max(1, int(v - 1).bit_length()) if v > 1 else 1
+
+
+class XcsLayout:
+    """The XCD column-split layout (see the module docstring).  Built on the device."""
+
+    kind = "xcs"
+
+    def __init__(self, data, cols, rowptr, n_cols, rowptr_host=None):
+        dev = data.device
+        caps = _abi.caps()
+        item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
+        nnz = int(data.numel())
+        n_rows = int(rowptr.numel()) - 1
+        self.n_rows, self.n_cols, self.nnz = n_rows, int(n_cols), nnz
+        host = _host_rowptr(rowptr) if rowptr_host is None else rowptr_host
+        lengths_h = np.diff(host)
+        cols = cols.to(torch.int32)
+
+        # 1. Eight column panels of about equal nnz, boundaries on 32-column (128 B) lines.
+        hist = torch.bincount(cols, minlength=self.n_cols) if nnz else \
+            torch.zeros(self.n_cols, dtype=torch.int64, device=dev)
+        cum = torch.cumsum(hist, 0)
+        targets = torch.tensor([(k * nnz + XCD_COUNT - 1) // XCD_COUNT
+                                for k in range(1, XCD_COUNT)], dtype=cum.dtype, device=dev)
+        inner = (torch.searchsorted(cum, targets) + 1).cpu().numpy()
+        cb = [0]
+        for b in inner.tolist():
+            b = min(self.n_cols, (int(b) + 31) // 32 * 32)
+            cb.append(max(cb[-1], b))
+        cb.append(self.n_cols)
+        widths = np.diff(np.array(cb))
+        self.panel_base_host = cb
+        self.col_bits = _ceil_log2(max(int(widths.max()), 2))
+        row_bits = 32 - self.col_bits
+        self.rows_cap = min(rows_cap, 1 << row_bits)
+        self.panel_base = torch.tensor(cb[:XCD_COUNT], dtype=torch.int32, device=dev)
+
+        # 2. Row tiles: greedy over rows (<= rows_cap rows, <= 8 * item_cap entries); a row
+        #    longer than that is a tile of its own.
+        tile_nnz = XCD_COUNT * item_cap
+        plan = build_row_block_plan(host, None, tile_nnz, self.rows_cap, tile_nnz,
+                                    max(1, int(lengths_h.max()) if n_rows else 1))
+        desc = plan.desc.numpy().astype(np.int64)
+        short = desc[:, 2] == 0
+        t_r0 = desc[:, 0]
+        t_R = np.where(short, desc[:, 1] - desc[:, 0], 1)
+        n_tiles = int(desc.shape[0])
+        self.n_tiles = n_tiles
+        t_r0_d = torch.from_numpy(t_r0).to(dev)
+        t_R_d = torch.from_numpy(t_R).to(dev)
+        tile_of_row = torch.repeat_interleave(torch.arange(n_tiles, device=dev), t_R_d)
+        lengths = torch.from_numpy(lengths_h).to(dev)
+
+        # 3. Entry -> (tile, panel); stable sort keeps row order (then original order).
+        entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths)
+        entry_tile = tile_of_row[entry_row]
+        bounds = torch.tensor(cb[1:XCD_COUNT], dtype=torch.int32, device=dev)
+        panel = torch.bucketize(cols, bounds, right=True)
+        key = entry_tile * XCD_COUNT + panel
+        key_sorted, perm = torch.sort(key, stable=True)
+        del key
+
+        # 4. Pieces (tile, panel) -> items of <= item_cap entries (equal split).
+        n_pieces = n_tiles * XCD_COUNT
+        cnt = torch.bincount(key_sorted, minlength=n_pieces) if nnz else \
+            torch.zeros(n_pieces, dtype=torch.int64, device=dev)
+        n_sub = (cnt + item_cap - 1) // item_cap
+        tile_tot = cnt.view(n_tiles, XCD_COUNT).sum(1)
+        empty_tiles = tile_tot == 0
+        n_sub.view(n_tiles, XCD_COUNT)[:, 0] += empty_tiles.to(n_sub.dtype)  # one dummy item
+        n_items = int(n_sub.sum().item())
+        piece_first_item = torch.cumsum(n_sub, 0) - n_sub
+        base = torch.where(n_sub > 0, cnt // n_sub.clamp(min=1), torch.zeros_like(cnt))
+        rem = torch.where(n_sub > 0, cnt % n_sub.clamp(min=1), torch.zeros_like(cnt))
+        item_piece = torch.repeat_interleave(torch.arange(n_pieces, device=dev), n_sub)
+        item_j = torch.arange(n_items, device=dev) - piece_first_item[item_piece]
+        item_len = base[item_piece] + (item_j < rem[item_piece]).to(base.dtype)
+        item_off = item_j * base[item_piece] + torch.minimum(item_j, rem[item_piece])
+        item_tile = item_piece // XCD_COUNT
+        item_panel = item_piece % XCD_COUNT
+        items_per_tile = torch.bincount(item_tile, minlength=n_tiles)
+        tile_first_item = torch.cumsum(items_per_tile, 0) - items_per_tile
+        item_k = torch.arange(n_items, device=dev) - tile_first_item[item_tile]
+        padded = (item_len + 3) // 4 * 4
+        item_start = torch.cumsum(padded, 0) - padded
+        n_entries = int(padded.sum().item()) if n_items else 0
+        if n_entries > _INDEX_LIMIT_INT32:
+            raise ValueError("matrix too large for the XCS layout")
+        self.n_entries = n_entries
+
+        # 5. Destination of every sorted entry; the new entry arrays.
+        piece_start = torch.cumsum(cnt, 0) - cnt
+        o = torch.arange(nnz, device=dev) - piece_start[key_sorted]
+        b = base[key_sorted]
+        rm = rem[key_sorted]
+        big = (b + 1) * rm
+        j = torch.where(o < big, o // (b + 1), rm + (o - big) // b.clamp(min=1))
+        item_of = piece_first_item[key_sorted] + j
+        dest = item_start[item_of] + (o - item_off[item_of])
+        del o, b, rm, big, j
+        vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
+        vals[dest] = data[perm]
+        loc_row = (entry_row[perm] - t_r0_d[key_sorted // XCD_COUNT]).to(torch.int64)
+        pan = key_sorted % XCD_COUNT
+        colp = cols[perm].to(torch.int64) - self.panel_base.to(torch.int64)[pan]
+        packed = (loc_row << self.col_bits) | colp
+        pidx = torch.zeros(max(n_entries, 4), dtype=torch.int64, device=dev)
+        pidx[dest] = packed
+        self.vals = vals
+        self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
+        del packed, colp, pan, loc_row, pidx, dest
+
+        # 6. Direct / split / empty rows and the per-tile masks.
+        row_min = torch.full((n_rows,), n_items, dtype=torch.int64, device=dev)
+        row_max = torch.full((n_rows,), -1, dtype=torch.int64, device=dev)
+        if nnz:
+            er = entry_row[perm]
+            row_min.scatter_reduce_(0, er, item_of, reduce="amin")
+            row_max.scatter_reduce_(0, er, item_of, reduce="amax")
+            del er
+        del entry_row, perm, key_sorted, item_of
+        empty = lengths == 0
+        split = (row_max > row_min) & ~empty
+        W = (t_R_d + 31) // 32
+        mask_off = torch.cumsum(2 * W, 0) - 2 * W
+        n_words = int((2 * W).sum().item())
+        rows = torch.arange(n_rows, device=dev)
+        lr = rows - t_r0_d[tile_of_row]
+        word = mask_off[tile_of_row] + lr // 32
+        bit = torch.ones_like(lr) << (lr % 32)
+        masks = torch.zeros(max(n_words, 1), dtype=torch.int64, device=dev)
+        masks.scatter_add_(0, word[split], bit[split])
+        masks.scatter_add_(0, (word + W[tile_of_row])[empty], bit[empty])
+        self.masks = torch.where(masks >= (1 << 31), masks - (1 << 32), masks).to(torch.int32)
+        S = torch.bincount(tile_of_row[split], minlength=n_tiles) if n_rows else \
+            torch.zeros(n_tiles, dtype=torch.int64, device=dev)
+        slots = S * items_per_tile
+        self.tile_part_base = (torch.cumsum(slots, 0) - slots).contiguous()
+        self.n_partials = int(slots.sum().item()) if n_tiles else 0
+        self.n_split_rows = int(split.sum().item()) if n_rows else 0
+        tiles = torch.stack([mask_off, S, items_per_tile, torch.zeros_like(S)], 1)
+        self.tiles = tiles.to(torch.int32).contiguous()
+        # second-pass groups: tiles with split rows; split rows in (tile, row) order
+        gt = torch.nonzero(S > 0).flatten()
+        self.split_rows = torch.nonzero(split).flatten().to(torch.int32)
+        first = torch.cumsum(S, 0) - S
+        self.groups = torch.stack([first[gt], S[gt], items_per_tile[gt], torch.zeros_like(gt)],
+                                  1).to(torch.int32).contiguous()
+        self.group_base = self.tile_part_base[gt].contiguous()
+        self.n_groups = int(gt.numel())
+
+        # 7. Launch order: XCD p runs the items of panel p, in tile order; lists padded to
+        #    the same length q so that slot p*q + j lands on XCD p.
+        per_panel = torch.bincount(item_panel, minlength=XCD_COUNT)
+        q = int(per_panel.max().item()) if n_items else 0
+        self.n_slots = XCD_COUNT * q
+        order = torch.argsort(item_panel, stable=True)
+        panel_first = torch.cumsum(per_panel, 0) - per_panel
+        rank = torch.arange(n_items, device=dev) - panel_first[item_panel[order]]
+        slot_of = item_panel[order] * q + rank
+        d = torch.zeros((max(self.n_slots, 1), 8), dtype=torch.int64, device=dev)
+        d[:, 2] = -1
+        it = order
+        d[slot_of] = torch.stack([item_start[it], item_len[it], item_tile[it], item_k[it],
+                                  t_r0_d[item_tile[it]], t_R_d[item_tile[it]], item_panel[it],
+                                  torch.zeros_like(it)], 1)
+        self.items = d.to(torch.int32).contiguous()
+        self.n_items = n_items
+        self.max_items_per_panel = q
+        self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+
+    def kernel_name(self):
+        return "spmv_xcs_kernel"
+
+    def describe(self):
+        return {"layout": self.kind, "tiles": self.n_tiles, "items": self.n_items,
+                "slots": self.n_slots, "split_rows": self.n_split_rows,
+                "partials": self.n_partials, "panel_base": self.panel_base_host,
+                "col_bits": self.col_bits, "padded_entries": self.n_entries}
+
+    def launch(self, x, y, acc_f64, row_map=None, n_out=0):
+        L = _abi.lib()
+        _abi.check(
+            L.fsp_spmv_xcs(_abi.dtype_code(self.vals.dtype), int(acc_f64), _abi.ptr(self.vals),
+                           _abi.ptr(self.pidx), self.n_entries, _abi.ptr(self.panel_base),
+                           self.col_bits, _abi.ptr(x), _abi.ptr(y), _abi.ptr(row_map), n_out,
+                           _abi.ptr(self.items), self.n_slots, _abi.ptr(self.tiles),
+                           _abi.ptr(self.tile_part_base), _abi.ptr(self.masks),
+                           _abi.ptr(self.partials), _abi.ptr(self.groups),
+                           _abi.ptr(self.group_base), _abi.ptr(self.split_rows), self.n_groups,
+                           _abi.stream_handle(y.device)),
+            "fsp_spmv_xcs")
+        return y
+
+
+def sample_indices(n, k, device):
+    """min(n, k) indices spread evenly over [0, n), computed in exact int64 arithmetic."""
+    if n <= k:
+        return torch.arange(n, device=device)
+    return torch.arange(k, device=device, dtype=torch.int64) * (n - 1) // (k - 1)
+
+
+def prefers_xcs(cols, rowptr, n_cols, value_bytes):
+    """True when most entries gather x far from their row's diagonal position and x does not
+    fit one XCD's L2 (the row-block layout would then miss L2 on almost every gather)."""
+    nnz = int(cols.numel())
+    n_rows = int(rowptr.numel()) - 1
+    if nnz == 0 or n_rows == 0 or int(n_cols) * value_bytes <= L2_BYTES:
+        return False
+    idx = sample_indices(nnz, SAMPLE, cols.device)
+    rp = rowptr.to(torch.int64)
+    rows = torch.searchsorted(rp, idx, right=True) - 1
+    diag = rows.to(torch.float64) * (float(n_cols) / float(n_rows))
+    far = (cols[idx].to(torch.float64) - diag).abs() > NEAR_COLUMNS
+    return bool(far.to(torch.float32).mean().item() > 0.5)
+
+
+def build_layout(data, cols, rowptr, n_cols):
+    """The layout for one CSR (or COO row-run) matrix: XCS when it pays, else row blocks."""
+    mode = FORCE
+    nnz = int(data.numel())
+    host = _host_rowptr(rowptr)
+    if mode is None:
+        mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
+    if mode == "xcs" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(n_cols) < (1 << 27) and \
+            int(rowptr.numel()) > 1:
+        return XcsLayout(data, cols, rowptr, n_cols, host)
+    return RowBlockLayout(data, cols, rowptr, host)
+
+
+__all__ = ["RowBlockLayout", "XcsLayout", "build_layout", "prefers_xcs", "sample_indices",
+           "FORCE"]
+del ctypes

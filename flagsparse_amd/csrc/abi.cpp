@@ -33,6 +33,8 @@ extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }
 extern "C" int64_t fsp_spmv_chunk_nnz_cap(void) { return kSpmvChunkCap; }
 extern "C" int64_t fsp_spmm_block_nnz_cap(void) { return kSpmmNnzCap; }
+extern "C" int64_t fsp_xcs_item_cap(void) { return kXcsItemCap; }
+extern "C" int64_t fsp_xcs_rows_cap(void) { return kXcsRowsCap; }
 
 extern "C" int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
                                    int64_t rows_cap, int64_t long_threshold, int64_t chunk,

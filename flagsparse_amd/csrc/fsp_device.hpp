@@ -128,15 +128,26 @@ __device__ __forceinline__ int xcd_logical_block(int i, int n) {
   return (x < r) ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
 }
 
-// Agent-scope accesses for the cross-workgroup partial sums: the XCD L2s are not coherent
-// with each other, so partials and tickets go through these.
-template <typename A>
-__device__ __forceinline__ void store_agent(A* p, A v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <typename A>
-__device__ __forceinline__ A load_agent(const A* p) {
-  return __hip_atomic_load(const_cast<A*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Second pass of every split-row SpMV: rows whose entries were summed by several workgroups
+// get y[row] = sum over j < n of partials[base + j*S + s], j in increasing order (a fixed
+// order, so the result does not depend on which workgroup finished first).  Group g covers S
+// rows split_rows[first .. first + S), its partials start at group_base[g] and are laid out
+// [n][S].  It runs as a separate launch on the same stream: the kernel boundary makes the
+// first pass's partials visible on every XCD, so neither pass needs a device-scope fence.
+template <typename T, typename A>
+__global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
+    const i32x4* __restrict__ groups, const int64_t* __restrict__ group_base,
+    const int* __restrict__ split_rows, const A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map) {
+  const i32x4 g = groups[blockIdx.x];
+  const int first = g.x, S = g.y, n = g.z;
+  const int64_t base = group_base[blockIdx.x];
+  for (int s = threadIdx.x; s < S; s += kBlock) {
+    A acc = A(0);
+    for (int j = 0; j < n; ++j) acc += partials[base + (int64_t)j * S + s];
+    const int row = split_rows[first + s];
+    y[row_map ? row_map[row] : row] = T(acc);
+  }
 }
 
 }  // namespace fsp

@@ -18,6 +18,19 @@ constexpr int64_t kSpmvChunkUnitsPerThread = 4;
 constexpr int64_t kSpmvChunkCap = kSpmvChunkUnitsPerThread * 4 * 256 - 3;
 constexpr int64_t kSpmmSlots = 2048;                     // LDS (col, val) slots per SpMM block
 constexpr int64_t kSpmmNnzCap = kSpmmSlots - 3;
+constexpr int64_t kXcsItemCap = 2048;                    // entries of one XCS item
+constexpr int64_t kXcsRowsCap = 4096;                    // rows of one XCS tile
+
+// Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).
+int fill_zero_f32(float* y, int64_t n, hipStream_t st);
+int fill_zero_f64(double* y, int64_t n, hipStream_t st);
+template <typename T> int fill_zero(T* y, int64_t n, hipStream_t st);
+template <> inline int fill_zero<float>(float* y, int64_t n, hipStream_t st) {
+  return fill_zero_f32(y, n, st);
+}
+template <> inline int fill_zero<double>(double* y, int64_t n, hipStream_t st) {
+  return fill_zero_f64(y, n, st);
+}
 
 int set_error(int code, const std::string& msg);
 int check_hip(hipError_t e, const char* what);

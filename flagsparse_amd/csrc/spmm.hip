@@ -14,8 +14,8 @@
 //     16-byte loads; group g computes row r0+g alone (no cross-lane reduction), 4 B rows in
 //     flight per lane.
 //   * row part {row, k, nch, part}: the 256/G groups stride over the part's entries, then a
-//     fixed-order LDS reduction over groups; with nch > 1 the last-arriving workgroup of the
-//     (row, tile) adds the parts in index order.
+//     fixed-order LDS reduction over groups; with nch > 1 the part's sums go to partials and
+//     a second launch (spmm_split_combine_kernel) adds a row's parts in index order.
 #include "fsp_device.hpp"
 #include "fsp_internal.hpp"
 
@@ -58,6 +58,13 @@ __device__ __forceinline__ void store_vec(T* p, const A (&acc)[VW]) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+struct SplitGroups {
+  const int32_t* groups;
+  const int64_t* base;
+  const int32_t* rows;
+  int64_t n;
+};
+
 template <typename T, typename A, int VW>
 constexpr int spmm_scratch_bytes() {
   return (kSlots * (int)sizeof(T) > kBlock * VW * (int)sizeof(A)) ? kSlots * (int)sizeof(T)
@@ -69,11 +76,10 @@ __global__ __launch_bounds__(kBlock) void spmm_rowblock_kernel(
     const T* __restrict__ vals, const int* __restrict__ cols, const P* __restrict__ rowptr,
     P nnz_total, const T* __restrict__ B, int64_t ldb, int N, T* __restrict__ C, int64_t ldc,
     const i32x4* __restrict__ desc, int n_desc, P chunk, int lg, A* __restrict__ partials,
-    unsigned* __restrict__ tickets, int n_tiles, int xcd_remap) {
+    int xcd_remap) {
   __shared__ int s_col[kSlots];
   __shared__ __attribute__((aligned(16))) unsigned char s_raw[spmm_scratch_bytes<T, A, VW>()];
   __shared__ P s_ptr[kBlock + 1];
-  __shared__ int s_last;
   T* s_val = reinterpret_cast<T*>(s_raw);
   A* s_red = reinterpret_cast<A*>(s_raw);  // reused after the entries are consumed
 
@@ -202,73 +208,77 @@ __global__ __launch_bounds__(kBlock) void spmm_rowblock_kernel(
   if (mine)
     for (int g = 0; g < ngrp; ++g) sum += s_red[g * W + tid];
 
-  if (nch == 1) {
-    if (mine) C[(int64_t)row * ldc + col] = T(sum);
-    return;
+  if (!mine) return;
+  if (nch == 1) C[(int64_t)row * ldc + col] = T(sum);
+  else partials[(int64_t)(part + k) * N + col] = sum;
+}
+
+// Second pass for rows cut into parts: C[row, :] = sum over k < nch of the part sums, k in
+// increasing order.  One workgroup per split row (group {g, 1, nch, 0}, first part
+// group_base[g]); a separate launch, so the first pass needs no device-scope fence.
+template <typename T, typename A>
+__global__ __launch_bounds__(kBlock) void spmm_split_combine_kernel(
+    const i32x4* __restrict__ groups, const int64_t* __restrict__ group_base,
+    const int* __restrict__ split_rows, const A* __restrict__ partials, int N,
+    T* __restrict__ C, int64_t ldc) {
+  const i32x4 g = groups[blockIdx.x];
+  const int nch = g.z;
+  const int64_t part = group_base[blockIdx.x];
+  const int row = split_rows[g.x];
+  for (int col = threadIdx.x; col < N; col += kBlock) {
+    A acc = A(0);
+    for (int k = 0; k < nch; ++k) acc += partials[(part + k) * N + col];
+    C[(int64_t)row * ldc + col] = T(acc);
   }
-  if (mine) store_agent(&partials[(int64_t)(part + k) * N + col], sum);
-  __threadfence();
-  __syncthreads();
-  unsigned* ticket = &tickets[(int64_t)part * n_tiles + tile];
-  if (tid == 0) {
-    __threadfence();
-    const unsigned t = atomicAdd(ticket, 1u);
-    __threadfence();
-    s_last = (t == unsigned(nch - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (mine) {
-    A f = A(0);
-    for (int q = 0; q < nch; ++q) f += load_agent(&partials[(int64_t)(part + q) * N + col]);
-    C[(int64_t)row * ldc + col] = T(f);
-  }
-  if (tid == 0) store_agent(ticket, 0u);
 }
 
 template <typename T, typename A, typename P, int VW>
 int launch_spmm(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
                 const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc, const int32_t* desc,
-                int64_t n_desc, int64_t chunk, int lg, void* partials, uint32_t* tickets,
+                int64_t n_desc, int64_t chunk, int lg, void* partials, const SplitGroups& sg,
                 int64_t n_tiles, int xcd_remap, hipStream_t st) {
   hipLaunchKernelGGL((spmm_rowblock_kernel<T, A, P, VW, true>),
                      dim3((unsigned)n_desc, (unsigned)n_tiles), dim3(kBlock), 0, st,
                      static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr), (P)nnz,
                      static_cast<const T*>(B), ldb, (int)N, static_cast<T*>(C), ldc,
                      reinterpret_cast<const i32x4*>(desc), (int)n_desc, (P)chunk, lg,
-                     static_cast<A*>(partials), tickets, (int)n_tiles, xcd_remap);
-  return check_hip(hipGetLastError(), "spmm_rowblock_kernel launch");
+                     static_cast<A*>(partials), xcd_remap);
+  int rc = check_hip(hipGetLastError(), "spmm_rowblock_kernel launch");
+  if (rc || sg.n == 0) return rc;
+  hipLaunchKernelGGL((spmm_split_combine_kernel<T, A>), dim3((unsigned)sg.n), dim3(kBlock), 0, st,
+                     reinterpret_cast<const i32x4*>(sg.groups), sg.base, sg.rows,
+                     static_cast<const A*>(partials), (int)N, static_cast<T*>(C), ldc);
+  return check_hip(hipGetLastError(), "spmm_split_combine_kernel launch");
 }
 
 template <typename T, typename A, typename P>
 int dispatch_vec(int vec, const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
                  const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc,
                  const int32_t* desc, int64_t n_desc, int64_t chunk, int lg, void* partials,
-                 uint32_t* tickets, int64_t n_tiles, int xcd_remap, hipStream_t st) {
+                 const SplitGroups& sg, int64_t n_tiles, int xcd_remap, hipStream_t st) {
   if constexpr (sizeof(T) == 4) {
     if (vec == 4)
       return launch_spmm<T, A, P, 4>(vals, cols, rowptr, nnz, B, ldb, N, C, ldc, desc, n_desc,
-                                     chunk, lg, partials, tickets, n_tiles, xcd_remap, st);
+                                     chunk, lg, partials, sg, n_tiles, xcd_remap, st);
   }
   if (vec == 2)
     return launch_spmm<T, A, P, 2>(vals, cols, rowptr, nnz, B, ldb, N, C, ldc, desc, n_desc,
-                                   chunk, lg, partials, tickets, n_tiles, xcd_remap, st);
+                                   chunk, lg, partials, sg, n_tiles, xcd_remap, st);
   return launch_spmm<T, A, P, 1>(vals, cols, rowptr, nnz, B, ldb, N, C, ldc, desc, n_desc, chunk,
-                                 lg, partials, tickets, n_tiles, xcd_remap, st);
+                                 lg, partials, sg, n_tiles, xcd_remap, st);
 }
 
 template <typename T, typename A>
 int dispatch_ptr(int rowptr_bits, int vec, const void* vals, const int32_t* cols,
                  const void* rowptr, int64_t nnz, const void* B, int64_t ldb, int64_t N, void* C,
                  int64_t ldc, const int32_t* desc, int64_t n_desc, int64_t chunk, int lg,
-                 void* partials, uint32_t* tickets, int64_t n_tiles, int xcd_remap,
+                 void* partials, const SplitGroups& sg, int64_t n_tiles, int xcd_remap,
                  hipStream_t st) {
   if (rowptr_bits == 32)
     return dispatch_vec<T, A, int>(vec, vals, cols, rowptr, nnz, B, ldb, N, C, ldc, desc, n_desc,
-                                   chunk, lg, partials, tickets, n_tiles, xcd_remap, st);
+                                   chunk, lg, partials, sg, n_tiles, xcd_remap, st);
   return dispatch_vec<T, A, int64_t>(vec, vals, cols, rowptr, nnz, B, ldb, N, C, ldc, desc,
-                                     n_desc, chunk, lg, partials, tickets, n_tiles, xcd_remap, st);
+                                     n_desc, chunk, lg, partials, sg, n_tiles, xcd_remap, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -282,13 +292,17 @@ extern "C" int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int3
                             const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                             const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc,
                             const int32_t* desc, int64_t n_desc, int64_t chunk, int lanes_per_row,
-                            int vec, void* partials, uint32_t* tickets, int xcd_remap,
-                            void* stream) {
+                            int vec, void* partials, const int32_t* groups,
+                            const int64_t* group_base, const int32_t* split_rows,
+                            int64_t n_groups, int xcd_remap, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmm_csr: dtype");
   if (rowptr_bits != 32 && rowptr_bits != 64)
     return set_error(FSP_EINVAL, "fsp_spmm_csr: rowptr_bits must be 32 or 64");
-  if (n_rows < 0 || nnz < 0 || N < 0 || n_desc < 0)
+  if (n_rows < 0 || nnz < 0 || N < 0 || n_desc < 0 || n_groups < 0)
     return set_error(FSP_EINVAL, "fsp_spmm_csr: negative size");
+  if (n_groups > 0x7fffffffLL) return set_error(FSP_EINVAL, "fsp_spmm_csr: too many groups");
+  if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmm_csr: null split-row pointer");
   if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL || N > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmm_csr: size exceeds 2^31-1");
   if (rowptr_bits == 32 && nnz > 0x7fffffffLL)
@@ -314,17 +328,19 @@ extern "C" int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int3
   const int64_t W = (int64_t)lanes_per_row * vec;
   const int64_t n_tiles = (N + W - 1) / W;
   if (n_tiles > 65535) return set_error(FSP_EINVAL, "fsp_spmm_csr: too many column tiles");
+  if (!aligned16(groups)) return set_error(FSP_EINVAL, "fsp_spmm_csr: groups must be 16-byte aligned");
+  const SplitGroups sg{groups, group_base, split_rows, n_groups};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FSP_F32) {
     if (acc_f64)
       return dispatch_ptr<float, double>(rowptr_bits, vec, vals, cols, rowptr, nnz, B, ldb, N, C,
-                                         ldc, desc, n_desc, chunk, lg, partials, tickets, n_tiles,
+                                         ldc, desc, n_desc, chunk, lg, partials, sg, n_tiles,
                                          xcd_remap, st);
     return dispatch_ptr<float, float>(rowptr_bits, vec, vals, cols, rowptr, nnz, B, ldb, N, C, ldc,
-                                      desc, n_desc, chunk, lg, partials, tickets, n_tiles,
+                                      desc, n_desc, chunk, lg, partials, sg, n_tiles,
                                       xcd_remap, st);
   }
   return dispatch_ptr<double, double>(rowptr_bits, vec, vals, cols, rowptr, nnz, B, ldb, N, C,
-                                      ldc, desc, n_desc, chunk, lg, partials, tickets, n_tiles,
+                                      ldc, desc, n_desc, chunk, lg, partials, sg, n_tiles,
                                       xcd_remap, st);
 }

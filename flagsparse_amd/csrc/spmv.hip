@@ -13,9 +13,9 @@
 //     then each row is summed by a group of G lanes (G = 256 / next_pow2(rows), <= 64) with a
 //     butterfly shuffle reduction.
 //   * long-row chunk   {row, k, nch, part}: 256 threads sum <= 4093 entries of one row in
-//     registers, reduce across the workgroup; with nch > 1 the chunk sum goes to partials[]
-//     and the last-arriving workgroup (ticket counter) adds partials[part .. part+nch) in
-//     index order, so the result does not depend on arrival order.
+//     registers, reduce across the workgroup; with nch > 1 the chunk sum goes to
+//     partials[part + k] and a second launch (split_row_combine_kernel) adds
+//     partials[part .. part+nch) in index order, so the result does not depend on timing.
 #include "fsp_device.hpp"
 #include "fsp_internal.hpp"
 
@@ -33,11 +33,10 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
     const T* __restrict__ vals, const int* __restrict__ cols, const P* __restrict__ rowptr,
     P nnz_total, const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
     const i32x4* __restrict__ desc, int n_desc, P chunk, A* __restrict__ partials,
-    unsigned* __restrict__ tickets, int xcd_remap) {
+    int xcd_remap) {
   __shared__ A s_prod[kStreamSlots];
   __shared__ P s_ptr[kStreamRows + 1];
   __shared__ A s_red[kWavesPerBlock];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   int b = blockIdx.x;
@@ -137,34 +136,10 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
     for (int j = 0; j < 4; ++j) acc += A(v[u][j]) * A(xv[u][j]);
 
   const A total = block_sum(acc, s_red);
-  const int out_row = row_map ? row_map[row] : row;
-  if (nch == 1) {
-    if (tid == 0) y[out_row] = T(total);
-    return;
-  }
   if (tid == 0) {
-    store_agent(&partials[part + k], total);
-    __threadfence();
-    const unsigned t = atomicAdd(&tickets[part], 1u);
-    __threadfence();
-    s_last = (t == unsigned(nch - 1));
+    if (nch == 1) y[row_map ? row_map[row] : row] = T(total);
+    else partials[part + k] = total;
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  A a = A(0);
-  for (int i = tid; i < nch; i += kBlock) a += load_agent(&partials[part + i]);
-  const A fin = block_sum(a, s_red);
-  if (tid == 0) {
-    y[out_row] = T(fin);
-    store_agent(&tickets[part], 0u);
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void fill_zero_kernel(T* __restrict__ y, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) y[i] = T(0);
 }
 
 template <typename T>
@@ -178,6 +153,53 @@ __global__ __launch_bounds__(kBlock) void spmv_coo_atomic_kernel(
     atomicAdd(&y[rows[i]], vals[i] * x[cols[i]]);
 }
 
+template <typename T, typename A, typename P>
+int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
+                const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
+                int64_t n_groups, int xcd_remap, hipStream_t st) {
+  if (row_map) {
+    int rc = fill_zero<T>(static_cast<T*>(y), n_out, st);
+    if (rc) return rc;
+  }
+  if (n_desc == 0) return FSP_OK;
+  hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, true>), dim3((unsigned)n_desc), dim3(kBlock),
+                     0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
+                     (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
+                     reinterpret_cast<const i32x4*>(desc), (int)n_desc, (P)chunk,
+                     static_cast<A*>(partials), xcd_remap);
+  int rc = check_hip(hipGetLastError(), "spmv_rowblock_kernel launch");
+  if (rc || n_groups == 0) return rc;
+  hipLaunchKernelGGL((split_row_combine_kernel<T, A>), dim3((unsigned)n_groups), dim3(kBlock), 0,
+                     st, reinterpret_cast<const i32x4*>(groups), group_base, split_rows,
+                     static_cast<const A*>(partials), static_cast<T*>(y), row_map);
+  return check_hip(hipGetLastError(), "split_row_combine_kernel launch");
+}
+
+template <typename T, typename A>
+int dispatch_ptr(int rowptr_bits, const void* vals, const int32_t* cols, const void* rowptr,
+                 int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
+                 const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
+                 int64_t n_groups, int xcd_remap, hipStream_t st) {
+  if (rowptr_bits == 32)
+    return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
+                                  chunk, partials, groups, group_base, split_rows, n_groups,
+                                  xcd_remap, st);
+  return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
+                                    chunk, partials, groups, group_base, split_rows, n_groups,
+                                    xcd_remap, st);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void fill_zero_kernel(T* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) y[i] = T(0);
+}
+
 template <typename T>
 int launch_fill(T* y, int64_t n, hipStream_t st) {
   if (n <= 0) return FSP_OK;
@@ -187,39 +209,11 @@ int launch_fill(T* y, int64_t n, hipStream_t st) {
   return check_hip(hipGetLastError(), "fill_zero_kernel launch");
 }
 
-template <typename T, typename A, typename P>
-int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
-                const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                uint32_t* tickets, int xcd_remap, hipStream_t st) {
-  if (row_map) {
-    int rc = launch_fill<T>(static_cast<T*>(y), n_out, st);
-    if (rc) return rc;
-  }
-  if (n_desc == 0) return FSP_OK;
-  hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, true>), dim3((unsigned)n_desc), dim3(kBlock),
-                     0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
-                     (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
-                     reinterpret_cast<const i32x4*>(desc), (int)n_desc, (P)chunk,
-                     static_cast<A*>(partials), tickets, xcd_remap);
-  return check_hip(hipGetLastError(), "spmv_rowblock_kernel launch");
-}
-
-template <typename T, typename A>
-int dispatch_ptr(int rowptr_bits, const void* vals, const int32_t* cols, const void* rowptr,
-                 int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                 uint32_t* tickets, int xcd_remap, hipStream_t st) {
-  if (rowptr_bits == 32)
-    return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
-                                  chunk, partials, tickets, xcd_remap, st);
-  return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
-                                    chunk, partials, tickets, xcd_remap, st);
-}
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 }  // namespace
+
+int fill_zero_f32(float* y, int64_t n, hipStream_t st) { return launch_fill<float>(y, n, st); }
+int fill_zero_f64(double* y, int64_t n, hipStream_t st) { return launch_fill<double>(y, n, st); }
+
 }  // namespace fsp
 
 using namespace fsp;
@@ -228,14 +222,16 @@ extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int3
                             const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                             const void* x, void* y, const int32_t* row_map, int64_t n_out,
                             const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                            uint32_t* tickets, int xcd_remap, void* stream) {
+                            const int32_t* groups, const int64_t* group_base,
+                            const int32_t* split_rows, int64_t n_groups, int xcd_remap,
+                            void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_csr: dtype");
   if (rowptr_bits != 32 && rowptr_bits != 64)
     return set_error(FSP_EINVAL, "fsp_spmv_csr: rowptr_bits must be 32 or 64");
-  if (n_rows < 0 || nnz < 0 || n_desc < 0 || n_out < 0)
+  if (n_rows < 0 || nnz < 0 || n_desc < 0 || n_out < 0 || n_groups < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_csr: negative size");
-  if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: more than 2^31-1 rows or descriptors");
+  if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL || n_groups > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: more than 2^31-1 rows, descriptors or groups");
   if (rowptr_bits == 32 && nnz > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_csr: nnz exceeds int32 rowptr range");
   if (chunk < 1 || chunk > kSpmvChunkCap)
@@ -243,19 +239,24 @@ extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int3
   if (n_desc > 0 && (!rowptr || !y || !desc))
     return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
   if (nnz > 0 && (!vals || !cols || !x)) return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
-  if (!aligned16(vals) || !aligned16(cols) || !aligned16(desc))
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: vals, cols and desc must be 16-byte aligned");
+  if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: null split-row pointer");
+  if (!aligned16(vals) || !aligned16(cols) || !aligned16(desc) || !aligned16(groups))
+    return set_error(FSP_EINVAL, "fsp_spmv_csr: vals, cols, desc and groups must be 16-byte aligned");
   if (row_map && !y) return set_error(FSP_EINVAL, "fsp_spmv_csr: null y");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FSP_F32) {
     if (acc_f64)
       return dispatch_ptr<float, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                         desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+                                         desc, n_desc, chunk, partials, groups, group_base,
+                                         split_rows, n_groups, xcd_remap, st);
     return dispatch_ptr<float, float>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+                                      desc, n_desc, chunk, partials, groups, group_base,
+                                      split_rows, n_groups, xcd_remap, st);
   }
   return dispatch_ptr<double, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, n_desc, chunk, partials, tickets, xcd_remap, st);
+                                      desc, n_desc, chunk, partials, groups, group_base,
+                                      split_rows, n_groups, xcd_remap, st);
 }
 
 extern "C" int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows,
@@ -272,13 +273,13 @@ extern "C" int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* r
   const int64_t blocks = (nnz + nnz_per_block - 1) / nnz_per_block;
   if (blocks > 0x7fffffffLL) return set_error(FSP_EINVAL, "fsp_spmv_coo_atomic: grid too large");
   if (dtype == FSP_F32) {
-    int rc = launch_fill<float>(static_cast<float*>(y), n_rows, st);
+    int rc = fill_zero<float>(static_cast<float*>(y), n_rows, st);
     if (rc || nnz == 0) return rc;
     hipLaunchKernelGGL(spmv_coo_atomic_kernel<float>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
                        static_cast<const float*>(vals), rows, cols, nnz,
                        static_cast<const float*>(x), static_cast<float*>(y), nnz_per_block);
   } else {
-    int rc = launch_fill<double>(static_cast<double*>(y), n_rows, st);
+    int rc = fill_zero<double>(static_cast<double*>(y), n_rows, st);
     if (rc || nnz == 0) return rc;
     hipLaunchKernelGGL(spmv_coo_atomic_kernel<double>, dim3((unsigned)blocks), dim3(kBlock), 0, st,
                        static_cast<const double*>(vals), rows, cols, nnz,

@@ -306,6 +306,14 @@ class _SpmmKernelCsr:
         self._rowptr_host = rowptr_to_host(indptr64)
         self._plans = {}
 
+    def kernel_name(self):
+        return "spmm_rowblock_kernel"
+
+    def describe(self):
+        return {"layout": "rowblock", "plans": {g: {"descriptors": p.n_desc,
+                                                    "split_rows": p.n_split_rows}
+                                                for g, p in self._plans.items()}}
+
     def plan(self, lanes):
         p = self._plans.get(lanes)
         if p is None:
@@ -327,15 +335,16 @@ def _run_spmm(kc, B, C, acc_f64, tile_cols=None):
     dtype = B.dtype
     lanes, vec = _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols)
     plan = kc.plan(lanes)
-    n_tiles = -(-n_dense_cols // (lanes * vec))
-    partials, tickets = plan.workspace(n_dense_cols, n_tiles)
+    partials = plan.workspace(n_dense_cols)
+    groups, group_base, split_rows = plan.split_groups()
     L = _abi.lib()
     _abi.check(
         L.fsp_spmm_csr(_abi.dtype_code(dtype), 1 if acc_f64 else 0, _abi.ptr(kc.data),
                        _abi.ptr(kc.cols), _abi.ptr(kc.rowptr), kc.rowptr_bits, kc.n_rows, kc.nnz,
                        _abi.ptr(B), B.stride(0), n_dense_cols, _abi.ptr(C), C.stride(0),
                        _abi.ptr(plan.desc), plan.n_desc, plan.chunk, lanes, vec,
-                       _abi.ptr(partials), _abi.ptr(tickets), XCD_REMAP,
+                       _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
+                       _abi.ptr(split_rows), int(groups.shape[0]), XCD_REMAP,
                        _abi.stream_handle(C.device)),
         "fsp_spmm_csr")
     return C

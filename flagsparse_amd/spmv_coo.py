@@ -16,10 +16,8 @@ import time
 import torch
 
 from . import _abi
-from ._common import _INDEX_LIMIT_INT32, _aligned
-from ._plan import build_row_block_plan, rowptr_to_host
-
-XCD_REMAP = 1
+from ._common import _INDEX_LIMIT_INT32
+from ._spmv_layouts import build_layout
 
 
 class PreparedCoo:
@@ -37,9 +35,7 @@ class PreparedCoo:
         "n_segs",
         "use_seg_kernel",
         "_run_rows",
-        "_plan",
-        "_kdata",
-        "_kcol",
+        "_layout",
     )
 
     def __init__(self, data, row, col, shape, seg_starts=None):
@@ -57,22 +53,28 @@ class PreparedCoo:
             self.n_segs = int(seg_starts.numel()) - 1
             self.use_seg_kernel = self.n_segs > 0
         self._run_rows = None
-        self._plan = None
-        self._kdata = _aligned(data)
-        self._kcol = _aligned(col)
+        self._layout = None
 
-    def _run_plan(self):
-        """Descriptor table over the row runs; run -> row map unless it is the identity."""
-        if self._plan is None:
-            caps = _abi.caps()
-            self._plan = build_row_block_plan(
-                rowptr_to_host(self.seg_starts), self.data.device, caps["spmv_stream_nnz"],
-                caps["spmv_stream_rows"], caps["spmv_stream_nnz"], caps["spmv_chunk_nnz"])
+    def _run_layout(self):
+        """Kernel layout over the row runs (flagsparse_amd/_spmv_layouts.py) and the
+        run -> row map, omitted when it is the identity."""
+        if self._layout is None:
+            self._layout = build_layout(self.data, self.col, self.seg_starts, self.n_cols)
             if self.n_segs == self.n_rows:
                 self._run_rows = None  # sorted and every row present: run k is row k
             else:
                 self._run_rows = self.row[self.seg_starts[:-1].to(torch.int64)].to(torch.int32)
-        return self._plan
+        return self._layout
+
+    def _kernel_name(self):
+        if self.use_seg_kernel:
+            return self._run_layout().kernel_name()
+        return "spmv_coo_atomic_kernel"
+
+    def _kernel_plan_description(self):
+        if self.use_seg_kernel:
+            return self._run_layout().describe()
+        return {"layout": "atomic"}
 
 
 def _sort_coo_lex_inplace(data, row, col, n_cols):
@@ -144,7 +146,7 @@ def prepare_spmv_coo(data, row, col, shape, sort_by_row=True):
     d, kr, kc, seg = _prepare_coo_tensors(data, row, col, shape, sort_by_row)
     prepared = PreparedCoo(d, kr, kc, shape, seg_starts=seg)
     if prepared.use_seg_kernel:
-        prepared._run_plan()
+        prepared._run_layout()
     return prepared
 
 
@@ -173,19 +175,9 @@ def _run_spmv_coo(prepared, x, y, block_size):
         y.zero_()
         return y
     if prepared.use_seg_kernel:
-        plan = prepared._run_plan()
-        partials, tickets = plan.workspace()
-        rowptr = prepared.seg_starts
-        bits = 32 if rowptr.dtype == torch.int32 else 64
-        _abi.check(
-            L.fsp_spmv_csr(_abi.dtype_code(dtype), 1 if dtype == torch.float64 else 0,
-                           _abi.ptr(prepared._kdata), _abi.ptr(prepared._kcol), _abi.ptr(rowptr),
-                           bits, prepared.n_segs, prepared.nnz, _abi.ptr(x), _abi.ptr(y),
-                           _abi.ptr(prepared._run_rows), prepared.n_rows, _abi.ptr(plan.desc),
-                           plan.n_desc, plan.chunk, _abi.ptr(partials), _abi.ptr(tickets),
-                           XCD_REMAP, stream),
-            "fsp_spmv_csr (COO runs)")
-        return y
+        layout = prepared._run_layout()
+        acc_f64 = dtype == torch.float64
+        return layout.launch(x, y, acc_f64, row_map=prepared._run_rows, n_out=prepared.n_rows)
     _abi.check(
         L.fsp_spmv_coo_atomic(_abi.dtype_code(dtype), _abi.ptr(prepared.data),
                               _abi.ptr(prepared.row), _abi.ptr(prepared.col), prepared.nnz,

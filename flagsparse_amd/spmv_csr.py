@@ -10,26 +10,23 @@ as the reference's base path does (:498-536); ``use_opt=True`` accumulates in th
 (:161-279).  float64 always accumulates in float64.  A caller's ``max_segments`` truncates
 rows exactly where the reference's static tile loop stops (:111-118 base, :308-314 opt).
 
-The kernel is one launch of ``spmv_rowblock_kernel`` (flagsparse_amd/csrc/spmv.hip) over a
-row-block descriptor table built once per matrix.
+The kernel is one launch over a layout built once per matrix (flagsparse_amd/_spmv_layouts.py):
+row blocks (csrc/spmv.hip) or, when x gathers would miss L2, the XCD column split
+(csrc/spmv_xcs.hip).
 """
 
 import time
 
 import torch
 
-from . import _abi
 from ._common import (
     SUPPORTED_INDEX_DTYPES,
     SUPPORTED_VALUE_DTYPES,
     _INDEX_LIMIT_INT32,
-    _aligned,
     _require_kernel_dtype,
 )
-from ._plan import build_row_block_plan, rowptr_to_host, truncate_rows
-
-# Place consecutive descriptors on one XCD so rows sharing x lines meet in the same L2.
-XCD_REMAP = 1
+from ._plan import truncate_rows
+from ._spmv_layouts import build_layout
 
 # Opt-path buckets of the reference (max_row_nnz, block_size, num_warps, num_stages,
 # batch_rows) - spmv_csr.py:64-89.  Only their truncation effect under a caller's
@@ -47,31 +44,6 @@ _SPMV_OPT_BUCKET_CONFIGS_FP64 = (
     (8192, 256, 8, 2, 1),
     (None, 512, 16, 1, 1),
 )
-
-
-class _KernelCsr:
-    """Kernel-facing CSR arrays (aligned) with their descriptor plan."""
-
-    __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "plan")
-
-    def __init__(self, data, cols, rowptr, plan):
-        self.data = _aligned(data)
-        self.cols = _aligned(cols)
-        if rowptr.dtype == torch.int32:
-            self.rowptr, self.rowptr_bits = rowptr.contiguous(), 32
-        elif rowptr.numel() and int(rowptr[-1].item()) <= _INDEX_LIMIT_INT32:
-            self.rowptr, self.rowptr_bits = rowptr.to(torch.int32), 32
-        else:
-            self.rowptr, self.rowptr_bits = rowptr.to(torch.int64).contiguous(), 64
-        self.nnz = int(data.numel())
-        self.plan = plan
-
-
-def _spmv_plan(rowptr, device):
-    caps = _abi.caps()
-    return build_row_block_plan(rowptr_to_host(rowptr), device, caps["spmv_stream_nnz"],
-                                caps["spmv_stream_rows"], caps["spmv_stream_nnz"],
-                                caps["spmv_chunk_nnz"])
 
 
 def _opt_bucket_block_sizes(row_lengths, fp64):
@@ -192,6 +164,7 @@ class PreparedCsrSpmv:
         return caps
 
     def _kernel(self, opt):
+        """The kernel layout (flagsparse_amd/_spmv_layouts.py) for the base or opt path."""
         key = "opt" if opt else "base"
         kc = self._kernels.get(key)
         if kc is not None:
@@ -200,12 +173,12 @@ class PreparedCsrSpmv:
         if caps is None:
             kc = self._kernels.get("full")
             if kc is None:
-                plan = _spmv_plan(self.kernel_indptr, self.data.device)
-                kc = _KernelCsr(self.data, self.kernel_indices, self.kernel_indptr, plan)
+                kc = build_layout(self.data, self.kernel_indices, self.kernel_indptr,
+                                  self.n_cols)
                 self._kernels["full"] = kc
         else:
             d, c, ip = truncate_rows(self.data, self.kernel_indices, self.kernel_indptr, caps)
-            kc = _KernelCsr(d, c, ip, _spmv_plan(ip, self.data.device))
+            kc = build_layout(d, c, ip, self.n_cols)
         self._kernels[key] = kc
         return kc
 
@@ -321,19 +294,8 @@ def _run_spmv_csr(prepared, x, opt, y):
     _require_kernel_dtype(dtype, "flagsparse_spmv_csr")
     if prepared.n_rows == 0:
         return y
-    kc = prepared._kernel(opt)
-    plan = kc.plan
-    partials, tickets = plan.workspace()
-    acc_f64 = 1 if (dtype == torch.float64 or not opt) else 0
-    L = _abi.lib()
-    _abi.check(
-        L.fsp_spmv_csr(_abi.dtype_code(dtype), acc_f64, _abi.ptr(kc.data), _abi.ptr(kc.cols),
-                       _abi.ptr(kc.rowptr), kc.rowptr_bits, prepared.n_rows, kc.nnz, _abi.ptr(x),
-                       _abi.ptr(y), None, prepared.n_rows, _abi.ptr(plan.desc), plan.n_desc,
-                       plan.chunk, _abi.ptr(partials), _abi.ptr(tickets), XCD_REMAP,
-                       _abi.stream_handle(y.device)),
-        "fsp_spmv_csr")
-    return y
+    acc_f64 = dtype == torch.float64 or not opt
+    return prepared._kernel(opt).launch(x, y, acc_f64)
 
 
 def flagsparse_spmv_csr(

@@ -18,6 +18,10 @@
  *                          spmv_csr.py:510-536 (_triton_spmv_csr_impl_prepared, default
  *                          path, fp32 accumulated in fp64); with row_map != NULL it also
  *                          replaces the row-run launch of spmv_coo.py:254-268 (_spmv_coo_seg_*).
+ *   fsp_spmv_xcs         - the same launches as fsp_spmv_csr (spmv_csr.py:329-376, :510-536,
+ *                          spmv_coo.py:254-268) for matrices whose x does not fit one XCD's L2:
+ *                          columns split into one panel per XCD (layout built by the prepare
+ *                          step, flagsparse_amd/_spmv_layouts.py).
  *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
  *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
  *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
@@ -54,6 +58,8 @@ int64_t fsp_spmv_stream_nnz_cap(void);   /* max nnz of one short-row block      
 int64_t fsp_spmv_stream_rows_cap(void);  /* max rows of one short-row block           */
 int64_t fsp_spmv_chunk_nnz_cap(void);    /* max nnz of one long-row chunk             */
 int64_t fsp_spmm_block_nnz_cap(void);    /* max nnz of one SpMM row block / row part  */
+int64_t fsp_xcs_item_cap(void);          /* max entries of one XCS item               */
+int64_t fsp_xcs_rows_cap(void);          /* max rows of one XCS tile                  */
 
 /*
  * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
@@ -79,16 +85,47 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
  *   rowptr     n_rows+1 offsets, int32 (rowptr_bits=32) or int64 (64)
  *   row_map    NULL: output row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
  *   desc       n_desc descriptors from fsp_plan_row_blocks with the caps above
- *   partials   >= n_parts slots of 8 bytes; tickets >= n_parts uint32, all zero on entry
- *              (the kernel leaves them zero again).  Calls sharing a workspace must not overlap.
  *   chunk      the chunk size the plan was built with (<= fsp_spmv_chunk_nnz_cap())
+ *   partials   >= n_parts slots of 8 bytes (chunk sums of split rows)
+ *   groups     n_groups split-row groups, 4 int32 each {first, S, n, 0}: rows
+ *              split_rows[first .. first+S) get sum over j < n of
+ *              partials[group_base[g] + j*S + s] (a second launch on the same stream).  For
+ *              this layout every split row is its own group {g, 1, nch, 0} with base = part.
+ *              Calls sharing partials must not overlap.
  *   xcd_remap  1: place consecutive descriptors on the same XCD (L2 locality of x)
  */
 int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                  const void* x, void* y, const int32_t* row_map, int64_t n_out,
                  const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                 uint32_t* tickets, int xcd_remap, void* stream);
+                 const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
+                 int64_t n_groups, int xcd_remap, void* stream);
+
+/*
+ * y = A @ x in the XCD column-split layout (fp32/fp64 values, fp64 or native accumulation).
+ *   vals, pidx   n_entries padded entries (16-byte aligned): pidx = (local row << col_bits) |
+ *                (column - panel_base[panel]); every item starts on a multiple of 4
+ *   panel_base   8 column offsets; col_bits in [1, 24]
+ *   row_map      NULL: tile row r0 + r is y[r0 + r]; else y[row_map[r0 + r]] and y[0..n_out)
+ *                is zeroed first
+ *   items        n_slots slots of 8 int32 in launch order (slot j runs on XCD j / (n_slots/8)
+ *                when n_slots is a multiple of 8): {entry start, count, tile, rank in tile,
+ *                r0, rows, panel, 0}; tile -1 marks an empty slot
+ *   tiles        4 int32 per tile: {mask word offset, split rows S, items, 0}
+ *   tile_part_base  first partial slot of each tile (int64); masks: per tile W = ceil(rows/32)
+ *                split words then W empty-row words
+ *   partials     sum over tiles of S * items slots of 8 bytes, laid out [item rank][S]
+ *   groups       split-row groups as for fsp_spmv_csr: one per tile with S > 0,
+ *                {first, S, items, 0}, base = the tile's first partial slot, split_rows the
+ *                tile's split rows in row order.  Calls sharing partials must not overlap.
+ */
+int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
+                 int64_t n_entries, const int32_t* panel_base, int col_bits, const void* x,
+                 void* y, const int32_t* row_map, int64_t n_out, const int32_t* items,
+                 int64_t n_slots, const int32_t* tiles, const int64_t* tile_part_base,
+                 const uint32_t* masks, void* partials, const int32_t* groups,
+                 const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
+                 void* stream);
 
 /*
  * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)
@@ -105,14 +142,17 @@ int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows, const 
  *                  built with rows_cap <= 256/G and nnz_cap <= fsp_spmm_block_nnz_cap()
  *   vec            elements per lane per load: 4 (fp32) / 2 (fp64) for 16-byte loads, or 1;
  *                  vec > 1 requires ldb, ldc, N multiples of vec and 16-byte aligned B, C
- *   partials       >= n_parts * N slots of 8 bytes; tickets >= n_parts * n_tiles uint32 zeroed,
- *                  n_tiles = ceil(N / (G*vec)).  Calls sharing a workspace must not overlap.
+ *   partials       >= n_parts * N slots of 8 bytes (part sums of rows cut into parts)
+ *   groups         one per row cut into parts, {g, 1, nch, 0}: C[split_rows[g], :] = sum over
+ *                  k < nch of partials[(group_base[g] + k) * N + :] (a second launch on the
+ *                  same stream).  Calls sharing partials must not overlap.
  */
 int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                  const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc,
                  const int32_t* desc, int64_t n_desc, int64_t chunk, int lanes_per_row,
-                 int vec, void* partials, uint32_t* tickets, int xcd_remap, void* stream);
+                 int vec, void* partials, const int32_t* groups, const int64_t* group_base,
+                 const int32_t* split_rows, int64_t n_groups, int xcd_remap, void* stream);
 
 #ifdef __cplusplus
 }

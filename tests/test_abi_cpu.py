@@ -124,19 +124,23 @@ def test_planner_rejects_bad_arguments():
 
 def test_kernel_entry_points_reject_before_any_hip_call():
     L = _abi.lib()
-    # unsupported dtype code
-    assert L.fsp_spmv_csr(7, 0, None, None, None, 32, 0, 0, None, None, None, 0, None, 0, 1,
-                          None, None, 0, None) == -3
+
+    def spmv(dtype=0, bits=32, chunk=1, n_groups=0):
+        return L.fsp_spmv_csr(dtype, 0, None, None, None, bits, 0, 0, None, None, None, 0, None, 0,
+                              chunk, None, None, None, None, n_groups, 0, None)
+
+    def spmm(dtype=0, lanes=1, vec=1):
+        return L.fsp_spmm_csr(dtype, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0,
+                              1, lanes, vec, None, None, None, None, 0, 0, None)
+
+    assert spmv(dtype=7) == -3                    # unsupported dtype code
     assert b"dtype" in L.fsp_last_error()
-    # bad rowptr width
-    assert L.fsp_spmv_csr(0, 0, None, None, None, 16, 0, 0, None, None, None, 0, None, 0, 1,
-                          None, None, 0, None) == -1
-    # chunk beyond the compiled capacity
-    assert L.fsp_spmv_csr(0, 0, None, None, None, 32, 0, 0, None, None, None, 0, None, 0,
-                          10**9, None, None, 0, None) == -1
-    # SpMM: lanes_per_row not a power of two, vec not allowed
-    assert L.fsp_spmm_csr(0, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0, 1, 3,
-                          1, None, None, 0, None) == -1
-    assert L.fsp_spmm_csr(1, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0, 1, 4,
-                          4, None, None, 0, None) == -1
+    assert spmv(bits=16) == -1                    # bad rowptr width
+    assert spmv(chunk=10**9) == -1                # chunk beyond the compiled capacity
+    assert spmv(n_groups=3) == -1                 # split-row groups without their arrays
+    assert b"split-row" in L.fsp_last_error()
+    assert spmm(lanes=3) == -1                    # lanes_per_row not a power of two
+    assert spmm(dtype=1, lanes=4, vec=4) == -1    # 4-wide vectors are fp32 only
+    assert L.fsp_spmv_xcs(0, 0, None, None, 0, None, 25, None, None, None, 0, None, 0, None, None,
+                          None, None, None, None, None, 0, None) == -1  # col_bits > 24
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1

@@ -1,0 +1,121 @@
+"""SpMV through the XCD column-split layout on the GPU (spmv_xcs_kernel), forced for every
+matrix here, against the fp64 CPU oracle; the automatic choice is checked to pick it for
+random-column matrices and to keep row blocks for banded ones.
+
+Bars as for the row-block kernel: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
+allclose ratio, and for the default float32 path at most 1 ulp from float32(fp64 oracle).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import flagsparse_amd as fs
+from flagsparse_amd import _spmv_layouts, synthetic
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def force_xcs():
+    old = _spmv_layouts.FORCE
+    _spmv_layouts.FORCE = "xcs"
+    yield
+    _spmv_layouts.FORCE = old
+
+
+def _ulp(a, b):
+    def ordered(v):
+        i = np.ascontiguousarray(v, dtype=np.float32).view(np.int32).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+    return np.abs(ordered(a) - ordered(b))
+
+
+def _check(y, ref64, exact_fp32=False):
+    name = "float64" if y.dtype == torch.float64 else "float32"
+    err = oracle.rel_l2(y, ref64)
+    assert err <= oracle.REL_L2_BOUND[name], f"rel_l2 {err:.3e}"
+    atol, rtol = oracle.REF_SCRIPT_TOL[name]
+    assert oracle.allclose_ratio(y, ref64, atol, rtol) <= 1.0
+    if exact_fp32:
+        u = _ulp(y.cpu().numpy(), ref64.astype(np.float32))
+        assert u.size == 0 or u.max() <= 1, u.max()
+
+
+def _csr_from_lengths(lengths, n_cols, seed, dtype):
+    keys = synthetic._distinct_sorted_columns(torch.as_tensor(lengths, dtype=torch.int64),
+                                              n_cols, seed, 1)
+    ip, cols = synthetic._csr_from_keys(keys, len(lengths), n_cols)
+    vals = synthetic.uniform_values(seed, 2, cols.numel(), dtype, "cpu")
+    x = synthetic.uniform_values(seed, 3, n_cols, dtype, "cpu")
+    return vals, cols, ip, x, (len(lengths), n_cols)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("use_opt", [False, True])
+def test_powerlaw(dev, force_xcs, dtype, use_opt):
+    data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 17, cap=60000, dtype=dtype)
+    print(f"xcs powerlaw {dtype} use_opt={use_opt}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
+    assert p._kernel(use_opt).kind == "xcs"
+    y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
+    _check(y, oracle.spmv_csr(ptr, idx, data, x),
+           exact_fp32=(dtype == torch.float32 and not use_opt))
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt))
+
+
+@pytest.mark.parametrize("lengths", [
+    [3, 0, 40000, 1, 1, 2] + [0] * 9000 + [17000, 5, 0, 6144, 7],
+    [1] * 20000 + [0] * 5000 + [2] * 7000,
+    [0] * 100 + [200000] + [0] * 100,
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_edges(dev, force_xcs, lengths, dtype):
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, 1 << 20, 13, dtype)
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev),
+                                   x.to(dev), shape, use_opt=use_opt)
+        _check(y, oracle.spmv_csr(ptr, idx, data, x),
+               exact_fp32=(dtype == torch.float32 and not use_opt))
+
+
+def test_unsorted_duplicates_and_truncation(dev, force_xcs):
+    data, idx, ptr = synthetic.build_random_csr(60000, 3000000, 400000, torch.float32,
+                                                torch.int64, "cpu", seed=4)
+    x = synthetic.uniform_values(4, 9, 3000000, torch.float32, "cpu")
+    d, i, p, xd = data.to(dev), idx.to(dev), ptr.to(dev), x.to(dev)
+    _check(fs.flagsparse_spmv_csr(d, i, p, xd, (60000, 3000000)),
+           oracle.spmv_csr(ptr, idx, data, x), exact_fp32=True)
+    row_len = (ptr[1:] - ptr[:-1]).numpy()
+    prep = fs.prepare_spmv_csr(d, i, p, (60000, 3000000), block_nnz=4, max_segments=2)
+    for use_opt in (False, True):
+        caps = oracle.spmv_row_caps(row_len, use_opt, False, prep.block_nnz, prep.max_segments, 2)
+        y = fs.flagsparse_spmv_csr(x=xd, prepared=prep, use_opt=use_opt)
+        _check(y, oracle.spmv_csr(ptr, idx, data, x, row_cap=caps))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_coo_runs(dev, force_xcs, dtype):
+    data, row, col, x, shape = synthetic.coo_uniform(1 << 17, 40 << 16, dtype=dtype)
+    ref = oracle.spmv_coo(row, col, data, x, shape[0])
+    p = fs.prepare_spmv_coo(data.to(dev), row.to(dev), col.to(dev), shape)
+    assert p._run_layout().kind == "xcs"
+    _check(fs.flagsparse_spmv_coo(x=x.to(dev), prepared=p), ref)
+    # rows without entries (run -> row map path)
+    keep = (row % 3) != 0
+    d2, r2, c2 = data[keep], row[keep], col[keep]
+    p2 = fs.prepare_spmv_coo(d2.to(dev), r2.to(dev), c2.to(dev), shape)
+    _check(fs.flagsparse_spmv_coo(x=x.to(dev), prepared=p2),
+           oracle.spmv_coo(r2, c2, d2, x, shape[0]))
+
+
+def test_automatic_choice(dev):
+    data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=5000)  # x: 8 MiB
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
+    assert p._kernel(False).kind == "xcs"
+    _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
+           exact_fp32=True)
+    d, i, pp, xx, sh = synthetic.csr_poisson2d(1024)
+    p = fs.prepare_spmv_csr(d.to(dev), i.to(dev), pp.to(dev), sh)
+    assert p._kernel(False).kind == "rowblock"

@@ -1,0 +1,170 @@
+"""The XCD column-split SpMV layout (flagsparse_amd/_spmv_layouts.py), built on the CPU and
+checked without a GPU: structural invariants the kernel relies on (every entry exactly once,
+item capacity and alignment, in-bounds packed indices, panel-to-XCD slot order), and a
+step-by-step emulation of spmv_xcs_kernel's semantics over the layout (direct rows, split-row
+partials added in item order, empty rows) against the fp64 oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from flagsparse_amd import _abi, synthetic
+from flagsparse_amd._spmv_layouts import XcsLayout, prefers_xcs, sample_indices
+from oracle import oracle
+
+
+def _emulate(layout, x, acc=np.float64):
+    """numpy restatement of spmv_xcs_kernel over the layout (every slot, then every tile)."""
+    items = layout.items.numpy().reshape(-1, 8)
+    tiles = layout.tiles.numpy()
+    masks = layout.masks.numpy().view(np.uint32)
+    pbase = layout.tile_part_base.numpy()
+    vals = layout.vals.numpy().astype(acc)
+    pidx = layout.pidx.numpy().view(np.uint32)
+    cb = layout.panel_base.numpy()
+    cbits = layout.col_bits
+    y = np.full(layout.n_rows, np.nan)
+    partials = np.full(max(layout.n_partials, 1), np.nan)
+    for e0, ln, tile, k, r0, R, panel, _ in items:
+        if tile < 0:
+            continue
+        moff, S, n_items, _ = tiles[tile]
+        W = (R + 31) // 32
+        split = lambda r: (masks[moff + r // 32] >> (r % 32)) & 1  # noqa: E731
+        empty = lambda r: (masks[moff + W + r // 32] >> (r % 32)) & 1  # noqa: E731
+        p = pidx[e0:e0 + ln]
+        lrow = (p >> cbits).astype(np.int64)
+        col = cb[panel] + (p & ((1 << cbits) - 1)).astype(np.int64)
+        prod = vals[e0:e0 + ln] * x[col].astype(acc)
+        assert np.all(np.diff(lrow) >= 0)
+        rank = 0
+        for r in range(R):
+            if empty(r):
+                if k == 0:
+                    y[r0 + r] = 0.0
+                continue
+            sel = prod[lrow == r]
+            s = acc(0)
+            for v in sel:
+                s = acc(s + v)
+            if split(r):
+                partials[pbase[tile] + k * S + rank] = s
+                rank += 1
+            elif sel.size:
+                y[r0 + r] = s
+    # second pass (split_row_combine_kernel): groups of split rows, partials [n][S]
+    groups = layout.groups.numpy()
+    gbase = layout.group_base.numpy()
+    split_rows = layout.split_rows.numpy()
+    for (first, S, n, _), base in zip(groups, gbase):
+        for si in range(S):
+            s = acc(0)
+            for j in range(n):
+                s = acc(s + partials[base + j * S + si])
+            y[split_rows[first + si]] = s
+    return y
+
+
+def _check_structure(layout, data, cols, rowptr):
+    caps = _abi.caps()
+    items = layout.items.numpy().reshape(-1, 8)
+    real = items[items[:, 2] >= 0]
+    assert np.all(real[:, 0] % 4 == 0) and np.all(real[:, 1] <= caps["xcs_item"])
+    assert np.all(real[:, 5] <= layout.rows_cap)
+    # slot p*q + j runs on XCD p: every real item of XCD p's range gathers from panel p
+    q = layout.max_items_per_panel
+    for slot, it in enumerate(items):
+        if it[2] >= 0:
+            assert it[6] == slot // q
+    # every original entry appears exactly once (multiset of (row, col, value))
+    pidx = layout.pidx.numpy().view(np.uint32)
+    vals = layout.vals.numpy()
+    cb = layout.panel_base.numpy()
+    got = []
+    for e0, ln, tile, k, r0, R, panel, _ in real:
+        p = pidx[e0:e0 + ln]
+        lr = (p >> layout.col_bits).astype(np.int64)
+        assert np.all(lr < R)
+        c = cb[panel] + (p & ((1 << layout.col_bits) - 1)).astype(np.int64)
+        hi = cb[panel + 1] if panel + 1 < len(cb) else layout.n_cols
+        assert np.all((c >= cb[panel]) & (c < hi))
+        got += list(zip((r0 + lr).tolist(), c.tolist(), vals[e0:e0 + ln].tolist()))
+    rp = rowptr.numpy()
+    want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
+            for i in range(rp[r], rp[r + 1])]
+    assert sorted(got) == sorted(want)
+
+
+def _case(lengths, n_cols, seed, dtype=torch.float32, unsorted=False):
+    lengths = torch.as_tensor(lengths, dtype=torch.int64)
+    keys = synthetic._distinct_sorted_columns(lengths, n_cols, seed, 1)
+    ip, cols = synthetic._csr_from_keys(keys, lengths.numel(), n_cols)
+    if unsorted:  # reverse each row's columns
+        for r in range(lengths.numel()):
+            a, b = int(ip[r]), int(ip[r + 1])
+            cols[a:b] = cols[a:b].flip(0)
+    vals = synthetic.uniform_values(seed, 2, cols.numel(), dtype, "cpu")
+    x = synthetic.uniform_values(seed, 3, n_cols, dtype, "cpu")
+    return vals, cols.to(torch.int32), ip, x
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_xcs_random_short_rows(seed):
+    rng = np.random.default_rng(seed)
+    lengths = rng.zipf(2.0, 6000).clip(max=300)
+    lengths[rng.integers(0, 6000, 400)] = 0
+    vals, cols, ip, x = _case(lengths, 50000, seed)
+    lay = XcsLayout(vals, cols, ip, 50000)
+    _check_structure(lay, vals, cols, ip)
+    assert lay.n_split_rows > 0
+    y = _emulate(lay, x.numpy())
+    ref = oracle.spmv_csr(ip, cols, vals, x)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_xcs_long_rows_and_empty_tiles():
+    # long rows beyond a tile (8 * item cap), item splits, a run of empty rows wider than a tile
+    lengths = [3, 0, 40000, 1, 1, 2] + [0] * 9000 + [17000, 5, 0, 2048 * 3, 7]
+    vals, cols, ip, x = _case(lengths, 300000, 4, unsorted=True)
+    lay = XcsLayout(vals, cols, ip, 300000)
+    _check_structure(lay, vals, cols, ip)
+    y = _emulate(lay, x.numpy())
+    ref = oracle.spmv_csr(ip, cols, vals, x)
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_xcs_skewed_columns_and_empty_matrix():
+    # every entry in a narrow column range: most panels empty
+    n_cols = 200000
+    lengths = torch.full((3000,), 4, dtype=torch.int64)
+    keys = synthetic._distinct_sorted_columns(lengths, 64, 9, 1)
+    ip, cols = synthetic._csr_from_keys(keys, 3000, 64)
+    cols = (cols + 1000).to(torch.int32)
+    vals = synthetic.uniform_values(9, 2, cols.numel(), torch.float64, "cpu")
+    x = synthetic.uniform_values(9, 3, n_cols, torch.float64, "cpu")
+    lay = XcsLayout(vals, cols, ip, n_cols)
+    _check_structure(lay, vals, cols, ip)
+    np.testing.assert_allclose(_emulate(lay, x.numpy()), oracle.spmv_csr(ip, cols, vals, x),
+                               rtol=1e-12, atol=1e-12)
+    # no entries at all: every row written as 0 by its tile's dummy item
+    ip0 = torch.zeros(5001, dtype=torch.int64)
+    lay = XcsLayout(torch.empty(0), torch.empty(0, dtype=torch.int32), ip0, 100)
+    assert np.all(_emulate(lay, np.ones(100)) == 0.0)
+
+
+def test_layout_choice():
+    # uniform random columns over a large x -> XCS; a banded matrix -> row blocks
+    vals, cols, ip, _ = _case([12] * 20000, 4 << 20, 2)
+    assert prefers_xcs(cols, ip, 4 << 20, 4)
+    d, i, p, _, shape = synthetic.csr_poisson2d(1024)
+    assert not prefers_xcs(i, p, shape[1], 8)
+    assert not prefers_xcs(cols, ip, 1 << 20, 4)  # x of 4 MiB fits one L2
+
+
+def test_sample_indices_stay_in_bounds():
+    # float32 spacing is 2 above 2^24: an evenly spaced sample must still end at n - 1
+    for n in (1, 5, 1 << 20, (1 << 24) + 2, 25165824, 100663296, (1 << 31) - 1):
+        idx = sample_indices(n, 1 << 20, "cpu")
+        assert idx.numel() == min(n, 1 << 20)
+        assert int(idx.min()) == 0 and int(idx.max()) == n - 1
+        assert bool((idx[1:] >= idx[:-1]).all())

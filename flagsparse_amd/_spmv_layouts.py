@@ -30,13 +30,19 @@ from ._plan import build_row_block_plan, rowptr_to_host
 
 XCD_COUNT = 8
 L2_BYTES = 4 << 20
+# Bytes of x one panel may span: leaves room in the 4 MiB L2 for the entry stream.  More
+# panels also split more rows (more partial slots), so this is a balance measured on MI355X:
+# 8.4 MB of x (2M fp32 columns) runs best as 8 panels, 33.5 MB (8M columns) as 16.
+PANEL_BYTES = 3 << 20
 # A column counts as "near" its row when within this many columns of the row's position on
 # the diagonal; the row-block layout is kept when most entries are near (x reuse in L2).
 NEAR_COLUMNS = 1 << 16
 SAMPLE = 1 << 20
 
-# Test hook: None (choose per matrix), "rowblock" or "xcs".
+# Test hooks: layout (None: choose per matrix, "rowblock" or "xcs"); panels per XCD (None:
+# from the size of x).
 FORCE = None
+FORCE_PANELS_PER_XCD = None
 
 
 def _host_rowptr(rowptr):
@@ -97,7 +103,7 @@ class XcsLayout:
 
     kind = "xcs"
 
-    def __init__(self, data, cols, rowptr, n_cols, rowptr_host=None):
+    def __init__(self, data, cols, rowptr, n_cols, rowptr_host=None, panels_per_xcd=None):
         dev = data.device
         caps = _abi.caps()
         item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
@@ -108,58 +114,82 @@ class XcsLayout:
         lengths_h = np.diff(host)
         cols = cols.to(torch.int32)
 
-        # 1. Eight column panels of about equal nnz, boundaries on 32-column (128 B) lines.
+        # 1. P = 8*m column panels of about equal nnz (m panels per XCD, run one after the
+        #    other, so that one panel of x - at most PANEL_BYTES - sits in the XCD's L2), each
+        #    at most 2^b columns wide with b the fewest bits that can cover n_cols in P panels
+        #    (more bits for the row in pidx).
+        m = panels_per_xcd
+        if m is None:
+            m = 1
+            while m < 8 and self.n_cols * data.element_size() > XCD_COUNT * m * PANEL_BYTES:
+                m *= 2
+        P = XCD_COUNT * m
+        self.n_panels = P
         hist = torch.bincount(cols, minlength=self.n_cols) if nnz else \
             torch.zeros(self.n_cols, dtype=torch.int64, device=dev)
         cum = torch.cumsum(hist, 0)
-        targets = torch.tensor([(k * nnz + XCD_COUNT - 1) // XCD_COUNT
-                                for k in range(1, XCD_COUNT)], dtype=cum.dtype, device=dev)
+        targets = torch.tensor([(k * nnz + P - 1) // P for k in range(1, P)], dtype=cum.dtype,
+                               device=dev)
         inner = (torch.searchsorted(cum, targets) + 1).cpu().numpy()
+        wmax = 1 << _ceil_log2(max(2, -(-self.n_cols // P)))
         cb = [0]
-        for b in inner.tolist():
-            b = min(self.n_cols, (int(b) + 31) // 32 * 32)
-            cb.append(max(cb[-1], b))
+        for k, b in enumerate(inner.tolist(), start=1):
+            lo = max(cb[-1], self.n_cols - (P - k) * wmax)
+            hi = min(self.n_cols, cb[-1] + wmax)
+            cb.append(min(max(int(b), lo), hi))
         cb.append(self.n_cols)
         widths = np.diff(np.array(cb))
+        assert int(widths.max()) <= wmax
         self.panel_base_host = cb
         self.col_bits = _ceil_log2(max(int(widths.max()), 2))
         row_bits = 32 - self.col_bits
         self.rows_cap = min(rows_cap, 1 << row_bits)
-        self.panel_base = torch.tensor(cb[:XCD_COUNT], dtype=torch.int32, device=dev)
+        self.panel_base = torch.tensor(cb[:P], dtype=torch.int32, device=dev)
+        if self.rows_cap < 256:
+            raise ValueError("column panels too wide for the XCS packing")
 
-        # 2. Row tiles: greedy over rows (<= rows_cap rows, <= 8 * item_cap entries); a row
-        #    longer than that is a tile of its own.
-        tile_nnz = XCD_COUNT * item_cap
-        plan = build_row_block_plan(host, None, tile_nnz, self.rows_cap, tile_nnz,
-                                    max(1, int(lengths_h.max()) if n_rows else 1))
+        # 2. Row tiles.  A row longer than 8 * item_cap entries is a tile of its own (its
+        #    partials are one value per item).  The other rows are covered greedily by tiles
+        #    of <= rows_cap consecutive rows and <= 8 * item_cap entries, in which the long
+        #    rows are rows without entries - they do not cut the run of short rows.
+        tile_nnz = P * item_cap
+        long_mask = lengths_h > tile_nnz
+        long_rows = np.nonzero(long_mask)[0]
+        short_ptr = np.zeros(n_rows + 1, dtype=np.int64)
+        short_ptr[1:] = np.cumsum(np.where(long_mask, 0, lengths_h))
+        plan = build_row_block_plan(short_ptr, None, tile_nnz, self.rows_cap, tile_nnz, 1)
         desc = plan.desc.numpy().astype(np.int64)
-        short = desc[:, 2] == 0
-        t_r0 = desc[:, 0]
-        t_R = np.where(short, desc[:, 1] - desc[:, 0], 1)
-        n_tiles = int(desc.shape[0])
+        n_long = int(long_rows.size)
+        t_r0 = np.concatenate([long_rows, desc[:, 0]]).astype(np.int64)
+        t_R = np.concatenate([np.ones(n_long, dtype=np.int64), desc[:, 1] - desc[:, 0]])
+        n_tiles = int(t_r0.size)
         self.n_tiles = n_tiles
+        self.n_long_tiles = n_long
         t_r0_d = torch.from_numpy(t_r0).to(dev)
         t_R_d = torch.from_numpy(t_R).to(dev)
-        tile_of_row = torch.repeat_interleave(torch.arange(n_tiles, device=dev), t_R_d)
+        tile_of_row = torch.repeat_interleave(torch.arange(n_long, n_tiles, device=dev),
+                                              t_R_d[n_long:])
+        if n_long:
+            tile_of_row[torch.from_numpy(long_rows).to(dev)] = torch.arange(n_long, device=dev)
         lengths = torch.from_numpy(lengths_h).to(dev)
 
         # 3. Entry -> (tile, panel); stable sort keeps row order (then original order).
         entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths)
         entry_tile = tile_of_row[entry_row]
-        bounds = torch.tensor(cb[1:XCD_COUNT], dtype=torch.int32, device=dev)
+        bounds = torch.tensor(cb[1:P], dtype=torch.int32, device=dev)
         panel = torch.bucketize(cols, bounds, right=True)
-        key = entry_tile * XCD_COUNT + panel
+        key = entry_tile * P + panel
         key_sorted, perm = torch.sort(key, stable=True)
         del key
 
         # 4. Pieces (tile, panel) -> items of <= item_cap entries (equal split).
-        n_pieces = n_tiles * XCD_COUNT
+        n_pieces = n_tiles * P
         cnt = torch.bincount(key_sorted, minlength=n_pieces) if nnz else \
             torch.zeros(n_pieces, dtype=torch.int64, device=dev)
         n_sub = (cnt + item_cap - 1) // item_cap
-        tile_tot = cnt.view(n_tiles, XCD_COUNT).sum(1)
+        tile_tot = cnt.view(n_tiles, P).sum(1)
         empty_tiles = tile_tot == 0
-        n_sub.view(n_tiles, XCD_COUNT)[:, 0] += empty_tiles.to(n_sub.dtype)  # one dummy item
+        n_sub.view(n_tiles, P)[:, 0] += empty_tiles.to(n_sub.dtype)  # one dummy item
         n_items = int(n_sub.sum().item())
         piece_first_item = torch.cumsum(n_sub, 0) - n_sub
         base = torch.where(n_sub > 0, cnt // n_sub.clamp(min=1), torch.zeros_like(cnt))
@@ -168,12 +198,19 @@ class XcsLayout:
         item_j = torch.arange(n_items, device=dev) - piece_first_item[item_piece]
         item_len = base[item_piece] + (item_j < rem[item_piece]).to(base.dtype)
         item_off = item_j * base[item_piece] + torch.minimum(item_j, rem[item_piece])
-        item_tile = item_piece // XCD_COUNT
-        item_panel = item_piece % XCD_COUNT
+        item_tile = item_piece // P
+        item_panel = item_piece % P
         items_per_tile = torch.bincount(item_tile, minlength=n_tiles)
         tile_first_item = torch.cumsum(items_per_tile, 0) - items_per_tile
         item_k = torch.arange(n_items, device=dev) - tile_first_item[item_tile]
-        padded = (item_len + 3) // 4 * 4
+        # Thread-major storage inside an item: with Q = ceil(len/4) quads, qp = ceil(Q/256)
+        # quads per thread and nt = ceil(Q/qp) threads, thread t owns the logical quads
+        # [qp*t, qp*t + qp), stored at memory quads t + nt*u.  A load of quad u by every thread
+        # is then one contiguous span, and each thread holds a contiguous run of entries.
+        q_tot = (item_len + 3) // 4
+        qp = torch.clamp((q_tot + 255) // 256, min=1)
+        nt = (q_tot + qp - 1) // qp
+        padded = 4 * nt * qp
         item_start = torch.cumsum(padded, 0) - padded
         n_entries = int(padded.sum().item()) if n_items else 0
         if n_entries > _INDEX_LIMIT_INT32:
@@ -188,12 +225,16 @@ class XcsLayout:
         big = (b + 1) * rm
         j = torch.where(o < big, o // (b + 1), rm + (o - big) // b.clamp(min=1))
         item_of = piece_first_item[key_sorted] + j
-        dest = item_start[item_of] + (o - item_off[item_of])
+        oi = o - item_off[item_of]  # logical position inside the item
+        qpi = qp[item_of]
+        lq = oi // 4
+        dest = item_start[item_of] + 4 * (lq // qpi + nt[item_of] * (lq % qpi)) + oi % 4
+        del oi, qpi, lq
         del o, b, rm, big, j
         vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
         vals[dest] = data[perm]
-        loc_row = (entry_row[perm] - t_r0_d[key_sorted // XCD_COUNT]).to(torch.int64)
-        pan = key_sorted % XCD_COUNT
+        loc_row = (entry_row[perm] - t_r0_d[key_sorted // P]).to(torch.int64)
+        pan = key_sorted % P
         colp = cols[perm].to(torch.int64) - self.panel_base.to(torch.int64)[pan]
         packed = (loc_row << self.col_bits) | colp
         pidx = torch.zeros(max(n_entries, 4), dtype=torch.int64, device=dev)
@@ -202,17 +243,37 @@ class XcsLayout:
         self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
         del packed, colp, pan, loc_row, pidx, dest
 
-        # 6. Direct / split / empty rows and the per-tile masks.
+        # 6. Direct / split / empty rows, the per-tile masks, and the split-row slots: one
+        #    per (item, split row it holds), an item's slots consecutive in row order.
         row_min = torch.full((n_rows,), n_items, dtype=torch.int64, device=dev)
         row_max = torch.full((n_rows,), -1, dtype=torch.int64, device=dev)
+        er = entry_row[perm]
         if nnz:
-            er = entry_row[perm]
             row_min.scatter_reduce_(0, er, item_of, reduce="amin")
             row_max.scatter_reduce_(0, er, item_of, reduce="amax")
-            del er
-        del entry_row, perm, key_sorted, item_of
+        del entry_row, perm, key_sorted
         empty = lengths == 0
         split = (row_max > row_min) & ~empty
+        sel = split[er]  # sorted entries of split rows, in (item, row) order
+        pair_key = torch.unique_consecutive(item_of[sel] * max(n_rows, 1) + er[sel])
+        del sel, er, item_of
+        pair_item = pair_key // max(n_rows, 1)
+        pair_row = pair_key % max(n_rows, 1)
+        n_pairs = int(pair_key.numel())
+        per_item = torch.bincount(pair_item, minlength=n_items) if n_pairs else \
+            torch.zeros(n_items, dtype=torch.int64, device=dev)
+        item_slot = torch.cumsum(per_item, 0) - per_item
+        by_row = torch.sort(pair_row, stable=True)[1]  # item order kept within a row
+        self.slots = by_row.to(torch.int32).contiguous()
+        self.split_rows = torch.nonzero(split).flatten().to(torch.int32).contiguous()
+        counts = torch.bincount(pair_row, minlength=n_rows)[split.nonzero().flatten()] \
+            if n_pairs else torch.zeros(0, dtype=torch.int64, device=dev)
+        sp = torch.zeros(counts.numel() + 1, dtype=torch.int64, device=dev)
+        sp[1:] = torch.cumsum(counts, 0)
+        self.split_ptr = sp.to(torch.int32).contiguous()
+        self.n_split_rows = int(self.split_rows.numel())
+        self.n_partials = n_pairs
+        del pair_key, pair_item, pair_row, by_row, counts
         W = (t_R_d + 31) // 32
         mask_off = torch.cumsum(2 * W, 0) - 2 * W
         n_words = int((2 * W).sum().item())
@@ -224,38 +285,31 @@ class XcsLayout:
         masks.scatter_add_(0, word[split], bit[split])
         masks.scatter_add_(0, (word + W[tile_of_row])[empty], bit[empty])
         self.masks = torch.where(masks >= (1 << 31), masks - (1 << 32), masks).to(torch.int32)
-        S = torch.bincount(tile_of_row[split], minlength=n_tiles) if n_rows else \
-            torch.zeros(n_tiles, dtype=torch.int64, device=dev)
-        slots = S * items_per_tile
-        self.tile_part_base = (torch.cumsum(slots, 0) - slots).contiguous()
-        self.n_partials = int(slots.sum().item()) if n_tiles else 0
-        self.n_split_rows = int(split.sum().item()) if n_rows else 0
-        tiles = torch.stack([mask_off, S, items_per_tile, torch.zeros_like(S)], 1)
-        self.tiles = tiles.to(torch.int32).contiguous()
-        # second-pass groups: tiles with split rows; split rows in (tile, row) order
-        gt = torch.nonzero(S > 0).flatten()
-        self.split_rows = torch.nonzero(split).flatten().to(torch.int32)
-        first = torch.cumsum(S, 0) - S
-        self.groups = torch.stack([first[gt], S[gt], items_per_tile[gt], torch.zeros_like(gt)],
-                                  1).to(torch.int32).contiguous()
-        self.group_base = self.tile_part_base[gt].contiguous()
-        self.n_groups = int(gt.numel())
 
-        # 7. Launch order: XCD p runs the items of panel p, in tile order; lists padded to
-        #    the same length q so that slot p*q + j lands on XCD p.
-        per_panel = torch.bincount(item_panel, minlength=XCD_COUNT)
-        q = int(per_panel.max().item()) if n_items else 0
+        # 7. Launch order: XCD x runs the items of panels x, x + 8, x + 16, ... (one panel
+        #    after the other, each in tile order); lists padded to the same length q so that
+        #    slot x*q + j lands on XCD x.
+        xcd = item_panel % XCD_COUNT
+        phase = item_panel // XCD_COUNT
+        per_xcd = torch.bincount(xcd, minlength=XCD_COUNT)
+        q = int(per_xcd.max().item()) if n_items else 0
         self.n_slots = XCD_COUNT * q
-        order = torch.argsort(item_panel, stable=True)
-        panel_first = torch.cumsum(per_panel, 0) - per_panel
-        rank = torch.arange(n_items, device=dev) - panel_first[item_panel[order]]
-        slot_of = item_panel[order] * q + rank
-        d = torch.zeros((max(self.n_slots, 1), 8), dtype=torch.int64, device=dev)
-        d[:, 2] = -1
+        skey = (xcd * m + phase) * (n_tiles + 1) + item_tile
+        order = torch.sort(skey, stable=True)[1]
+        xcd_first = torch.cumsum(per_xcd, 0) - per_xcd
+        rank = torch.arange(n_items, device=dev) - xcd_first[xcd[order]]
+        slot_of = xcd[order] * q + rank
+        d = torch.zeros((max(self.n_slots, 1), 12), dtype=torch.int64, device=dev)
+        d[:, 10] = -1
         it = order
-        d[slot_of] = torch.stack([item_start[it], item_len[it], item_tile[it], item_k[it],
-                                  t_r0_d[item_tile[it]], t_R_d[item_tile[it]], item_panel[it],
+        t = item_tile[it]
+        pb = item_slot[it]
+        d[slot_of] = torch.stack([item_start[it], item_len[it], item_k[it], torch.zeros_like(t),
+                                  t_r0_d[t],
+                                  t_R_d[t], self.panel_base.to(torch.int64)[item_panel[it]],
+                                  mask_off[t], pb & 0xFFFFFFFF, pb >> 32, t,
                                   torch.zeros_like(it)], 1)
+        d = torch.where(d >= (1 << 31), d - (1 << 32), d)
         self.items = d.to(torch.int32).contiguous()
         self.n_items = n_items
         self.max_items_per_panel = q
@@ -265,7 +319,9 @@ class XcsLayout:
         return "spmv_xcs_kernel"
 
     def describe(self):
-        return {"layout": self.kind, "tiles": self.n_tiles, "items": self.n_items,
+        return {"layout": self.kind, "panels": self.n_panels, "tiles": self.n_tiles,
+                "long_row_tiles": self.n_long_tiles,
+                "items": self.n_items,
                 "slots": self.n_slots, "split_rows": self.n_split_rows,
                 "partials": self.n_partials, "panel_base": self.panel_base_host,
                 "col_bits": self.col_bits, "padded_entries": self.n_entries}
@@ -274,12 +330,11 @@ class XcsLayout:
         L = _abi.lib()
         _abi.check(
             L.fsp_spmv_xcs(_abi.dtype_code(self.vals.dtype), int(acc_f64), _abi.ptr(self.vals),
-                           _abi.ptr(self.pidx), self.n_entries, _abi.ptr(self.panel_base),
-                           self.col_bits, _abi.ptr(x), _abi.ptr(y), _abi.ptr(row_map), n_out,
-                           _abi.ptr(self.items), self.n_slots, _abi.ptr(self.tiles),
-                           _abi.ptr(self.tile_part_base), _abi.ptr(self.masks),
-                           _abi.ptr(self.partials), _abi.ptr(self.groups),
-                           _abi.ptr(self.group_base), _abi.ptr(self.split_rows), self.n_groups,
+                           _abi.ptr(self.pidx), self.n_entries, self.col_bits, _abi.ptr(x),
+                           _abi.ptr(y), _abi.ptr(row_map), n_out, _abi.ptr(self.items),
+                           self.n_slots, _abi.ptr(self.masks), _abi.ptr(self.partials),
+                           _abi.ptr(self.split_rows), _abi.ptr(self.split_ptr),
+                           _abi.ptr(self.slots), self.n_split_rows,
                            _abi.stream_handle(y.device)),
             "fsp_spmv_xcs")
         return y
@@ -314,9 +369,12 @@ def build_layout(data, cols, rowptr, n_cols):
     host = _host_rowptr(rowptr)
     if mode is None:
         mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
-    if mode == "xcs" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(n_cols) < (1 << 27) and \
+    if mode == "xcs" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(n_cols) <= (1 << 27) and \
             int(rowptr.numel()) > 1:
-        return XcsLayout(data, cols, rowptr, n_cols, host)
+        try:
+            return XcsLayout(data, cols, rowptr, n_cols, host, FORCE_PANELS_PER_XCD)
+        except ValueError:
+            pass  # too large for the packing: row blocks
     return RowBlockLayout(data, cols, rowptr, host)
 
 

@@ -134,17 +134,23 @@ __device__ __forceinline__ int xcd_logical_block(int i, int n) {
 // rows split_rows[first .. first + S), its partials start at group_base[g] and are laid out
 // [n][S].  It runs as a separate launch on the same stream: the kernel boundary makes the
 // first pass's partials visible on every XCD, so neither pass needs a device-scope fence.
+// With reset != 0 every slot read is set back to 0, for first passes that write only the
+// slots of rows they hold.
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
     const i32x4* __restrict__ groups, const int64_t* __restrict__ group_base,
-    const int* __restrict__ split_rows, const A* __restrict__ partials, T* __restrict__ y,
-    const int* __restrict__ row_map) {
+    const int* __restrict__ split_rows, A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map, int reset) {
   const i32x4 g = groups[blockIdx.x];
   const int first = g.x, S = g.y, n = g.z;
   const int64_t base = group_base[blockIdx.x];
   for (int s = threadIdx.x; s < S; s += kBlock) {
     A acc = A(0);
-    for (int j = 0; j < n; ++j) acc += partials[base + (int64_t)j * S + s];
+    for (int j = 0; j < n; ++j) {
+      A* p = &partials[base + (int64_t)j * S + s];
+      acc += *p;
+      if (reset) *p = A(0);
+    }
     const int row = split_rows[first + s];
     y[row_map ? row_map[row] : row] = T(acc);
   }

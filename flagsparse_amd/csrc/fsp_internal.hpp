@@ -19,7 +19,7 @@ constexpr int64_t kSpmvChunkCap = kSpmvChunkUnitsPerThread * 4 * 256 - 3;
 constexpr int64_t kSpmmSlots = 2048;                     // LDS (col, val) slots per SpMM block
 constexpr int64_t kSpmmNnzCap = kSpmmSlots - 3;
 constexpr int64_t kXcsItemCap = 2048;                    // entries of one XCS item
-constexpr int64_t kXcsRowsCap = 4096;                    // rows of one XCS tile
+constexpr int64_t kXcsRowsCap = 8192;                    // rows of one XCS tile
 
 // Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).
 int fill_zero_f32(float* y, int64_t n, hipStream_t st);

@@ -173,7 +173,7 @@ int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64
   if (rc || n_groups == 0) return rc;
   hipLaunchKernelGGL((split_row_combine_kernel<T, A>), dim3((unsigned)n_groups), dim3(kBlock), 0,
                      st, reinterpret_cast<const i32x4*>(groups), group_base, split_rows,
-                     static_cast<const A*>(partials), static_cast<T*>(y), row_map);
+                     static_cast<A*>(partials), static_cast<T*>(y), row_map, 0);
   return check_hip(hipGetLastError(), "split_row_combine_kernel launch");
 }
 

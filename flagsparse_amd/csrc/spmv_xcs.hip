@@ -8,14 +8,20 @@
 // Layout (built by the host prepare step, flagsparse_amd/_spmv_layouts.py):
 //   tiles   contiguous row ranges [r0, r0 + R), R <= kXcsRowsCap (a long row is a tile alone)
 //   items   the entries of one tile that fall in one panel, cut into pieces of <= kXcsItemCap
-//           entries; each item's entries are contiguous in (vals, pidx), start on a multiple
-//           of 4, and are ordered by row (original order inside a row)
-//   pidx    (local row << col_bits) | (column - panel_base[panel])
+//           entries, ordered by row (original order inside a row); an item's Q = ceil(len/4)
+//           quads of entries start on a multiple of 4 and are stored thread-major: with
+//           qp = ceil(Q/256) quads per thread and nt = ceil(Q/qp) threads, logical quad
+//           qp*t + u is at memory quad t + nt*u (coalesced loads, contiguous rows per thread)
+//   pidx    (local row << col_bits) | (column - the panel's first column)
+//   slots   one item descriptor per workgroup in launch order, 12 int32:
+//           {entry start, count, rank k in tile, 0, r0, rows R, panel first column,
+//            mask word offset, first partial slot (2 x int32), tile (-1: empty slot), 0}
 //   rows    "direct" when all of a row's entries lie in one item: that item writes y;
-//           "split" otherwise: every item of the tile writes one partial per split row (zero
-//           when it holds none of that row) and a second launch (split_row_combine_kernel)
-//           adds the tile's partials in item order - a fixed order, so the result does not
-//           depend on timing; "empty" rows are written as 0 by the tile's first item.
+//           "split" otherwise: every item holding entries of a split row writes that row's sum
+//           to a slot of its own (an item's slots are consecutive, in row order), and a
+//           second launch (xcs_split_combine_kernel) adds each split row's slots in item order
+//           - a fixed order, so the result does not depend on timing; "empty" rows are
+//           written as 0 by the tile's first item.
 //           No workgroup waits for or signals another: a device-scope fence would write back
 //           and invalidate the XCD's L2, which holds the x panel this layout exists to keep.
 //
@@ -30,175 +36,253 @@ namespace {
 
 constexpr int kItemCap = (int)kXcsItemCap;
 constexpr int kRowsCap = (int)kXcsRowsCap;
-constexpr int kItemUPT = kItemCap / (4 * kBlock);  // quads of entries per thread
-static_assert(kItemUPT * 4 * kBlock == kItemCap, "item capacity must be whole quads per thread");
 static_assert(kRowsCap % 32 == 0 && kRowsCap <= 65535, "row ids are kept as 16-bit values");
 
 __device__ __forceinline__ bool mask_bit(const uint32_t* m, int r) {
   return (m[r >> 5] >> (r & 31)) & 1u;
 }
 
+// Segmented sums over an item: thread t owns a contiguous run of the item's entries, which
+// holds whole runs (rows) and pieces of runs that continue from or into its neighbours.  A
+// workgroup-wide segmented scan over (has a run start, sum of the last run piece) - combine(a,
+// b) = (a.h | b.h, b.h ? b.v : a.v + b.v), evaluated in a fixed pattern - gives each thread
+// the sum of the run piece that ends just before its chunk.  No LDS round trip of products.
 template <typename T, typename A, bool NT>
 __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
-    const T* __restrict__ vals, const uint32_t* __restrict__ pidx,
-    const int* __restrict__ panel_base, int col_bits, const T* __restrict__ x,
-    T* __restrict__ y, const int* __restrict__ row_map, const i32x4* __restrict__ items,
-    int n_slots, const i32x4* __restrict__ tiles, const int64_t* __restrict__ tile_part_base,
-    const uint32_t* __restrict__ masks, A* __restrict__ partials) {
-  __shared__ A s_prod[kItemCap];
-  __shared__ uint16_t s_row[kItemCap];
-  __shared__ int16_t s_start[kRowsCap];  // first entry of each local row in this item, -1: none
-  __shared__ int16_t s_end[kRowsCap];    // one past its last entry
+    const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
+    const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
+    const i32x4* __restrict__ items, int n_slots, const uint32_t* __restrict__ masks,
+    A* __restrict__ partials) {
+  constexpr int kPer = kItemCap / kBlock;  // entries per thread at most
+  constexpr int kQuads = kPer / 4;
+  static_assert(kQuads * 4 == kPer, "whole quads of entries per thread");
   __shared__ uint32_t s_split[kRowsCap / 32];
   __shared__ uint32_t s_empty[kRowsCap / 32];
-  __shared__ int s_rank[kRowsCap / 32];
+  __shared__ int s_first_row[kWavesPerBlock];
+  __shared__ int s_last_row[kWavesPerBlock];
+  __shared__ int s_wh[kWavesPerBlock];
+  __shared__ int s_wc[kWavesPerBlock];
+  __shared__ A s_wv[kWavesPerBlock];
 
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
   const int slot = xcd_logical_block(blockIdx.x, n_slots);
-  const i32x4 d0 = items[2 * slot];
-  const i32x4 d1 = items[2 * slot + 1];
-  const int tile = d0.z;
-  if (tile < 0) return;  // padding slot
-  const int e0 = d0.x, len = d0.y, k = d0.w;
-  const int r0 = d1.x, R = d1.y, panel = d1.z;
+  const i32x4 d0 = items[3 * slot];
+  const i32x4 d1 = items[3 * slot + 1];
+  const i32x4 d2 = items[3 * slot + 2];
+  if (d2.z < 0) return;  // empty slot
+  const int e0 = d0.x, len = d0.y, k = d0.z;
+  const int r0 = d1.x, R = d1.y, cbase = d1.z, mask_off = d1.w;
+  const int64_t sbase = (int64_t)(((uint64_t)(uint32_t)d2.y << 32) | (uint32_t)d2.x);
   if (R <= 0 || R > kRowsCap || len < 0 || len > kItemCap) return;  // not a planner item
-  const i32x4 td = tiles[tile];
-  const int mask_off = td.x, S = td.y;
   const int W = (R + 31) >> 5;
 
+  // Split / empty row masks of the tile, published by the first barrier below.
   for (int w = tid; w < W; w += kBlock) {
     s_split[w] = masks[mask_off + w];
     s_empty[w] = masks[mask_off + W + w];
   }
-  for (int r = tid; r < R; r += kBlock) s_start[r] = -1;
 
-  // Entries -> products and local rows in LDS.
-  const int cbase = panel_base[panel];
-  const uint32_t cmask = (1u << col_bits) - 1u;
-  T v[kItemUPT][4];
-  uint32_t c[kItemUPT][4];
+  // Entries [i0, i0 + nm) of this thread (thread-major storage, see the file comment).
+  const int q_tot = (len + 3) >> 2;
+  const int qp = q_tot > 0 ? (q_tot + kBlock - 1) / kBlock : 1;
+  const int nt = (q_tot + qp - 1) / qp;
+  const int i0 = 4 * qp * tid;
+  const int nm = len - i0 < 0 ? 0 : (len - i0 > 4 * qp ? 4 * qp : len - i0);
+  T v[kPer];
+  uint32_t c[kPer];
 #pragma unroll
-  for (int u = 0; u < kItemUPT; ++u) {
-    const int i = 4 * (tid + u * kBlock);
-    if (i < len) {
+  for (int h = 0; h < kQuads; ++h) {
+    if (h < qp && 4 * h < nm) {
+      const int m = 4 * (tid + nt * h);  // memory position of logical quad qp*tid + h
       if constexpr (sizeof(T) == 4) {
-        const f32x4 vv = ld_stream<NT>(reinterpret_cast<const f32x4*>(vals + e0 + i));
-        v[u][0] = vv.x; v[u][1] = vv.y; v[u][2] = vv.z; v[u][3] = vv.w;
+        const f32x4 vv = ld_stream<NT>(reinterpret_cast<const f32x4*>(vals + e0 + m));
+        v[4 * h] = vv.x; v[4 * h + 1] = vv.y; v[4 * h + 2] = vv.z; v[4 * h + 3] = vv.w;
       } else {
-        const f64x2 a = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + e0 + i));
-        const f64x2 b = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + e0 + i + 2));
-        v[u][0] = a.x; v[u][1] = a.y; v[u][2] = b.x; v[u][3] = b.y;
+        const f64x2 a = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + e0 + m));
+        const f64x2 b = ld_stream<NT>(reinterpret_cast<const f64x2*>(vals + e0 + m + 2));
+        v[4 * h] = a.x; v[4 * h + 1] = a.y; v[4 * h + 2] = b.x; v[4 * h + 3] = b.y;
       }
-      const i32x4 cc = ld_stream<NT>(reinterpret_cast<const i32x4*>(pidx + e0 + i));
-      c[u][0] = (uint32_t)cc.x; c[u][1] = (uint32_t)cc.y;
-      c[u][2] = (uint32_t)cc.z; c[u][3] = (uint32_t)cc.w;
+      const i32x4 cc = ld_stream<NT>(reinterpret_cast<const i32x4*>(pidx + e0 + m));
+      c[4 * h] = (uint32_t)cc.x; c[4 * h + 1] = (uint32_t)cc.y;
+      c[4 * h + 2] = (uint32_t)cc.z; c[4 * h + 3] = (uint32_t)cc.w;
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { v[u][j] = T(0); c[u][j] = 0u; }
+      for (int j = 0; j < 4; ++j) { v[4 * h + j] = T(0); c[4 * h + j] = 0u; }
     }
   }
-  T xv[kItemUPT][4];
+  const uint32_t cmask = (1u << col_bits) - 1u;
+  T xv[kPer];
 #pragma unroll
-  for (int u = 0; u < kItemUPT; ++u)
+  for (int q = 0; q < kPer; ++q) xv[q] = q < nm ? x[cbase + (int)(c[q] & cmask)] : T(0);
+  A prod[kPer];
+  int row[kPer];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 4 * (tid + u * kBlock) + j;
-      xv[u][j] = i < len ? x[cbase + (int)(c[u][j] & cmask)] : T(0);
-    }
-#pragma unroll
-  for (int u = 0; u < kItemUPT; ++u)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 4 * (tid + u * kBlock) + j;
-      if (i < len) {
-        s_prod[i] = A(v[u][j]) * A(xv[u][j]);
-        s_row[i] = (uint16_t)(c[u][j] >> col_bits);
-      }
-    }
-  __syncthreads();
-  // Row runs: entries are ordered by local row, so each present row is one run [start, end).
-  for (int i = tid; i < len; i += kBlock) {
-    const int r = s_row[i];
-    if (i == 0 || s_row[i - 1] != r) s_start[r] = (int16_t)i;
-    if (i == len - 1 || s_row[i + 1] != r) s_end[r] = (int16_t)(i + 1);
+  for (int q = 0; q < kPer; ++q) {
+    prod[q] = A(v[q]) * A(xv[q]);
+    row[q] = (int)(c[q] >> col_bits);
   }
 
-  // Split-row ranks: s_rank[w] = split rows in words [0, w).
-  if (tid < 64) {
-    int carry = 0;
-    for (int w0 = 0; w0 < W; w0 += 64) {
-      const int w = w0 + tid;
-      const int cnt = w < W ? __popc(s_split[w]) : 0;
-      int incl = cnt;
+  // Rows of the entries just before and just after this thread's chunk (-1: none).
+  const int my_first = nm > 0 ? row[0] : -1;
+  int my_last = row[0];
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int t = __shfl_up(incl, off, kWave);
-        if (tid >= off) incl += t;
-      }
-      if (w < W) s_rank[w] = carry + incl - cnt;
-      carry += __shfl(incl, kWave - 1, kWave);
-    }
-  }
-  __syncthreads();
+  for (int q = 1; q < kPer; ++q)
+    if (q < nm) my_last = row[q];
+  if (lane == 0) s_first_row[wid] = my_first;
+  if (lane == kWave - 1) s_last_row[wid] = my_last;
+  __syncthreads();  // also publishes the masks
+  int prev_row = __shfl_up(my_last, 1, kWave);
+  if (lane == 0) prev_row = wid > 0 ? s_last_row[wid - 1] : -1;
+  if (tid == 0) prev_row = -1;
+  int next_row = __shfl_down(my_first, 1, kWave);
+  if (lane == kWave - 1) next_row = wid + 1 < kWavesPerBlock ? s_first_row[wid + 1] : -1;
+  if (i0 + nm >= len) next_row = -1;  // my chunk ends the item
 
-  const int64_t pbase = tile_part_base[tile];
-  // Lanes per row: the largest power of two G <= 64 with G * next_pow2(R) <= 256.
-  int lg = 0;
-  if (R < kBlock) {
-    int p2 = 1, lp = 0;
-    while (p2 < R) { p2 <<= 1; ++lp; }
-    lg = 8 - lp;
-    if (lg > 6) lg = 6;
-  }
-  const int G = 1 << lg;
-  const int ngrp = kBlock >> lg;
-  const int grp = tid >> lg, lane = tid & (G - 1);
-  for (int r = grp; r < R; r += ngrp) {
-    if (mask_bit(s_empty, r)) {
-      if (k == 0 && lane == 0) {
-        const int row = r0 + r;
-        y[row_map ? row_map[row] : row] = T(0);
+  // Local pass over the chunk.  A run (row) "ends here" when its last entry is in this chunk.
+  // Runs that start and end here are recorded at the position of their last entry; the run
+  // the chunk starts with, when it continues from before (cont), is completed after the scan
+  // with the carry.  The last piece (sum since the last run start) feeds the scan.
+  const bool cont = nm > 0 && my_first == prev_row;
+  A piece = A(0);
+  A first_piece = A(0);
+  bool first_open = true;
+  int has_head = (nm > 0 && !cont) ? 1 : 0;
+  uint32_t ends = 0;  // bit q: a recorded run ends at entry q
+  A end_sum[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    end_sum[q] = A(0);
+    if (q < nm) {
+      if (q > 0 && row[q] != row[q - 1]) {  // the run of row[q - 1] ends at q - 1
+        if (first_open) {
+          first_piece = piece;
+          first_open = false;
+          if (!cont) { ends |= 1u << (q - 1); end_sum[q - 1] = piece; }
+        } else {
+          ends |= 1u << (q - 1);
+          end_sum[q - 1] = piece;
+        }
+        has_head = 1;
+        piece = A(0);
       }
-      continue;
+      piece += prod[q];
     }
-    const bool split = mask_bit(s_split, r);
-    const int lo = s_start[r];
-    if (!split && lo < 0) continue;  // a direct row written by another item
-    const int hi = lo < 0 ? lo : s_end[r];
-    A acc = A(0);
-    for (int i = lo + lane; i < hi; i += G) acc += s_prod[i];
-    if (G > 1) acc = group_sum(acc, G);
-    if (lane == 0) {
-      if (split) {
-        const int s = s_rank[r >> 5] + __popc(s_split[r >> 5] & ((1u << (r & 31)) - 1u));
-        partials[pbase + (int64_t)k * S + s] = acc;
-      } else {
-        const int row = r0 + r;
-        y[row_map ? row_map[row] : row] = T(acc);
+  }
+  const bool last_ends = nm > 0 && next_row != my_last;
+  if (first_open) first_piece = piece;
+  const bool first_pending = cont && (!first_open || last_ends);
+  if (last_ends && !(first_open && cont)) {
+#pragma unroll
+    for (int q = 0; q < kPer; ++q)
+      if (q == nm - 1) { ends |= 1u << q; end_sum[q] = piece; }
+  }
+  // Split runs ending here need consecutive slots: count them for the slot scan.
+  int n_split = (first_pending && mask_bit(s_split, my_first)) ? 1 : 0;
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if (((ends >> q) & 1u) && mask_bit(s_split, row[q])) ++n_split;
+
+  // Workgroup scans, one barrier: segmented scan of (has_head, last piece) gives the carry -
+  // the sum of the run piece that ends just before this chunk - and a plain scan of n_split
+  // gives this thread's first slot.
+  int h_in = has_head;
+  A v_in = piece;
+  int c_in = n_split;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int ho = __shfl_up(h_in, off, kWave);
+    const A vo = __shfl_up(v_in, off, kWave);
+    const int co = __shfl_up(c_in, off, kWave);
+    if (lane >= off) {
+      if (!h_in) v_in = vo + v_in;
+      h_in |= ho;
+      c_in += co;
+    }
+  }
+  if (lane == kWave - 1) {
+    s_wh[wid] = h_in;
+    s_wv[wid] = v_in;
+    s_wc[wid] = c_in;
+  }
+  int h_ex = __shfl_up(h_in, 1, kWave);
+  A v_ex = __shfl_up(v_in, 1, kWave);
+  int c_ex = __shfl_up(c_in, 1, kWave);
+  if (lane == 0) { h_ex = 0; v_ex = A(0); c_ex = 0; }
+  __syncthreads();
+  A pv = A(0);
+  int pc = 0;
+  for (int j = 0; j < wid; ++j) {  // waves before this one, in order
+    const A wv = s_wv[j];
+    if (!s_wh[j]) pv = pv + wv; else pv = wv;
+    pc += s_wc[j];
+  }
+  const A carry = h_ex ? v_ex : pv + v_ex;
+  int next_slot = pc + c_ex;
+
+  // Emit, in row order: direct rows go to y, split rows to the item's next slot.
+  auto emit = [&](int r, A sum) {
+    if (mask_bit(s_split, r)) {
+      partials[sbase + next_slot] = sum;
+      ++next_slot;
+    } else {
+      const int row_o = r0 + r;
+      y[row_map ? row_map[row_o] : row_o] = T(sum);
+    }
+  };
+  if (first_pending) emit(my_first, carry + first_piece);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q)
+    if ((ends >> q) & 1u) emit(row[q], end_sum[q]);
+
+  // Empty rows: the tile's first item writes y = 0.
+  if (k == 0) {
+    for (int w = tid; w < W; w += kBlock) {
+      uint32_t e = s_empty[w];
+      while (e) {
+        const int b = __ffs(e) - 1;
+        e &= e - 1u;
+        const int row_e = r0 + w * 32 + b;
+        y[row_map ? row_map[row_e] : row_e] = T(0);
       }
     }
   }
 }
 
+// Second pass: split row i gets y[split_rows[i]] = sum of partials[slots[j]] for j in
+// [split_ptr[i], split_ptr[i+1]), j increasing (slots listed in item order, a fixed order).
+// A separate launch: the kernel boundary makes the first pass's partials visible on every
+// XCD, so neither pass needs a device-scope fence.
 template <typename T, typename A>
-int launch_xcs(const void* vals, const uint32_t* pidx, const int32_t* panel_base, int col_bits,
-               const void* x, void* y, const int32_t* row_map, const int32_t* items,
-               int64_t n_slots, const int32_t* tiles, const int64_t* tile_part_base,
-               const uint32_t* masks, void* partials, const int32_t* groups,
-               const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
-               hipStream_t st) {
+__global__ __launch_bounds__(kBlock) void xcs_split_combine_kernel(
+    const int* __restrict__ split_rows, const int* __restrict__ split_ptr,
+    const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map, int n_split) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n_split) return;
+  const int a = split_ptr[i], b = split_ptr[i + 1];
+  A acc = A(0);
+  for (int j = a; j < b; ++j) acc += partials[slots[j]];
+  const int row = split_rows[i];
+  y[row_map ? row_map[row] : row] = T(acc);
+}
+
+template <typename T, typename A>
+int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
+               const int32_t* row_map, const int32_t* items, int64_t n_slots,
+               const uint32_t* masks, void* partials, const int32_t* split_rows,
+               const int32_t* split_ptr, const int32_t* slots, int64_t n_split, hipStream_t st) {
   hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock), 0, st,
-                     static_cast<const T*>(vals), pidx, panel_base, col_bits,
-                     static_cast<const T*>(x), static_cast<T*>(y), row_map,
-                     reinterpret_cast<const i32x4*>(items), (int)n_slots,
-                     reinterpret_cast<const i32x4*>(tiles), tile_part_base, masks,
-                     static_cast<A*>(partials));
+                     static_cast<const T*>(vals), pidx, col_bits, static_cast<const T*>(x),
+                     static_cast<T*>(y), row_map, reinterpret_cast<const i32x4*>(items),
+                     (int)n_slots, masks, static_cast<A*>(partials));
   int rc = check_hip(hipGetLastError(), "spmv_xcs_kernel launch");
-  if (rc || n_groups == 0) return rc;
-  hipLaunchKernelGGL((split_row_combine_kernel<T, A>), dim3((unsigned)n_groups), dim3(kBlock), 0,
-                     st, reinterpret_cast<const i32x4*>(groups), group_base, split_rows,
-                     static_cast<const A*>(partials), static_cast<T*>(y), row_map);
-  return check_hip(hipGetLastError(), "split_row_combine_kernel launch");
+  if (rc || n_split == 0) return rc;
+  const int64_t blocks = (n_split + kBlock - 1) / kBlock;
+  hipLaunchKernelGGL((xcs_split_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0,
+                     st, split_rows, split_ptr, slots, static_cast<const A*>(partials),
+                     static_cast<T*>(y), row_map, (int)n_split);
+  return check_hip(hipGetLastError(), "xcs_split_combine_kernel launch");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -209,29 +293,25 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 using namespace fsp;
 
 extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
-                            int64_t n_entries, const int32_t* panel_base, int col_bits,
-                            const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                            const int32_t* items, int64_t n_slots, const int32_t* tiles,
-                            const int64_t* tile_part_base, const uint32_t* masks,
-                            void* partials, const int32_t* groups, const int64_t* group_base,
-                            const int32_t* split_rows, int64_t n_groups, void* stream) {
+                            int64_t n_entries, int col_bits, const void* x, void* y,
+                            const int32_t* row_map, int64_t n_out, const int32_t* items,
+                            int64_t n_slots, const uint32_t* masks, void* partials,
+                            const int32_t* split_rows, const int32_t* split_ptr,
+                            const int32_t* slots, int64_t n_split, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
-  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_groups < 0)
+  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_split < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: negative size");
   if (n_entries > 0x7fffffffLL - kXcsItemCap || n_slots > 0x3fffffffLL ||
-      n_groups > 0x7fffffffLL)
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or groups");
+      n_split > 0x7fffffffLL - kBlock)
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or split rows");
   if (col_bits < 1 || col_bits > 24)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: col_bits outside [1, 24]");
-  if (n_slots > 0 && (!vals || !pidx || !panel_base || !x || !y || !items || !tiles ||
-                      !tile_part_base || !masks))
+  if (n_slots > 0 && (!vals || !pidx || !x || !y || !items || !masks))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null pointer");
-  if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
+  if (n_split > 0 && (!split_rows || !split_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null split-row pointer");
-  if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items) || !aligned16(tiles) ||
-      !aligned16(groups))
-    return set_error(FSP_EINVAL,
-                     "fsp_spmv_xcs: vals, pidx, items, tiles and groups must be 16-byte aligned");
+  if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items))
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: vals, pidx and items must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (row_map && n_out > 0) {
     int rc = (dtype == FSP_F32) ? fill_zero<float>(static_cast<float*>(y), n_out, st)
@@ -241,14 +321,11 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
   if (n_slots == 0) return FSP_OK;
   if (dtype == FSP_F32) {
     if (acc_f64)
-      return launch_xcs<float, double>(vals, pidx, panel_base, col_bits, x, y, row_map, items,
-                                       n_slots, tiles, tile_part_base, masks, partials, groups,
-                                       group_base, split_rows, n_groups, st);
-    return launch_xcs<float, float>(vals, pidx, panel_base, col_bits, x, y, row_map, items,
-                                    n_slots, tiles, tile_part_base, masks, partials, groups,
-                                    group_base, split_rows, n_groups, st);
+      return launch_xcs<float, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
+                                       partials, split_rows, split_ptr, slots, n_split, st);
+    return launch_xcs<float, float>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
+                                    partials, split_rows, split_ptr, slots, n_split, st);
   }
-  return launch_xcs<double, double>(vals, pidx, panel_base, col_bits, x, y, row_map, items,
-                                    n_slots, tiles, tile_part_base, masks, partials, groups,
-                                    group_base, split_rows, n_groups, st);
+  return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
+                                    partials, split_rows, split_ptr, slots, n_split, st);
 }

@@ -104,28 +104,26 @@ int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
 /*
  * y = A @ x in the XCD column-split layout (fp32/fp64 values, fp64 or native accumulation).
  *   vals, pidx   n_entries padded entries (16-byte aligned): pidx = (local row << col_bits) |
- *                (column - panel_base[panel]); every item starts on a multiple of 4
- *   panel_base   8 column offsets; col_bits in [1, 24]
+ *                (column - the panel's first column); every item starts on a multiple of 4
+ *   col_bits     in [1, 24]
  *   row_map      NULL: tile row r0 + r is y[r0 + r]; else y[row_map[r0 + r]] and y[0..n_out)
  *                is zeroed first
- *   items        n_slots slots of 8 int32 in launch order (slot j runs on XCD j / (n_slots/8)
- *                when n_slots is a multiple of 8): {entry start, count, tile, rank in tile,
- *                r0, rows, panel, 0}; tile -1 marks an empty slot
- *   tiles        4 int32 per tile: {mask word offset, split rows S, items, 0}
- *   tile_part_base  first partial slot of each tile (int64); masks: per tile W = ceil(rows/32)
- *                split words then W empty-row words
- *   partials     sum over tiles of S * items slots of 8 bytes, laid out [item rank][S]
- *   groups       split-row groups as for fsp_spmv_csr: one per tile with S > 0,
- *                {first, S, items, 0}, base = the tile's first partial slot, split_rows the
- *                tile's split rows in row order.  Calls sharing partials must not overlap.
+ *   items        n_slots slots of 12 int32 in launch order (slot j runs on XCD j / (n_slots/8)
+ *                when n_slots is a multiple of 8): {entry start, count, rank k in tile, 0, r0,
+ *                rows, panel first column, mask word offset, first partial slot as two int32
+ *                (low, high), tile (-1 marks an empty slot), 0}
+ *   masks        per tile W = ceil(rows/32) split-row words then W empty-row words
+ *   partials     one slot of 8 bytes per (item, split row it holds); an item's slots are
+ *                consecutive in row order
+ *   split_rows   n_split rows summed over several items; row split_rows[i] gets the sum of
+ *                partials[slots[j]], j in [split_ptr[i], split_ptr[i+1]) increasing (a second
+ *                launch on the same stream).  Calls sharing partials must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
-                 int64_t n_entries, const int32_t* panel_base, int col_bits, const void* x,
-                 void* y, const int32_t* row_map, int64_t n_out, const int32_t* items,
-                 int64_t n_slots, const int32_t* tiles, const int64_t* tile_part_base,
-                 const uint32_t* masks, void* partials, const int32_t* groups,
-                 const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
-                 void* stream);
+                 int64_t n_entries, int col_bits, const void* x, void* y,
+                 const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
+                 const uint32_t* masks, void* partials, const int32_t* split_rows,
+                 const int32_t* split_ptr, const int32_t* slots, int64_t n_split, void* stream);
 
 /*
  * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)

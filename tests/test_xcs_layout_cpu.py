@@ -13,82 +13,104 @@ from flagsparse_amd._spmv_layouts import XcsLayout, prefers_xcs, sample_indices
 from oracle import oracle
 
 
+def _item_positions(e0, ln):
+    """Memory positions of an item's entries in logical (row) order: thread-major storage with
+    Q = ceil(ln/4) quads, qp = ceil(Q/256) quads per thread, nt = ceil(Q/qp) threads, logical
+    quad qp*t + u at memory quad t + nt*u."""
+    q = (ln + 3) // 4
+    qp = max(1, (q + 255) // 256)
+    nt = (q + qp - 1) // qp
+    o = np.arange(ln)
+    lq = o // 4
+    return e0 + 4 * (lq // qp + nt * (lq % qp)) + o % 4
+
+
 def _emulate(layout, x, acc=np.float64):
-    """numpy restatement of spmv_xcs_kernel over the layout (every slot, then every tile)."""
-    items = layout.items.numpy().reshape(-1, 8)
-    tiles = layout.tiles.numpy()
+    """numpy restatement of spmv_xcs_kernel + xcs_split_combine_kernel over the layout."""
+    items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
     masks = layout.masks.numpy().view(np.uint32)
-    pbase = layout.tile_part_base.numpy()
     vals = layout.vals.numpy().astype(acc)
     pidx = layout.pidx.numpy().view(np.uint32)
-    cb = layout.panel_base.numpy()
     cbits = layout.col_bits
     y = np.full(layout.n_rows, np.nan)
     partials = np.full(max(layout.n_partials, 1), np.nan)
-    for e0, ln, tile, k, r0, R, panel, _ in items:
+    written = np.zeros(max(layout.n_partials, 1), dtype=bool)
+    for e0, ln, k, _, r0, R, cbase, moff, plo, phi, tile, _ in items:
         if tile < 0:
             continue
-        moff, S, n_items, _ = tiles[tile]
+        slot = (plo & 0xFFFFFFFF) | (phi << 32)
         W = (R + 31) // 32
         split = lambda r: (masks[moff + r // 32] >> (r % 32)) & 1  # noqa: E731
         empty = lambda r: (masks[moff + W + r // 32] >> (r % 32)) & 1  # noqa: E731
-        p = pidx[e0:e0 + ln]
+        pos = _item_positions(e0, ln)
+        p = pidx[pos]
         lrow = (p >> cbits).astype(np.int64)
-        col = cb[panel] + (p & ((1 << cbits) - 1)).astype(np.int64)
-        prod = vals[e0:e0 + ln] * x[col].astype(acc)
+        col = cbase + (p & ((1 << cbits) - 1)).astype(np.int64)
+        prod = vals[pos] * x[col].astype(acc)
         assert np.all(np.diff(lrow) >= 0)
-        rank = 0
         for r in range(R):
             if empty(r):
                 if k == 0:
                     y[r0 + r] = 0.0
                 continue
             sel = prod[lrow == r]
+            if not sel.size:
+                continue
             s = acc(0)
             for v in sel:
                 s = acc(s + v)
-            if split(r):
-                partials[pbase[tile] + k * S + rank] = s
-                rank += 1
-            elif sel.size:
+            if split(r):  # the item's next slot, in row order
+                assert not written[slot]
+                partials[slot] = s
+                written[slot] = True
+                slot += 1
+            else:
+                assert np.isnan(y[r0 + r])  # a direct row is written by one item only
                 y[r0 + r] = s
-    # second pass (split_row_combine_kernel): groups of split rows, partials [n][S]
-    groups = layout.groups.numpy()
-    gbase = layout.group_base.numpy()
+    assert written[:layout.n_partials].all()
+    # second pass: each split row sums its slots in the listed (item) order
     split_rows = layout.split_rows.numpy()
-    for (first, S, n, _), base in zip(groups, gbase):
-        for si in range(S):
-            s = acc(0)
-            for j in range(n):
-                s = acc(s + partials[base + j * S + si])
-            y[split_rows[first + si]] = s
+    sptr = layout.split_ptr.numpy()
+    slots = layout.slots.numpy()
+    for i, row in enumerate(split_rows):
+        s = acc(0)
+        for j in range(sptr[i], sptr[i + 1]):
+            s = acc(s + partials[slots[j]])
+        y[row] = s
     return y
 
 
 def _check_structure(layout, data, cols, rowptr):
     caps = _abi.caps()
-    items = layout.items.numpy().reshape(-1, 8)
-    real = items[items[:, 2] >= 0]
+    items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
+    real = items[items[:, 10] >= 0]
     assert np.all(real[:, 0] % 4 == 0) and np.all(real[:, 1] <= caps["xcs_item"])
     assert np.all(real[:, 5] <= layout.rows_cap)
-    # slot p*q + j runs on XCD p: every real item of XCD p's range gathers from panel p
+    # slot x*q + j runs on XCD x: every real item of XCD x's range gathers from a panel
+    # p with p % 8 == x, and the panels come one after the other
     q = layout.max_items_per_panel
-    for slot, it in enumerate(items):
-        if it[2] >= 0:
-            assert it[6] == slot // q
+    cbl = list(layout.panel_base.numpy())
+    for x in range(8):
+        seq = [it for it in items[x * q:(x + 1) * q] if it[10] >= 0]
+        panels = [max(i for i, b in enumerate(cbl) if b == it[6]) for it in seq]
+        assert all(p % 8 == x or cbl.count(cbl[p]) > 1 for p in panels)
+        assert panels == sorted(panels) or any(cbl.count(b) > 1 for b in cbl)
     # every original entry appears exactly once (multiset of (row, col, value))
     pidx = layout.pidx.numpy().view(np.uint32)
     vals = layout.vals.numpy()
     cb = layout.panel_base.numpy()
     got = []
-    for e0, ln, tile, k, r0, R, panel, _ in real:
-        p = pidx[e0:e0 + ln]
+    for e0, ln, k, S, r0, R, cbase, moff, plo, phi, tile, _ in real:
+        panel = max(i for i, b in enumerate(cb) if b == cbase)
+        pos = _item_positions(e0, ln)
+        assert pos.size == 0 or pos.max() < layout.n_entries
+        p = pidx[pos]
         lr = (p >> layout.col_bits).astype(np.int64)
         assert np.all(lr < R)
-        c = cb[panel] + (p & ((1 << layout.col_bits) - 1)).astype(np.int64)
+        c = cbase + (p & ((1 << layout.col_bits) - 1)).astype(np.int64)
         hi = cb[panel + 1] if panel + 1 < len(cb) else layout.n_cols
-        assert np.all((c >= cb[panel]) & (c < hi))
-        got += list(zip((r0 + lr).tolist(), c.tolist(), vals[e0:e0 + ln].tolist()))
+        assert np.all((c >= cbase) & (c < hi))
+        got += list(zip((r0 + lr).tolist(), c.tolist(), vals[pos].tolist()))
     rp = rowptr.numpy()
     want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
             for i in range(rp[r], rp[r + 1])]
@@ -108,13 +130,14 @@ def _case(lengths, n_cols, seed, dtype=torch.float32, unsorted=False):
     return vals, cols.to(torch.int32), ip, x
 
 
-@pytest.mark.parametrize("seed", [0, 1])
-def test_xcs_random_short_rows(seed):
+@pytest.mark.parametrize("seed,per_xcd", [(0, 1), (1, 1), (0, 2), (1, 4)])
+def test_xcs_random_short_rows(seed, per_xcd):
     rng = np.random.default_rng(seed)
     lengths = rng.zipf(2.0, 6000).clip(max=300)
     lengths[rng.integers(0, 6000, 400)] = 0
     vals, cols, ip, x = _case(lengths, 50000, seed)
-    lay = XcsLayout(vals, cols, ip, 50000)
+    lay = XcsLayout(vals, cols, ip, 50000, panels_per_xcd=per_xcd)
+    assert lay.n_panels == 8 * per_xcd
     _check_structure(lay, vals, cols, ip)
     assert lay.n_split_rows > 0
     y = _emulate(lay, x.numpy())
@@ -126,7 +149,7 @@ def test_xcs_long_rows_and_empty_tiles():
     # long rows beyond a tile (8 * item cap), item splits, a run of empty rows wider than a tile
     lengths = [3, 0, 40000, 1, 1, 2] + [0] * 9000 + [17000, 5, 0, 2048 * 3, 7]
     vals, cols, ip, x = _case(lengths, 300000, 4, unsorted=True)
-    lay = XcsLayout(vals, cols, ip, 300000)
+    lay = XcsLayout(vals, cols, ip, 300000, panels_per_xcd=2)
     _check_structure(lay, vals, cols, ip)
     y = _emulate(lay, x.numpy())
     ref = oracle.spmv_csr(ip, cols, vals, x)

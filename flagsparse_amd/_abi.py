@@ -34,8 +34,8 @@ SIGNATURES = {
     "fsp_xcs_item_cap": (_i64, []),
     "fsp_xcs_rows_cap": (_i64, []),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
-    "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _i64,
-                            _i64, _p, _p, _p, _p, _i64, _i32, _p]),
+    "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p,
+                            _i64, _i64, _p, _p, _p, _p, _i64, _i32, _p]),
     "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64, _p, _p,
                             _p, _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),

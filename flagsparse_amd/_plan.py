@@ -20,13 +20,14 @@ from . import _abi
 class RowBlockPlan:
     """A descriptor table on the device plus the partial-sum workspace its split rows need."""
 
-    __slots__ = ("desc", "desc_host", "n_desc", "n_parts", "n_split_rows", "chunk", "rows_cap",
-                 "nnz_cap", "long_threshold", "_workspaces", "_groups")
+    __slots__ = ("desc", "desc_host", "ranges", "n_desc", "n_parts", "n_split_rows", "chunk",
+                 "rows_cap", "nnz_cap", "long_threshold", "_workspaces", "_groups")
 
     def __init__(self, desc, n_parts, n_split_rows, chunk, rows_cap, nnz_cap, long_threshold,
-                 desc_host=None):
+                 desc_host=None, ranges=None):
         self.desc = desc
         self.desc_host = desc_host
+        self.ranges = ranges
         self.n_desc = int(desc.shape[0])
         self.n_parts = int(n_parts)
         self.n_split_rows = int(n_split_rows)
@@ -86,11 +87,20 @@ def build_row_block_plan(rowptr_host, device, nnz_cap, rows_cap, long_threshold,
     _abi.check(L.fsp_plan_row_blocks(*args, desc.ctypes.data_as(ctypes.c_void_p), ctypes.byref(nd),
                                      ctypes.byref(npart), ctypes.byref(nsplit)),
                "fsp_plan_row_blocks")
+    # entry range [lo, hi) of every descriptor, so kernels need not read row pointers first
+    d = desc.astype(np.int64)
+    short = d[:, 2] == 0
+    lo = np.where(short, rp[d[:, 0]], rp[d[:, 0]] + d[:, 1] * int(chunk))
+    hi = np.where(short, rp[np.where(short, d[:, 1], d[:, 0])],
+                  np.minimum(lo + int(chunk), rp[np.minimum(d[:, 0] + 1, n_rows)]))
+    ranges = np.ascontiguousarray(np.stack([lo, hi], 1), dtype=np.int64)
     desc_t = torch.from_numpy(desc)
+    ranges_t = torch.from_numpy(ranges)
     if device is not None and torch.device(device).type != "cpu":
         desc_t = desc_t.to(device)
+        ranges_t = ranges_t.to(device)
     return RowBlockPlan(desc_t, npart.value, nsplit.value, chunk, rows_cap, nnz_cap,
-                        long_threshold, desc_host=desc)
+                        long_threshold, desc_host=desc, ranges=ranges_t)
 
 
 def truncate_rows(data, indices, indptr, caps):

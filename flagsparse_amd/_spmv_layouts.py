@@ -86,8 +86,8 @@ class RowBlockLayout:
             L.fsp_spmv_csr(_abi.dtype_code(self.data.dtype), int(acc_f64), _abi.ptr(self.data),
                            _abi.ptr(self.cols), _abi.ptr(self.rowptr), self.rowptr_bits,
                            self.n_rows, self.nnz, _abi.ptr(x), _abi.ptr(y), _abi.ptr(row_map),
-                           n_out, _abi.ptr(plan.desc), plan.n_desc, plan.chunk,
-                           _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
+                           n_out, _abi.ptr(plan.desc), _abi.ptr(plan.ranges), plan.n_desc,
+                           plan.chunk, _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
                            _abi.ptr(split_rows), int(groups.shape[0]), 1,
                            _abi.stream_handle(y.device)),
             "fsp_spmv_csr")

@@ -32,8 +32,8 @@ template <typename T, typename A, typename P, bool NT>
 __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
     const T* __restrict__ vals, const int* __restrict__ cols, const P* __restrict__ rowptr,
     P nnz_total, const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
-    const i32x4* __restrict__ desc, int n_desc, P chunk, A* __restrict__ partials,
-    int xcd_remap) {
+    const i32x4* __restrict__ desc, const int64_t* __restrict__ ranges, int n_desc, P chunk,
+    A* __restrict__ partials, int xcd_remap) {
   __shared__ A s_prod[kStreamSlots];
   __shared__ P s_ptr[kStreamRows + 1];
   __shared__ A s_red[kWavesPerBlock];
@@ -42,15 +42,15 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
   int b = blockIdx.x;
   if (xcd_remap) b = xcd_logical_block(b, n_desc);
   const i32x4 d = desc[b];
+  // The descriptor's entry range [lo, hi) comes from the plan, so the entry loads do not
+  // wait for the row pointers.
+  const P lo = (P)ranges[2 * b], hi = (P)ranges[2 * b + 1];
 
   if (d.z == 0) {
     // ---------------- short-row block: rows [r0, r0 + R) ----------------
     const int r0 = d.x, R = d.y - d.x;
-    if (R <= 0 || R > kStreamRows) return;  // not a planner descriptor; uniform per block
-    for (int i = tid; i <= R; i += kBlock) s_ptr[i] = rowptr[r0 + i];
-    __syncthreads();
-    const P lo = s_ptr[0], hi = s_ptr[R];
-    if (hi - lo > P(kSpmvStreamNnzCap)) return;  // uniform per block
+    if (R <= 0 || R > kStreamRows || hi - lo > P(kSpmvStreamNnzCap) || hi < lo)
+      return;  // not a planner descriptor; uniform per block
     const P s0 = lo & ~P(3);
 
     T v[kStreamUPT][4];
@@ -65,6 +65,13 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
         for (int j = 0; j < 4; ++j) { v[u][j] = T(0); c[u][j] = -1; }
       }
     }
+    constexpr int kPtrPT = (kStreamRows + kBlock) / kBlock;  // row pointers per thread
+    P rp[kPtrPT];
+#pragma unroll
+    for (int u = 0; u < kPtrPT; ++u) {
+      const int i = tid + u * kBlock;
+      rp[u] = i <= R ? rowptr[r0 + i] : P(0);
+    }
     T xv[kStreamUPT][4];
 #pragma unroll
     for (int u = 0; u < kStreamUPT; ++u)
@@ -76,6 +83,11 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (c[u][j] >= 0) s_prod[(int)(base + j - lo)] = A(v[u][j]) * A(xv[u][j]);
+    }
+#pragma unroll
+    for (int u = 0; u < kPtrPT; ++u) {
+      const int i = tid + u * kBlock;
+      if (i <= R) s_ptr[i] = rp[u];
     }
     __syncthreads();
 
@@ -107,9 +119,7 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
 
   // ---------------- long-row chunk ----------------
   const int row = d.x, k = d.y, nch = d.z, part = d.w;
-  const P rs = rowptr[row], re = rowptr[row + 1];
-  const P lo = rs + P(k) * chunk;
-  const P hi = (lo + chunk < re) ? lo + chunk : re;
+  if (hi - lo > chunk || hi < lo) return;  // not a planner descriptor; uniform per block
   const P s0 = lo & ~P(3);
 
   T v[kChunkUPT][4];
@@ -156,9 +166,9 @@ __global__ __launch_bounds__(kBlock) void spmv_coo_atomic_kernel(
 template <typename T, typename A, typename P>
 int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
                 const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
-                int64_t n_groups, int xcd_remap, hipStream_t st) {
+                const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                void* partials, const int32_t* groups, const int64_t* group_base,
+                const int32_t* split_rows, int64_t n_groups, int xcd_remap, hipStream_t st) {
   if (row_map) {
     int rc = fill_zero<T>(static_cast<T*>(y), n_out, st);
     if (rc) return rc;
@@ -167,7 +177,7 @@ int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64
   hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, true>), dim3((unsigned)n_desc), dim3(kBlock),
                      0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
                      (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
-                     reinterpret_cast<const i32x4*>(desc), (int)n_desc, (P)chunk,
+                     reinterpret_cast<const i32x4*>(desc), ranges, (int)n_desc, (P)chunk,
                      static_cast<A*>(partials), xcd_remap);
   int rc = check_hip(hipGetLastError(), "spmv_rowblock_kernel launch");
   if (rc || n_groups == 0) return rc;
@@ -180,16 +190,16 @@ int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64
 template <typename T, typename A>
 int dispatch_ptr(int rowptr_bits, const void* vals, const int32_t* cols, const void* rowptr,
                  int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                 const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
-                 int64_t n_groups, int xcd_remap, hipStream_t st) {
+                 const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                 void* partials, const int32_t* groups, const int64_t* group_base,
+                 const int32_t* split_rows, int64_t n_groups, int xcd_remap, hipStream_t st) {
   if (rowptr_bits == 32)
-    return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
-                                  chunk, partials, groups, group_base, split_rows, n_groups,
-                                  xcd_remap, st);
-  return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, n_desc,
-                                    chunk, partials, groups, group_base, split_rows, n_groups,
-                                    xcd_remap, st);
+    return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, ranges,
+                                  n_desc, chunk, partials, groups, group_base, split_rows,
+                                  n_groups, xcd_remap, st);
+  return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, ranges,
+                                    n_desc, chunk, partials, groups, group_base, split_rows,
+                                    n_groups, xcd_remap, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -221,10 +231,10 @@ using namespace fsp;
 extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                             const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                             const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                            const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                            const int32_t* groups, const int64_t* group_base,
-                            const int32_t* split_rows, int64_t n_groups, int xcd_remap,
-                            void* stream) {
+                            const int32_t* desc, const int64_t* ranges, int64_t n_desc,
+                            int64_t chunk, void* partials, const int32_t* groups,
+                            const int64_t* group_base, const int32_t* split_rows,
+                            int64_t n_groups, int xcd_remap, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_csr: dtype");
   if (rowptr_bits != 32 && rowptr_bits != 64)
     return set_error(FSP_EINVAL, "fsp_spmv_csr: rowptr_bits must be 32 or 64");
@@ -236,7 +246,7 @@ extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int3
     return set_error(FSP_EINVAL, "fsp_spmv_csr: nnz exceeds int32 rowptr range");
   if (chunk < 1 || chunk > kSpmvChunkCap)
     return set_error(FSP_EINVAL, "fsp_spmv_csr: chunk outside [1, fsp_spmv_chunk_nnz_cap()]");
-  if (n_desc > 0 && (!rowptr || !y || !desc))
+  if (n_desc > 0 && (!rowptr || !y || !desc || !ranges))
     return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
   if (nnz > 0 && (!vals || !cols || !x)) return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
   if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
@@ -248,15 +258,15 @@ extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int3
   if (dtype == FSP_F32) {
     if (acc_f64)
       return dispatch_ptr<float, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                         desc, n_desc, chunk, partials, groups, group_base,
-                                         split_rows, n_groups, xcd_remap, st);
+                                         desc, ranges, n_desc, chunk, partials, groups,
+                                         group_base, split_rows, n_groups, xcd_remap, st);
     return dispatch_ptr<float, float>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, n_desc, chunk, partials, groups, group_base,
-                                      split_rows, n_groups, xcd_remap, st);
+                                      desc, ranges, n_desc, chunk, partials, groups,
+                                      group_base, split_rows, n_groups, xcd_remap, st);
   }
   return dispatch_ptr<double, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, n_desc, chunk, partials, groups, group_base,
-                                      split_rows, n_groups, xcd_remap, st);
+                                      desc, ranges, n_desc, chunk, partials, groups,
+                                      group_base, split_rows, n_groups, xcd_remap, st);
 }
 
 extern "C" int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows,

@@ -85,6 +85,10 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
  *   rowptr     n_rows+1 offsets, int32 (rowptr_bits=32) or int64 (64)
  *   row_map    NULL: output row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
  *   desc       n_desc descriptors from fsp_plan_row_blocks with the caps above
+ *   ranges     n_desc pairs of int64 {lo, hi}: the entry range of each descriptor (a short
+ *              block's rowptr[r0] .. rowptr[r1], or chunk k of a row: lo = rowptr[row] +
+ *              k*chunk, hi = min(lo + chunk, rowptr[row+1])), so the kernel's entry loads do
+ *              not wait for the row pointers
  *   chunk      the chunk size the plan was built with (<= fsp_spmv_chunk_nnz_cap())
  *   partials   >= n_parts slots of 8 bytes (chunk sums of split rows)
  *   groups     n_groups split-row groups, 4 int32 each {first, S, n, 0}: rows
@@ -97,9 +101,9 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
 int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                  const void* x, void* y, const int32_t* row_map, int64_t n_out,
-                 const int32_t* desc, int64_t n_desc, int64_t chunk, void* partials,
-                 const int32_t* groups, const int64_t* group_base, const int32_t* split_rows,
-                 int64_t n_groups, int xcd_remap, void* stream);
+                 const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                 void* partials, const int32_t* groups, const int64_t* group_base,
+                 const int32_t* split_rows, int64_t n_groups, int xcd_remap, void* stream);
 
 /*
  * y = A @ x in the XCD column-split layout (fp32/fp64 values, fp64 or native accumulation).

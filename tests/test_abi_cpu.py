@@ -94,6 +94,13 @@ def _check_plan(lengths, nnz_cap, rows_cap, thr, chunk):
             i += nch
     assert next_row == n
     assert n_parts == part_cursor and n_split == split_rows
+    # the entry ranges handed to the kernels: consecutive, covering [0, nnz) exactly once
+    from flagsparse_amd._plan import build_row_block_plan
+    plan = build_row_block_plan(rowptr, None, nnz_cap, rows_cap, thr, chunk)
+    rg = plan.ranges.numpy()
+    if rg.shape[0]:
+        assert rg[0, 0] == 0 and rg[-1, 1] == rowptr[-1]
+        assert np.array_equal(rg[1:, 0], rg[:-1, 1]) and np.all(rg[:, 1] >= rg[:, 0])
 
 
 @pytest.mark.parametrize("seed", range(4))
@@ -126,8 +133,8 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     L = _abi.lib()
 
     def spmv(dtype=0, bits=32, chunk=1, n_groups=0):
-        return L.fsp_spmv_csr(dtype, 0, None, None, None, bits, 0, 0, None, None, None, 0, None, 0,
-                              chunk, None, None, None, None, n_groups, 0, None)
+        return L.fsp_spmv_csr(dtype, 0, None, None, None, bits, 0, 0, None, None, None, 0, None,
+                              None, 0, chunk, None, None, None, None, n_groups, 0, None)
 
     def spmm(dtype=0, lanes=1, vec=1):
         return L.fsp_spmm_csr(dtype, 0, None, None, None, 32, 0, 0, None, 0, 0, None, 0, None, 0,

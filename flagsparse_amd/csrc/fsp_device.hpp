@@ -15,8 +15,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef double f64x2 __attribute__((ext_vector_type(2)));
 
-// Streaming loads: the matrix arrays are read exactly once per call, so they are fetched
-// with the non-temporal hint and do not displace x / B lines from L2 and the MALL.
+// Streaming loads: the matrix arrays are read exactly once per call; with NT they are fetched
+// with the non-temporal hint and do not displace x / B lines from L2 and the MALL (used where
+// x or B is held in L2 on purpose: the XCS SpMV and the SpMM kernels).
 template <bool NT, typename V>
 __device__ __forceinline__ V ld_stream(const V* p) {
   if constexpr (NT) {

@@ -174,7 +174,10 @@ int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64
     if (rc) return rc;
   }
   if (n_desc == 0) return FSP_OK;
-  hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, true>), dim3((unsigned)n_desc), dim3(kBlock),
+  // Plain (temporal) loads for the entries: measured on MI355X they stream faster here than
+  // non-temporal ones when the kernel also writes y (cfg2: 60.5 vs 63.9 us), and this
+  // layout's x reuse is local enough not to need protection in L2.
+  hipLaunchKernelGGL((spmv_rowblock_kernel<T, A, P, false>), dim3((unsigned)n_desc), dim3(kBlock),
                      0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
                      (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
                      reinterpret_cast<const i32x4*>(desc), ranges, (int)n_desc, (P)chunk,

@@ -96,7 +96,8 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
  *              partials[group_base[g] + j*S + s] (a second launch on the same stream).  For
  *              this layout every split row is its own group {g, 1, nch, 0} with base = part.
  *              Calls sharing partials must not overlap.
- *   xcd_remap  1: place consecutive descriptors on the same XCD (L2 locality of x)
+ *   xcd_remap  1: place consecutive descriptors on the same XCD (L2 locality of x); 0: hardware
+ *              order (workgroup i on XCD i % 8), the faster choice measured for this kernel
  */
 int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,

@@ -38,6 +38,13 @@ constexpr int kItemCap = (int)kXcsItemCap;
 constexpr int kRowsCap = (int)kXcsRowsCap;
 static_assert(kRowsCap % 32 == 0 && kRowsCap <= 65535, "row ids are kept as 16-bit values");
 
+// Occupancy cap.  The kernel needs about 2 KiB of LDS and 64 VGPRs, so up to 8 workgroups
+// would share a CU; measured on MI355X, 5 per CU gathers fastest (cfg3: 562 us at 5, 574 at 6
+// and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue more x requests at the XCD's
+// L2.  The launch reserves this much dynamic LDS per workgroup (unused) so that
+// floor(160 KiB / (static + reserve)) = 5.
+constexpr unsigned kXcsLdsReserve = 28u * 1024u;
+
 __device__ __forceinline__ bool mask_bit(const uint32_t* m, int r) {
   return (m[r >> 5] >> (r & 31)) & 1u;
 }
@@ -139,53 +146,36 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   if (lane == kWave - 1) next_row = wid + 1 < kWavesPerBlock ? s_first_row[wid + 1] : -1;
   if (i0 + nm >= len) next_row = -1;  // my chunk ends the item
 
-  // Local pass over the chunk.  A run (row) "ends here" when its last entry is in this chunk.
-  // Runs that start and end here are recorded at the position of their last entry; the run
-  // the chunk starts with, when it continues from before (cont), is completed after the scan
-  // with the carry.  The last piece (sum since the last run start) feeds the scan.
+  // Every run (row) whose last entry lies in this chunk is emitted by this thread: at an
+  // internal row change, or at the chunk's last entry when the next entry belongs to another
+  // row.  The chunk's first run, when it continues from before (cont), gets the carry - the
+  // sum of its entries before this chunk - from the scan below.
+  //
+  // Pass 1 (before the scan): whether a run starts here, the sum of the last run piece (the
+  // scan's input) and how many emitted runs are split rows (each takes one partial slot).
+  // Pass 2 (after it) sums the runs again and emits them.  Nothing but prod and row stays
+  // live across the scan, which keeps the register count, and with it the number of waves in
+  // flight per SIMD, up.
   const bool cont = nm > 0 && my_first == prev_row;
-  A piece = A(0);
-  A first_piece = A(0);
-  bool first_open = true;
+  const bool last_ends = nm > 0 && next_row != my_last;
   int has_head = (nm > 0 && !cont) ? 1 : 0;
-  uint32_t ends = 0;  // bit q: a recorded run ends at entry q
-  A end_sum[kPer];
+  int n_split = 0;
+  A piece = A(0);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
-    end_sum[q] = A(0);
     if (q < nm) {
-      if (q > 0 && row[q] != row[q - 1]) {  // the run of row[q - 1] ends at q - 1
-        if (first_open) {
-          first_piece = piece;
-          first_open = false;
-          if (!cont) { ends |= 1u << (q - 1); end_sum[q - 1] = piece; }
-        } else {
-          ends |= 1u << (q - 1);
-          end_sum[q - 1] = piece;
-        }
+      if (q > 0 && row[q] != row[q - 1]) {
         has_head = 1;
+        if (mask_bit(s_split, row[q - 1])) ++n_split;
         piece = A(0);
       }
       piece += prod[q];
     }
   }
-  const bool last_ends = nm > 0 && next_row != my_last;
-  if (first_open) first_piece = piece;
-  const bool first_pending = cont && (!first_open || last_ends);
-  if (last_ends && !(first_open && cont)) {
-#pragma unroll
-    for (int q = 0; q < kPer; ++q)
-      if (q == nm - 1) { ends |= 1u << q; end_sum[q] = piece; }
-  }
-  // Split runs ending here need consecutive slots: count them for the slot scan.
-  int n_split = (first_pending && mask_bit(s_split, my_first)) ? 1 : 0;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q)
-    if (((ends >> q) & 1u) && mask_bit(s_split, row[q])) ++n_split;
+  if (last_ends && mask_bit(s_split, my_last)) ++n_split;
 
-  // Workgroup scans, one barrier: segmented scan of (has_head, last piece) gives the carry -
-  // the sum of the run piece that ends just before this chunk - and a plain scan of n_split
-  // gives this thread's first slot.
+  // Workgroup scans, one barrier: segmented scan of (has_head, last piece) gives the carry,
+  // and a plain scan of n_split gives this thread's first slot.
   int h_in = has_head;
   A v_in = piece;
   int c_in = n_split;
@@ -220,7 +210,7 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   const A carry = h_ex ? v_ex : pv + v_ex;
   int next_slot = pc + c_ex;
 
-  // Emit, in row order: direct rows go to y, split rows to the item's next slot.
+  // Pass 2, in row order: direct rows go to y, split rows to the item's next slot.
   auto emit = [&](int r, A sum) {
     if (mask_bit(s_split, r)) {
       partials[sbase + next_slot] = sum;
@@ -230,10 +220,20 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
       y[row_map ? row_map[row_o] : row_o] = T(sum);
     }
   };
-  if (first_pending) emit(my_first, carry + first_piece);
+  bool first = true;
+  A run = A(0);
 #pragma unroll
-  for (int q = 0; q < kPer; ++q)
-    if ((ends >> q) & 1u) emit(row[q], end_sum[q]);
+  for (int q = 0; q < kPer; ++q) {
+    if (q < nm) {
+      if (q > 0 && row[q] != row[q - 1]) {
+        emit(row[q - 1], (first && cont) ? carry + run : run);
+        first = false;
+        run = A(0);
+      }
+      run += prod[q];
+    }
+  }
+  if (last_ends) emit(my_last, (first && cont) ? carry + run : run);
 
   // Empty rows: the tile's first item writes y = 0.
   if (k == 0) {
@@ -272,7 +272,8 @@ int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void*
                const int32_t* row_map, const int32_t* items, int64_t n_slots,
                const uint32_t* masks, void* partials, const int32_t* split_rows,
                const int32_t* split_ptr, const int32_t* slots, int64_t n_split, hipStream_t st) {
-  hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock), 0, st,
+  hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
+                     kXcsLdsReserve, st,
                      static_cast<const T*>(vals), pidx, col_bits, static_cast<const T*>(x),
                      static_cast<T*>(y), row_map, reinterpret_cast<const i32x4*>(items),
                      (int)n_slots, masks, static_cast<A*>(partials));

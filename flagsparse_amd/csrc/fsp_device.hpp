@@ -130,21 +130,39 @@ __device__ __forceinline__ int xcd_logical_block(int i, int n) {
 }
 
 // Second pass of every split-row SpMV: rows whose entries were summed by several workgroups
-// get y[row] = sum over j < n of partials[base + j*S + s], j in increasing order (a fixed
-// order, so the result does not depend on which workgroup finished first).  Group g covers S
-// rows split_rows[first .. first + S), its partials start at group_base[g] and are laid out
-// [n][S].  It runs as a separate launch on the same stream: the kernel boundary makes the
-// first pass's partials visible on every XCD, so neither pass needs a device-scope fence.
-// With reset != 0 every slot read is set back to 0, for first passes that write only the
-// slots of rows they hold.
+// get y[row] = sum over j < n of partials[base + j*S + s], in a fixed order (j increasing for
+// S > 1; for S == 1 a fixed workgroup tree), so the result does not depend on which workgroup
+// finished first.  Group g covers S rows split_rows[first .. first + S), its partials start at
+// group_base[g] and are laid out [n][S].  It runs as a separate launch on the same stream: the
+// kernel boundary makes the first pass's partials visible on every XCD, so neither pass needs
+// a device-scope fence.  With reset != 0 every slot read is set back to 0, for first passes
+// that write only the slots of rows they hold.
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
     const i32x4* __restrict__ groups, const int64_t* __restrict__ group_base,
     const int* __restrict__ split_rows, A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int reset) {
+  __shared__ A red[kWavesPerBlock];
   const i32x4 g = groups[blockIdx.x];
   const int first = g.x, S = g.y, n = g.z;
   const int64_t base = group_base[blockIdx.x];
+  if (S == 1) {
+    // One row: the workgroup sums its n partials (thread t takes t, t + 256, ... in order,
+    // then the fixed-order workgroup sum), so a row cut into many chunks is not summed by a
+    // single thread.
+    A acc = A(0);
+    for (int j = threadIdx.x; j < n; j += kBlock) {
+      A* p = &partials[base + j];
+      acc += *p;
+      if (reset) *p = A(0);
+    }
+    acc = block_sum(acc, red);
+    if (threadIdx.x == 0) {
+      const int row = split_rows[first];
+      y[row_map ? row_map[row] : row] = T(acc);
+    }
+    return;
+  }
   for (int s = threadIdx.x; s < S; s += kBlock) {
     A acc = A(0);
     for (int j = 0; j < n; ++j) {

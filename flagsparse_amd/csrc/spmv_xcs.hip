@@ -261,8 +261,21 @@ __global__ __launch_bounds__(kBlock) void xcs_split_combine_kernel(
   const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= n_split) return;
   const int a = split_ptr[i], b = split_ptr[i + 1];
+  // Eight slots per round: all slot indices, then all partials, are requested before the
+  // first is used, so a row costs two memory round trips per eight slots, not two per slot.
+  constexpr int kU = 8;
   A acc = A(0);
-  for (int j = a; j < b; ++j) acc += partials[slots[j]];
+  for (int j0 = a; j0 < b; j0 += kU) {
+    int sl[kU];
+    A pv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) sl[u] = j0 + u < b ? slots[j0 + u] : -1;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) pv[u] = sl[u] >= 0 ? partials[sl[u]] : A(0);
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (j0 + u < b) acc += pv[u];
+  }
   const int row = split_rows[i];
   y[row_map ? row_map[row] : row] = T(acc);
 }

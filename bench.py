@@ -47,6 +47,9 @@ WORKLOADS = {
     "cfg4": "COO SpMV fp32 2M x 2M, 40M uniform draws deduplicated, row-sorted, int32, U(-1,1)",
     "cfg5": "CSR SpMM A 1M x 1M, 32 nnz/row (16 in a 512-wide band + 16 uniform), B row-major "
             "1M x N, int32, U(-1,1)",
+    "coo5": "COO SpMM: cfg5's matrix as row-sorted COO (int32 row/col), B row-major 1M x N, "
+            "through flagsparse_spmm_coo (per-call row-order check, bincount row pointer and "
+            "plan inside the step, as the reference's per-call coalesce/sort)",
     "copy": "plain device copy of 1 GiB (PMC calibration kernel)",
 }
 
@@ -58,8 +61,8 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--dtype", default=None, choices=("f32", "f64"),
-                    help="value type for cfg5 (default f32)")
-    ap.add_argument("--n", type=int, default=64, help="dense columns N for cfg5")
+                    help="value type for cfg5 / coo5 (default f32)")
+    ap.add_argument("--n", type=int, default=64, help="dense columns N for cfg5 / coo5")
     ap.add_argument("--opt", action="store_true",
                     help="SpMV: use_opt=True (native accumulation) instead of the default path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -212,6 +215,57 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
     }
 
 
+def _spmm_coo_workload(dev, dtype_name, N, torch, fs, synthetic):
+    from flagsparse_amd import spmm_coo as mod
+
+    vdt = torch.float64 if dtype_name == "f64" else torch.float32
+    data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
+    row = torch.repeat_interleave(torch.arange(shape[0], device=dev, dtype=torch.int32),
+                                  (ptr[1:] - ptr[:-1]).to(torch.int64))
+    col = idx.to(torch.int32)
+    del ptr, idx
+    B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
+    C = torch.empty((shape[0], N), dtype=vdt, device=dev)
+    coo = mod._CooRowOrder(data, row, col, shape[0], shape[1])
+    kc = coo.kernel_csr()
+    v = data.element_size()
+    nnz = int(data.numel())
+    # the kernel reads the CSR view: values, int32 columns, int32 row pointers
+    nbytes = nnz * (v + 4) + (shape[0] + 1) * 4 + shape[1] * N * v + shape[0] * N * v
+    info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
+            "path": "flagsparse_spmm_coo (row-run route, fp64 accumulation for fp32)",
+            "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * N * v + shape[0] * N * v}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        n = max(1, min(nnz, int(20e6 // max(1, N))))
+        r, c, d = row[:n].cpu(), col[:n].cpu(), data[:n].cpu()
+        Bh = B.cpu()
+        n_rows = int(r[-1]) + 1
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            oracle.spmm_coo(r, c, d, Bh, n_rows)
+            passes += 1
+            secs = time.perf_counter() - t0
+            if secs >= seconds or passes >= 1000:
+                break
+        frac = n / nnz
+        return {"value": round(nbytes * frac * passes / secs / 1e9, 3), "unit": "GB/s",
+                "cores": 1, "kind": "port",
+                "sample": f"{passes} passes of the fp64 C oracle COO SpMM over the first {n} "
+                          f"entries in {secs:.1f} s; bytes scaled by the entry fraction",
+                "gflops": round(2 * n * N * passes / secs / 1e9, 3)}
+
+    return {
+        "step": lambda: fs.flagsparse_spmm_coo(data, row, col, B, shape, out=C),
+        "launch": lambda: mod._run_spmm(kc, B, C, acc_f64=True),
+        "nbytes": nbytes, "flops": 2 * nnz * N, "info": info, "cpu": cpu,
+        "dtype": dtype_name, "kernel": kc.kernel_name(),
+        "tag": f"{kc.kernel_name()}_coo5_{dtype_name}_n{N}",
+    }
+
+
 def _copy_workload(dev, torch):
     n = (1 << 30) // 4
     src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -235,6 +289,8 @@ def _build(name, args, dev, torch):
         return _spmv_coo_workload(dev, torch, fs, synthetic)
     if name == "cfg5":
         return _spmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
+    if name == "coo5":
+        return _spmm_coo_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
     return _copy_workload(dev, torch)
 
 
@@ -289,8 +345,8 @@ def main():
     if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
         cpu = w["cpu"](args.cpu_seconds)
     workload = f"{args.workload}: {WORKLOADS[args.workload]}"
-    if args.workload == "cfg5":
-        workload = f"cfg5 ({w['dtype']}, N={args.n}): {WORKLOADS['cfg5']}"
+    if args.workload in ("cfg5", "coo5"):
+        workload = f"{args.workload} ({w['dtype']}, N={args.n}): {WORKLOADS[args.workload]}"
     info, dtype, kernel, tag = dict(w["info"]), w["dtype"], w["kernel"], w["tag"]
     del w
     torch.cuda.empty_cache()

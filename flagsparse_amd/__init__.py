@@ -2,9 +2,9 @@
 
 Drop-in for the hot path of the reference package ``flagsparse`` (src/flagsparse/__init__.py):
 the names below keep the reference's signatures, defaults, return values and exceptions.
-Names of the reference that lie outside this path (gather/scatter, SpSV, SpGEMM, SDDMM, COO
-SpMM and the CuPy-backed format containers) are listed in ``__all__`` as in the reference;
-calling them raises NotImplementedError.
+Names of the reference that lie outside this path (gather/scatter, SpSV, SpGEMM, SDDMM and the
+CuPy-backed format containers) are listed in ``__all__`` as in the reference; calling them
+raises NotImplementedError.
 
     import flagsparse_amd as flagsparse
     p = flagsparse.prepare_spmv_csr(data, indices, indptr, shape)
@@ -24,6 +24,7 @@ from .spmm_csr import (
     flagsparse_spmm_csr_opt,
     prepare_spmm_csr_opt,
 )
+from .spmm_coo import flagsparse_spmm_coo
 from .spmv_coo import PreparedCoo, flagsparse_spmv_coo, prepare_spmv_coo
 from .spmv_csr import (
     PreparedCsrSpmv,
@@ -46,6 +47,7 @@ HOT_PATH_EXPORTS = (
     "flagsparse_spmv_coo_tocsr",
     "flagsparse_spmm_csr_opt",
     "flagsparse_spmm_csr",
+    "flagsparse_spmm_coo",
     "benchmark_spmm_case",
     "benchmark_spmm_opt_case",
     "comprehensive_spmm_test",
@@ -67,7 +69,6 @@ OUT_OF_SCOPE_EXPORTS = (
     "comprehensive_scatter_test",
     "flagsparse_spsv_csr",
     "flagsparse_spsv_coo",
-    "flagsparse_spmm_coo",
     "prepare_spgemm_csr",
     "flagsparse_spgemm_csr",
     "SpGEMMPrepared",

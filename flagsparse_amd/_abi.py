@@ -41,6 +41,11 @@ SIGNATURES = {
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
     "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
                             _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),
+    "fsp_spmm_coo_atomic": (_i32, [_i32, _i32, _p, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64,
+                                   _p]),
+    "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p]),
+    "fsp_plan_windows_emit": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p,
+                                     _p, _p]),
 }
 
 

@@ -24,7 +24,7 @@ class RowBlockPlan:
                  "rows_cap", "nnz_cap", "long_threshold", "_workspaces", "_groups")
 
     def __init__(self, desc, n_parts, n_split_rows, chunk, rows_cap, nnz_cap, long_threshold,
-                 desc_host=None, ranges=None):
+                 desc_host=None, ranges=None, groups=None):
         self.desc = desc
         self.desc_host = desc_host
         self.ranges = ranges
@@ -36,7 +36,7 @@ class RowBlockPlan:
         self.nnz_cap = int(nnz_cap)
         self.long_threshold = int(long_threshold)
         self._workspaces = {}
-        self._groups = None
+        self._groups = groups
 
     def workspace(self, width=1):
         """Partial-sum buffer for ``width`` values per row part, kept on the plan and reused by
@@ -101,6 +101,43 @@ def build_row_block_plan(rowptr_host, device, nnz_cap, rows_cap, long_threshold,
         ranges_t = ranges_t.to(device)
     return RowBlockPlan(desc_t, npart.value, nsplit.value, chunk, rows_cap, nnz_cap,
                         long_threshold, desc_host=desc, ranges=ranges_t)
+
+
+def build_row_block_plan_device(rowptr, nnz_cap, rows_cap, long_threshold, chunk):
+    """The row-block plan built on the device (fsp_plan_windows_count / _emit): rows cut into
+    windows of ``rows_cap`` rows, each planned like the host planner; one small device-to-host
+    copy (the three totals) between the passes.  ``rowptr`` is an int32 or int64 device
+    tensor."""
+    L = _abi.lib()
+    dev = rowptr.device
+    bits = 32 if rowptr.dtype == torch.int32 else 64
+    rp = rowptr if bits == 32 else rowptr.to(torch.int64)
+    rp = rp.contiguous()
+    n_rows = int(rp.numel()) - 1
+    args = (_abi.ptr(rp), bits, n_rows, int(nnz_cap), int(rows_cap), int(long_threshold),
+            int(chunk))
+    n_win = -(-max(n_rows, 0) // int(rows_cap))
+    stream = _abi.stream_handle(dev)
+    counts = torch.empty((3, max(n_win, 1)), dtype=torch.int64, device=dev)
+    if n_win == 0:
+        counts.zero_()
+    _abi.check(L.fsp_plan_windows_count(*args, _abi.ptr(counts), stream), "fsp_plan_windows_count")
+    # exclusive prefix sums, one contiguous 1-D scan per counter
+    incl = torch.stack([torch.cumsum(counts[k], 0) for k in range(3)])
+    offsets = (incl - counts).contiguous()
+    nd, n_parts, n_split = (int(v) for v in incl[:, -1].tolist())
+    if max(nd, n_parts) > 0x7FFFFFFF:
+        raise ValueError("row-block plan: more than 2^31-1 descriptors or partial slots")
+    desc = torch.empty((nd, 4), dtype=torch.int32, device=dev)
+    ranges = torch.empty((nd, 2), dtype=torch.int64, device=dev)
+    groups = torch.empty((n_split, 4), dtype=torch.int32, device=dev)
+    group_base = torch.empty(n_split, dtype=torch.int64, device=dev)
+    split_rows = torch.empty(n_split, dtype=torch.int32, device=dev)
+    _abi.check(L.fsp_plan_windows_emit(*args, _abi.ptr(offsets), _abi.ptr(desc), _abi.ptr(ranges),
+                                       _abi.ptr(groups), _abi.ptr(group_base),
+                                       _abi.ptr(split_rows), stream), "fsp_plan_windows_emit")
+    return RowBlockPlan(desc, n_parts, n_split, chunk, rows_cap, nnz_cap, long_threshold,
+                        ranges=ranges, groups=(groups, group_base, split_rows))
 
 
 def truncate_rows(data, indices, indptr, caps):

@@ -232,6 +232,26 @@ __global__ __launch_bounds__(kBlock) void spmm_split_combine_kernel(
   }
 }
 
+// COO SpMM with atomics (the reference's "atomic" route, spmm_coo.py:244-271, 464-523):
+// C_acc[rows[e], n] += vals[e] * B[cols[e], n] for every entry e and column n < N, in the
+// accumulation type A (fp64 for fp32 inputs, as the reference's canonical fp64 compute).
+// Thread i of the flattened (entry, column) range handles entry i / N, column i % N, so the
+// lanes of a wave walk one B row and one C row contiguously.  The order of the additions, and
+// so the last bits of C_acc, are not deterministic (as in the reference).
+template <typename T, typename A>
+__global__ __launch_bounds__(kBlock) void spmm_coo_atomic_kernel(
+    const T* __restrict__ vals, const int* __restrict__ rows, const int* __restrict__ cols,
+    int64_t total, int N, const T* __restrict__ B, int64_t ldb, A* __restrict__ C,
+    int64_t ldc) {
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += stride) {
+    const int64_t e = i / N;
+    const int n = (int)(i - e * N);
+    const A prod = A(vals[e]) * A(B[(int64_t)cols[e] * ldb + n]);
+    atomicAdd(&C[(int64_t)rows[e] * ldc + n], prod);
+  }
+}
+
 template <typename T, typename A, typename P, int VW>
 int launch_spmm(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
                 const void* B, int64_t ldb, int64_t N, void* C, int64_t ldc, const int32_t* desc,
@@ -343,4 +363,43 @@ extern "C" int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int3
   return dispatch_ptr<double, double>(rowptr_bits, vec, vals, cols, rowptr, nnz, B, ldb, N, C,
                                       ldc, desc, n_desc, chunk, lg, partials, sg, n_tiles,
                                       xcd_remap, st);
+}
+
+extern "C" int fsp_spmm_coo_atomic(int dtype, int acc_f64, const void* vals, const int32_t* rows,
+                                   const int32_t* cols, int64_t nnz, const void* B, int64_t ldb,
+                                   int64_t N, void* C_acc, int64_t ldc, int64_t n_rows,
+                                   void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64)
+    return set_error(FSP_ENOTSUP, "fsp_spmm_coo_atomic: dtype");
+  if (nnz < 0 || N < 0 || n_rows < 0) return set_error(FSP_EINVAL, "fsp_spmm_coo_atomic: negative size");
+  if (N > 0x7fffffffLL || nnz > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmm_coo_atomic: size exceeds 2^31-1");
+  if (ldc < N || ldb < N) return set_error(FSP_EINVAL, "fsp_spmm_coo_atomic: ldb/ldc smaller than N");
+  if (n_rows > 0 && ldc > 0 && !C_acc) return set_error(FSP_EINVAL, "fsp_spmm_coo_atomic: null C");
+  if (nnz > 0 && N > 0 && (!vals || !rows || !cols || !B))
+    return set_error(FSP_EINVAL, "fsp_spmm_coo_atomic: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool wide = dtype == FSP_F64 || acc_f64;
+  // C_acc[0 .. n_rows*ldc) = 0, then the atomic pass.
+  int rc = wide ? fill_zero<double>(static_cast<double*>(C_acc), n_rows * ldc, st)
+                : fill_zero<float>(static_cast<float*>(C_acc), n_rows * ldc, st);
+  if (rc) return rc;
+  const int64_t total = nnz * N;
+  if (total == 0) return FSP_OK;
+  int64_t blocks = (total + kBlock - 1) / kBlock;
+  if (blocks > 65536) blocks = 65536;  // grid-stride loop covers the rest
+  if (dtype == FSP_F32 && acc_f64)
+    hipLaunchKernelGGL((spmm_coo_atomic_kernel<float, double>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, st, static_cast<const float*>(vals), rows, cols, total,
+                       (int)N, static_cast<const float*>(B), ldb, static_cast<double*>(C_acc), ldc);
+  else if (dtype == FSP_F32)
+    hipLaunchKernelGGL((spmm_coo_atomic_kernel<float, float>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, st, static_cast<const float*>(vals), rows, cols, total,
+                       (int)N, static_cast<const float*>(B), ldb, static_cast<float*>(C_acc), ldc);
+  else
+    hipLaunchKernelGGL((spmm_coo_atomic_kernel<double, double>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, st, static_cast<const double*>(vals), rows, cols, total,
+                       (int)N, static_cast<const double*>(B), ldb, static_cast<double*>(C_acc),
+                       ldc);
+  return check_hip(hipGetLastError(), "spmm_coo_atomic_kernel launch");
 }

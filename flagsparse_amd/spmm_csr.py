@@ -26,7 +26,7 @@ from ._common import (
     _require_kernel_dtype,
     _tolerance_for_dtype,
 )
-from ._plan import build_row_block_plan, rowptr_to_host
+from ._plan import build_row_block_plan_device
 from .synthetic import build_random_csr, build_random_dense
 
 SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
@@ -291,8 +291,7 @@ def _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols=None):
 class _SpmmKernelCsr:
     """Kernel-facing CSR arrays (aligned, int32 offsets when they fit) and plans per G."""
 
-    __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_rowptr_host",
-                 "_plans")
+    __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_plans")
 
     def __init__(self, data, cols, indptr64):
         self.data = _aligned(data)
@@ -303,7 +302,6 @@ class _SpmmKernelCsr:
             self.rowptr, self.rowptr_bits = indptr64.to(torch.int32), 32
         else:
             self.rowptr, self.rowptr_bits = indptr64, 64
-        self._rowptr_host = rowptr_to_host(indptr64)
         self._plans = {}
 
     def kernel_name(self):
@@ -321,8 +319,7 @@ class _SpmmKernelCsr:
             cap = _abi.caps()["spmm_block_nnz"]
             threshold = min(_SPMM_ROW_SPLIT_THRESHOLD, cap)
             chunk = min(cap, max(threshold, 16 * ngrp))
-            p = build_row_block_plan(self._rowptr_host, self.data.device, cap, ngrp, threshold,
-                                     chunk)
+            p = build_row_block_plan_device(self.rowptr, cap, ngrp, threshold, chunk)
             self._plans[lanes] = p
         return p
 

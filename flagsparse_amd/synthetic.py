@@ -294,6 +294,20 @@ def build_random_csr(n_rows, n_cols, nnz, value_dtype, index_dtype, device, seed
     return data, indices, indptr
 
 
+def build_random_coo(n_rows, n_cols, nnz, value_dtype, index_dtype, device, seed=0):
+    """Random COO for the COO SpMM benchmark case: nnz independent uniform (row, col) draws in
+    draw order (unsorted, duplicates possible), values ~ N(0, 1).  The reference's benchmark
+    calls a ``_build_random_coo`` helper (spmm_coo.py:866) that its sources do not define;
+    this is the natural COO counterpart of its _build_random_csr (_common.py:166-181)."""
+    if nnz <= 0 or n_rows <= 0 or n_cols <= 0:
+        empty = torch.empty(0, dtype=index_dtype, device=device)
+        return torch.empty(0, dtype=value_dtype, device=device), empty, empty.clone()
+    row = randint(seed, 73, nnz, n_rows, device).to(index_dtype)
+    col = randint(seed, 74, nnz, n_cols, device).to(index_dtype)
+    data = normal_values(seed, 75, nnz, value_dtype, device)
+    return data, row, col
+
+
 def build_random_dense(size, value_dtype, device, seed=0, stream=80):
     """Seeded counterpart of _build_random_dense (_common.py:149-157): N(0, 1) values."""
     shape = (size,) if isinstance(size, int) else tuple(size)

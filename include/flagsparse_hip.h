@@ -2,8 +2,8 @@
  * flagsparse_hip.h - C ABI of the MI355X (gfx950) CSR/COO SpMV and CSR SpMM library.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t passed as void*.
- * Nothing here allocates device memory: workspaces (partials, tickets, descriptor tables)
- * are owned by the caller, which sizes them from the plan functions below.
+ * Nothing here allocates device memory: workspaces (partial sums, descriptor tables) are
+ * owned by the caller, which sizes them from the plan functions below.
  * Every function returns 0 on success or a negative fsp_status; fsp_last_error() then
  * holds a message for the calling thread.  No C++ exception crosses this boundary.
  *
@@ -13,6 +13,9 @@
  *                          and spmm_csr.py:417-477 (_build_spmm_opt_split_metadata,
  *                          _build_spmm_opt_buckets); one descriptor table replaces the
  *                          per-bucket row lists.
+ *   fsp_plan_windows_count / fsp_plan_windows_emit
+ *                        - the same planning on the device (spmm_csr.py:417-477, the host
+ *                          Python loop over long rows included), for per-call plans.
  *   fsp_spmv_csr         - the Triton launches of spmv_csr.py:329-376
  *                          (_triton_spmv_csr_impl_opt_prepared, use_opt=True) and
  *                          spmv_csr.py:510-536 (_triton_spmv_csr_impl_prepared, default
@@ -25,7 +28,9 @@
  *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
  *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
  *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
- *                          long-row split).
+ *                          long-row split); for row-sorted COO also the row-run launch of
+ *                          spmm_coo.py:394-461 (_triton_spmm_coo_rowrun_impl).
+ *   fsp_spmm_coo_atomic  - spmm_coo.py:464-523 (_triton_spmm_coo_atomic_impl).
  */
 #ifndef FLAGSPARSE_HIP_H
 #define FLAGSPARSE_HIP_H
@@ -76,6 +81,33 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
                         int64_t rows_cap, int64_t long_threshold, int64_t chunk,
                         int32_t* desc_out, int64_t* n_desc, int64_t* n_parts,
                         int64_t* n_split_rows);
+
+/*
+ * The same plan built on the device in two passes (no host copy of rowptr, no host loop):
+ * the rows are cut into windows of rows_cap rows and each window is planned with the rules of
+ * fsp_plan_row_blocks, except that no block crosses a window boundary.  Replaces the host loop
+ * of spmm_csr.py:417-441 (_build_spmm_opt_split_metadata) and the bucket lists of :444-477 on
+ * the paths that plan on every call.
+ *   rowptr         device row pointers, int32 (rowptr_bits 32) or int64 (64), n_rows + 1
+ *   counts         pass 1 output, device int64 [3][n_win], n_win = ceil(n_rows / rows_cap):
+ *                  per window the number of descriptors, partial slots and split rows
+ *   offsets        pass 2 input: the exclusive prefix sum of each of the three rows of counts
+ *   desc           [n_desc] int32 quadruples, as fsp_plan_row_blocks writes them
+ *   ranges         optional [n_desc][2] int64 entry ranges {lo, hi} (as fsp_spmv_csr takes)
+ *   groups, group_base, split_rows
+ *                  one combine group per split row, {s, 1, nch, 0} / first part / row (the
+ *                  fsp_spmv_csr / fsp_spmm_csr group format); sized by pass 1's totals
+ * Both passes are asynchronous on stream; the caller reads the totals (one small copy) between
+ * them to size the tables.
+ */
+int fsp_plan_windows_count(const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz_cap,
+                           int64_t rows_cap, int64_t long_threshold, int64_t chunk,
+                           int64_t* counts, void* stream);
+int fsp_plan_windows_emit(const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz_cap,
+                          int64_t rows_cap, int64_t long_threshold, int64_t chunk,
+                          const int64_t* offsets, int32_t* desc, int64_t* ranges,
+                          int32_t* groups, int64_t* group_base, int32_t* split_rows,
+                          void* stream);
 
 /*
  * y = A @ x for CSR A (or COO row runs when row_map != NULL).
@@ -156,6 +188,20 @@ int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const int32_t* desc, int64_t n_desc, int64_t chunk, int lanes_per_row,
                  int vec, void* partials, const int32_t* groups, const int64_t* group_base,
                  const int32_t* split_rows, int64_t n_groups, int xcd_remap, void* stream);
+
+/*
+ * COO SpMM with atomics: C_acc[rows[e], n] += vals[e] * B[cols[e], n] for every entry e and
+ * n < N.  Replaces the reference's atomic route, spmm_coo.py:244-271 (_spmm_coo_atomic_real_
+ * kernel) and :464-523 (_triton_spmm_coo_atomic_impl).  C_acc[0 .. n_rows*ldc) is zeroed first;
+ * it holds fp64 when dtype is FSP_F64 or acc_f64 != 0 (the reference computes fp32 inputs in
+ * fp64), else fp32, and the caller rounds it to the output dtype.  The addition order, and so
+ * the last bits of C_acc, are not deterministic.  The row-run route (flagsparse_spmm_coo's
+ * default) needs no entry point of its own: row-ordered entries with their row pointer are CSR,
+ * and go through fsp_spmm_csr.
+ */
+int fsp_spmm_coo_atomic(int dtype, int acc_f64, const void* vals, const int32_t* rows,
+                        const int32_t* cols, int64_t nnz, const void* B, int64_t ldb, int64_t N,
+                        void* C_acc, int64_t ldc, int64_t n_rows, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,3 +65,22 @@ void oracle_spmm_csr_f64(int64_t n_rows, const int64_t* rowptr, const int64_t* c
     }
   }
 }
+
+/*
+ * C = A @ B for COO entries in the given order, row-major B[., ldb] and C[n_rows, ldc]:
+ * C[0..n_rows) = 0, then C[rows[i], n] += vals[i] * B[cols[i], n] for n < N, fp64.  Follows
+ * spmm_coo.py:136-180 (row-run kernel over the lexicographically sorted, coalesced entries;
+ * rows without a run keep 0 from C = zeros at spmm_coo.py:414) and its fp64 torch.sparse
+ * reference (spmm_coo.py:697-713): duplicates of one (row, col) are summed.
+ */
+void oracle_spmm_coo_f64(int64_t nnz, const int64_t* rows, const int64_t* cols,
+                         const double* vals, const double* B, int64_t ldb, int64_t N,
+                         int64_t n_rows, double* C, int64_t ldc) {
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t n = 0; n < N; ++n) C[r * ldc + n] = 0.0;
+  for (int64_t i = 0; i < nnz; ++i) {
+    double* c = C + rows[i] * ldc;
+    const double* b = B + cols[i] * ldb;
+    for (int64_t n = 0; n < N; ++n) c[n] += vals[i] * b[n];
+  }
+}

@@ -7,10 +7,10 @@ TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and bench.py
 Two kinds of restatement live here, each citing the FlagSparse source it follows (paths
 relative to ``src/flagsparse/sparse_operations/`` unless stated):
 
-* fp64 arithmetic (``spmv_csr``, ``spmv_coo``, ``spmm_csr``): thin ctypes wrappers over
-  ``fsp_oracle.c``, a plain row-by-row fp64 sum - the definition of correctness every
-  reference test of this path uses (tests/test_spmv.py:143-174, tests/test_spmv_coo.py:56-71,
-  tests/test_spmm.py:270-311).
+* fp64 arithmetic (``spmv_csr``, ``spmv_coo``, ``spmm_csr``, ``spmm_coo``): thin ctypes
+  wrappers over ``fsp_oracle.c``, a plain row-by-row fp64 sum - the definition of correctness
+  every reference test of this path uses (tests/test_spmv.py:143-174,
+  tests/test_spmv_coo.py:56-71, tests/test_spmm.py:270-311, tests/test_spmm_coo.py:98-140).
 * integer planning semantics that change results or observable attributes: the SpMV
   ``block_nnz`` doubling, the ``max_segments`` row truncation of both SpMV paths, the SpMM
   ALG1 launch table and its ``max_segments`` ValueError, the SpMM opt buckets and split
@@ -53,6 +53,8 @@ def _load():
         lib.oracle_spmv_coo_f64.restype = None
         lib.oracle_spmm_csr_f64.argtypes = [i64, p, p, p, p, i64, i64, p, i64]
         lib.oracle_spmm_csr_f64.restype = None
+        lib.oracle_spmm_coo_f64.argtypes = [i64, p, p, p, p, i64, i64, i64, p, i64]
+        lib.oracle_spmm_coo_f64.restype = None
         _lib = lib
     return _lib
 
@@ -116,6 +118,21 @@ def spmm_csr(indptr, indices, data, B):
     C = np.zeros((max(n_rows, 0), N), dtype=np.float64)
     if n_rows > 0 and N > 0:
         _load().oracle_spmm_csr_f64(n_rows, _ptr(ip), _ptr(ix), _ptr(dv), _ptr(Bv), N, N,
+                                    _ptr(C), N)
+    return C
+
+
+def spmm_coo(row, col, data, B, n_rows):
+    """fp64 C = A @ B for COO entries (any order, duplicates summed), row-major B
+    (oracle_spmm_coo_f64)."""
+    r = _np(row, np.int64)
+    c = _np(col, np.int64)
+    dv = _np(data, np.float64)
+    Bv = _np(B, np.float64)
+    N = Bv.shape[1] if Bv.ndim == 2 else 0
+    C = np.zeros((n_rows, N), dtype=np.float64)
+    if n_rows > 0 and N > 0 and r.size > 0:
+        _load().oracle_spmm_coo_f64(r.size, _ptr(r), _ptr(c), _ptr(dv), _ptr(Bv), N, N, n_rows,
                                     _ptr(C), N)
     return C
 

@@ -15,6 +15,11 @@ Cases:
   longrow_spmm_f32 the reference's long-row API case shape (tests/test_spmm.py:383-395):
                    (2, 2048), a 1536-entry row and a 4-entry row, N = 48
   coo_dups_f32     unsorted COO with repeated (row, col) pairs and empty rows
+  coo_spmm_ref_f32/f64
+                   the reference's duplicate/unsorted COO SpMM case (tests/test_spmm_coo.py:
+                   497-503: shape (4, 6), its fixed row/col lists, N = 48), seeded values
+  coo_spmm_dups_f32/f64
+                   unsorted COO with repeated (row, col) pairs and empty rows @ B, N = 24
   spmm_f32/f64_N   small CSR @ B for N in {1, 3, 4, 16, 64}
 
 Run from the repository root:  python tests/golden/make_golden.py
@@ -89,6 +94,30 @@ def main():
                       shape=(n_rows, n_cols)) @ _np(x).astype(np.float64)
     _save("coo_dups_f32", data=_np(vals), row=_np(row).astype(np.int32),
           col=_np(col).astype(np.int32), x=_np(x), shape=np.array([n_rows, n_cols]), y=y)
+
+    # COO SpMM: the reference's duplicate/unsorted case and a larger unsorted one
+    for dtype, tag in ((torch.float32, "f32"), (torch.float64, "f64")):
+        row = torch.tensor([2, 0, 2, 1, 2, 0, 3, 2], dtype=torch.int32)
+        col = torch.tensor([1, 4, 1, 3, 0, 4, 2, 5], dtype=torch.int32)
+        vals = synthetic.uniform_values(5, 1, row.numel(), dtype, "cpu")
+        B = synthetic.dense_uniform(6, 48, dtype, seed=5)
+        C = sp.coo_matrix((_np(vals).astype(np.float64), (_np(row), _np(col))),
+                          shape=(4, 6)) @ _np(B).astype(np.float64)
+        _save(f"coo_spmm_ref_{tag}", data=_np(vals), row=_np(row), col=_np(col), B=_np(B),
+              shape=np.array([4, 6], dtype=np.int64), C=C)
+
+        n_rows, n_cols, nnz = 500, 400, 4000
+        row = synthetic.randint(6, 1, nnz, n_rows - 50, "cpu")  # rows >= 450 stay empty
+        col = synthetic.randint(6, 2, nnz, n_cols, "cpu")
+        row[:200] = row[200:400]
+        col[:200] = col[200:400]
+        vals = synthetic.uniform_values(6, 3, nnz, dtype, "cpu")
+        B = synthetic.dense_uniform(n_cols, 24, dtype, seed=6)
+        C = sp.coo_matrix((_np(vals).astype(np.float64), (_np(row), _np(col))),
+                          shape=(n_rows, n_cols)) @ _np(B).astype(np.float64)
+        _save(f"coo_spmm_dups_{tag}", data=_np(vals), row=_np(row).astype(np.int32),
+              col=_np(col).astype(np.int32), B=_np(B),
+              shape=np.array([n_rows, n_cols], dtype=np.int64), C=C)
 
     # small SpMM
     for dtype, tag in ((torch.float32, "f32"), (torch.float64, "f64")):

@@ -129,6 +129,19 @@ def test_planner_rejects_bad_arguments():
     assert rc == -1
 
 
+def test_device_planner_rejects_bad_arguments():
+    L = _abi.lib()
+    # (rowptr, bits, n_rows, nnz_cap, rows_cap, long_threshold, chunk, counts, stream)
+    assert L.fsp_plan_windows_count(None, 16, 0, 10, 4, 5, 5, None, None) == -1
+    assert b"rowptr_bits" in L.fsp_last_error()
+    assert L.fsp_plan_windows_count(None, 32, 0, 10, 4, 11, 5, None, None) == -1
+    assert b"long_threshold" in L.fsp_last_error()
+    assert L.fsp_plan_windows_count(None, 32, 3, 10, 4, 5, 5, None, None) == -1  # null rowptr
+    assert L.fsp_plan_windows_emit(None, 64, -1, 10, 4, 5, 5, None, None, None, None, None,
+                                   None, None) == -1
+    assert L.fsp_plan_windows_count(None, 32, 0, 10, 4, 5, 5, None, None) == 0  # nothing to do
+
+
 def test_kernel_entry_points_reject_before_any_hip_call():
     L = _abi.lib()
 

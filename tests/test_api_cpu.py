@@ -4,7 +4,8 @@ touches the device (argument types, shapes, knobs, CPU tensors).
 
 Reference: src/flagsparse/__init__.py:5-63 (names), sparse_operations/spmv_csr.py:379-452,
 455, 557-569, 650, 687-700; spmv_coo.py:182-225, 284-297; spmm_csr.py:197-281, 480,
-1057-1080, 1129-1160 (signatures and checks).
+1057-1080, 1129-1160; spmm_coo.py:312-371, 626-694, 848-862, 1146-1158 (signatures and
+checks).
 """
 
 import inspect
@@ -62,17 +63,40 @@ REFERENCE_SIGNATURES = {
                                 ("index_dtype", torch.int32), ("warmup", 20), ("iters", 200),
                                 ("block_n", None), ("block_nnz", None), ("max_segments", None),
                                 ("run_cusparse", True)],
+    "flagsparse_spmm_coo": [("data", None), ("row", None), ("col", None), ("B", None),
+                            ("shape", None), ("block_n", None), ("block_nnz", 256), ("out", None),
+                            ("return_time", False)],
+    "spmm_coo.benchmark_spmm_coo_case": [
+        ("n_rows", 4096), ("n_cols", 4096), ("nnz", 65536), ("n_dense_cols", 32),
+        ("value_dtype", torch.float32), ("index_dtype", torch.int32), ("warmup", 20),
+        ("iters", 200), ("block_n", None), ("block_nnz", 256), ("run_cusparse", True),
+        ("route", "rowrun"), ("compare_routes", False)],
+    "spmm_coo.comprehensive_spmm_coo_test": [
+        ("n_rows", 4096), ("n_cols", 4096), ("nnz", 65536), ("n_dense_cols", 32),
+        ("dtype", torch.float32), ("index_dtype", torch.int32), ("warmup", 20), ("iters", 200),
+        ("block_n", None), ("block_nnz", 256), ("run_cusparse", True)],
 }
 # Parameters without a default in the reference (positional-required).
 REQUIRED = {
     "prepare_spmv_csr": 4, "prepare_spmv_coo_tocsr": 4, "prepare_spmv_coo": 4,
-    "prepare_spmm_csr_opt": 4, "flagsparse_spmm_csr": 5,
+    "prepare_spmm_csr_opt": 4, "flagsparse_spmm_csr": 5, "flagsparse_spmm_coo": 5,
 }
+
+
+def _resolve(name):
+    """``fs.<name>``, or ``flagsparse_amd.<module>.<name>`` for the benchmark cases that the
+    reference reaches through its sparse_operations modules."""
+    if "." in name:
+        import importlib
+
+        mod, attr = name.split(".")
+        return getattr(importlib.import_module(f"flagsparse_amd.{mod}"), attr)
+    return getattr(fs, name)
 
 
 @pytest.mark.parametrize("name", sorted(REFERENCE_SIGNATURES))
 def test_signature_matches_reference(name):
-    params = list(inspect.signature(getattr(fs, name)).parameters.values())
+    params = list(inspect.signature(_resolve(name)).parameters.values())
     want = REFERENCE_SIGNATURES[name]
     # same parameters in the same order; trailing additions must be optional keywords
     assert [p.name for p in params[:len(want)]] == [w[0] for w in want]
@@ -180,6 +204,39 @@ def test_spmm_host_validation():
         fs.flagsparse_spmm_csr_opt(B=B, prepared=object())
     with pytest.raises(ValueError, match="required"):
         fs.flagsparse_spmm_csr_opt(B=B)
+
+
+def test_spmm_coo_host_validation():
+    # the reference's API negative cases that fail before the device is touched
+    # (tests/test_spmm_coo.py:956-969; spmm_coo.py:312-336, 655-660)
+    data = torch.tensor([1.0, 2.0, 3.0])
+    row = torch.tensor([0, 0, 1], dtype=torch.int32)
+    col = torch.tensor([0, 1, 1], dtype=torch.int32)
+    B = torch.ones(2, 4)
+    for kw in ({"block_n": 0}, {"block_nnz": 0}):
+        with pytest.raises(ValueError, match="positive"):
+            fs.flagsparse_spmm_coo(data, row, col, B, (2, 2), **kw)
+    with pytest.raises(ValueError, match="2-tuple"):
+        fs.flagsparse_spmm_coo(data, row, col, B, (2,))
+    with pytest.raises(ValueError, match="2D"):
+        fs.flagsparse_spmm_coo(data, row, col, B[0], (2, 2))
+    with pytest.raises(ValueError, match="same length"):
+        fs.flagsparse_spmm_coo(data, row[:-1], col, B, (2, 2))
+    with pytest.raises(ValueError, match="same length"):
+        fs.flagsparse_spmm_coo(data, row, col[:-1], B, (2, 2))
+    with pytest.raises(ValueError, match="n_cols=2"):
+        fs.flagsparse_spmm_coo(data, row, col, torch.ones(3, 4), (2, 2))
+    with pytest.raises(ValueError, match="non-negative"):
+        fs.flagsparse_spmm_coo(data, row, col, torch.ones(0, 4), (-1, 0))
+    with pytest.raises(ValueError, match="CUDA"):
+        fs.flagsparse_spmm_coo(data, row, col, B, (2, 2))
+    from flagsparse_amd import spmm_coo
+
+    with pytest.raises(ValueError, match="route"):
+        spmm_coo._normalize_spmm_coo_route("csr")
+    cfg = spmm_coo._resolve_spmm_coo_launch_config(48, 1000)
+    assert (cfg["block_n"], cfg["block_nnz"], cfg["required_nnz_tiles"]) == (64, 256, 4)
+    assert (cfg["heuristic_warp_size"], cfg["heuristic_factor"]) == (32, 2)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

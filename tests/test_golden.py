@@ -20,6 +20,8 @@ from oracle import oracle
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 CSR_CASES = ["cfg1_csr_f32", "poisson64_f64", "ragged_f32", "ragged_f64"]
 SPMM_CASES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(HERE, "spmm_*.npz")))
+COO_SPMM_CASES = ["coo_spmm_ref_f32", "coo_spmm_ref_f64", "coo_spmm_dups_f32",
+                  "coo_spmm_dups_f64"]
 
 
 def _load(name):
@@ -29,7 +31,7 @@ def _load(name):
 
 def test_fixture_inventory():
     assert len(SPMM_CASES) == 10
-    for name in CSR_CASES + ["coo_dups_f32", "longrow_spmm_f32"]:
+    for name in CSR_CASES + ["coo_dups_f32", "longrow_spmm_f32"] + COO_SPMM_CASES:
         assert os.path.exists(os.path.join(HERE, name + ".npz"))
 
 
@@ -51,6 +53,13 @@ def test_oracle_spmv_coo_on_fixture():
 def test_oracle_spmm_on_fixture(name):
     g = _load(name)
     C = oracle.spmm_csr(g["indptr"], g["indices"], g["data"], g["B"])
+    np.testing.assert_allclose(C, g["C"], rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("name", COO_SPMM_CASES)
+def test_oracle_spmm_coo_on_fixture(name):
+    g = _load(name)
+    C = oracle.spmm_coo(g["row"], g["col"], g["data"], g["B"], int(g["shape"][0]))
     np.testing.assert_allclose(C, g["C"], rtol=1e-12, atol=1e-12)
 
 
@@ -122,4 +131,18 @@ def test_gpu_spmm_fixture(dev, name):
     C = fs.flagsparse_spmm_csr(t["data"], t["indices"], t["indptr"], t["B"], shape)
     _check(C, g["C"])
     C = fs.flagsparse_spmm_csr_opt(t["data"], t["indices"], t["indptr"], t["B"], shape)
+    _check(C, g["C"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", COO_SPMM_CASES)
+@pytest.mark.parametrize("route", ["rowrun", "atomic"])
+def test_gpu_spmm_coo_fixture(dev, name, route):
+    from flagsparse_amd import spmm_coo
+
+    g = _load(name)
+    t = {k: torch.from_numpy(g[k]).to(dev) for k in ("data", "row", "col", "B")}
+    shape = tuple(int(v) for v in g["shape"])
+    print(f"fixture {name} route={route}", flush=True)
+    C = spmm_coo._run_spmm_coo_route(t["data"], t["row"], t["col"], t["B"], shape, route=route)
     _check(C, g["C"])

@@ -1,0 +1,105 @@
+"""The device row-block planner (fsp_plan_windows_count / _emit) on the GPU.
+
+Its contract: the rows are cut into windows of rows_cap rows and each window is planned with
+the host planner's rules (fsp_plan_row_blocks).  So the device table must equal, exactly, the
+concatenation of host-planner tables of the windows (row ids and partial-slot bases shifted),
+and its entry ranges and combine groups must match the descriptors.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from flagsparse_amd import _abi
+from flagsparse_amd._plan import build_row_block_plan_device
+
+pytestmark = pytest.mark.gpu
+
+CAPS = [(2045, 16, 128, 2045), (2045, 64, 128, 1024), (2045, 256, 128, 256),
+        (2045, 1024, 2045, 4093), (100, 7, 50, 33), (1, 1, 1, 1)]
+
+
+def _host_plan(rowptr, nnz_cap, rows_cap, thr, chunk):
+    L = _abi.lib()
+    rp = np.ascontiguousarray(rowptr, dtype=np.int64)
+    nd, npart, nsplit = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    args = (rp.ctypes.data_as(ctypes.c_void_p), rp.size - 1, nnz_cap, rows_cap, thr, chunk)
+    assert L.fsp_plan_row_blocks(*args, None, ctypes.byref(nd), ctypes.byref(npart),
+                                 ctypes.byref(nsplit)) == 0
+    desc = np.zeros((nd.value, 4), dtype=np.int64)
+    d32 = np.zeros((nd.value, 4), dtype=np.int32)
+    assert L.fsp_plan_row_blocks(*args, d32.ctypes.data_as(ctypes.c_void_p), ctypes.byref(nd),
+                                 ctypes.byref(npart), ctypes.byref(nsplit)) == 0
+    desc[:] = d32
+    return desc, npart.value, nsplit.value
+
+
+def _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk):
+    n = rowptr.size - 1
+    tables, parts, splits = [], 0, 0
+    for w0 in range(0, n, rows_cap):
+        w1 = min(w0 + rows_cap, n)
+        desc, np_w, ns_w = _host_plan(rowptr[w0:w1 + 1] - rowptr[w0], nnz_cap, rows_cap, thr,
+                                      chunk)
+        short = desc[:, 2] == 0
+        desc[:, 0] += w0
+        desc[short, 1] += w0
+        split = (~short) & (desc[:, 3] >= 0)
+        desc[split, 3] += parts
+        tables.append(desc)
+        parts += np_w
+        splits += ns_w
+    desc = np.concatenate(tables) if tables else np.zeros((0, 4), dtype=np.int64)
+    return desc, parts, splits
+
+
+def _lengths(seed, n):
+    rng = np.random.default_rng(seed)
+    lengths = rng.zipf(1.7, n).clip(max=30000) - 1 + (rng.random(n) < 0.2)
+    lengths[rng.integers(0, n, max(1, n // 60))] = 0
+    return lengths.astype(np.int64)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("caps", CAPS)
+@pytest.mark.parametrize("bits", [32, 64])
+def test_device_plan_matches_windowed_host_plan(dev, seed, caps, bits):
+    nnz_cap, rows_cap, thr, chunk = caps
+    lengths = _lengths(seed, 3000)
+    rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    rp_dev = torch.from_numpy(rowptr).to(dev).to(torch.int32 if bits == 32 else torch.int64)
+    print(f"device plan seed={seed} caps={caps} bits={bits}", flush=True)
+    plan = build_row_block_plan_device(rp_dev, nnz_cap, rows_cap, thr, chunk)
+    want, parts, splits = _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk)
+    got = plan.desc.cpu().numpy().astype(np.int64)
+    assert np.array_equal(got, want)
+    assert (plan.n_parts, plan.n_split_rows) == (parts, splits)
+    # entry ranges
+    rg = plan.ranges.cpu().numpy()
+    short = want[:, 2] == 0
+    lo = np.where(short, rowptr[want[:, 0]], rowptr[want[:, 0]] + want[:, 1] * chunk)
+    hi = np.where(short, rowptr[np.where(short, want[:, 1], want[:, 0])],
+                  np.minimum(lo + chunk, rowptr[np.minimum(want[:, 0] + 1, lengths.size)]))
+    assert np.array_equal(rg[:, 0], lo) and np.array_equal(rg[:, 1], hi)
+    # combine groups: one per split row, in row order, {s, 1, nch, 0} / first part / row
+    groups, base, rows = (t.cpu().numpy() for t in plan.split_groups())
+    first = (~short) & (want[:, 3] >= 0) & (want[:, 1] == 0)
+    assert np.array_equal(rows, want[first, 0])
+    assert np.array_equal(base, want[first, 3])
+    assert np.array_equal(groups[:, 0], np.arange(rows.size))
+    assert np.all(groups[:, 1] == 1) and np.array_equal(groups[:, 2], want[first, 2])
+
+
+def test_device_plan_edges(dev):
+    for lengths in (np.zeros(0, np.int64), np.zeros(5000, np.int64),
+                    np.array([2045, 2046, 4093, 4094, 1, 0], np.int64),
+                    np.array([200000], np.int64)):
+        rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+        rp_dev = torch.from_numpy(rowptr).to(dev)
+        for caps in ((2045, 16, 128, 2045), (2045, 1024, 2045, 4093)):
+            plan = build_row_block_plan_device(rp_dev, *caps)
+            want, parts, splits = _windowed_expectation(rowptr, *caps)
+            assert np.array_equal(plan.desc.cpu().numpy().astype(np.int64), want)
+            assert (plan.n_parts, plan.n_split_rows) == (parts, splits)

@@ -4,8 +4,9 @@ The reference ships no golden vectors for this path (its tests draw unseeded inp
 against fp64 torch.sparse / cuSPARSE), so every oracle function is pinned here by something
 other than a retyped formula:
 
-  spmv_csr, spmv_coo, spmm_csr     scipy.sparse (an independent CSR/COO implementation), exact
-                                   integer arithmetic, Poisson closed forms, unit vectors
+  spmv_csr, spmv_coo, spmm_csr,    scipy.sparse (an independent CSR/COO implementation), exact
+  spmm_coo                         integer arithmetic, Poisson closed forms, unit vectors,
+                                   identity / permutation matrices
   spmv_csr(row_cap=...)            a loop-by-loop emulation of the reference's tile loops
                                    (spmv_csr.py:106-118, 176-190, 240-250) on a dense copy
   spmv_prepare_knobs               brute-force search over block_nnz doublings + known answers
@@ -185,6 +186,37 @@ def test_spmm_csr_edge_shapes():
     C = oracle.spmm_csr(np.array([0, 2, 3]), np.array([0, 1, 1]), np.array([1.0, 2.0, 3.0]),
                         np.empty((2, 0)))
     assert C.shape == (2, 0)
+
+
+@pytest.mark.parametrize("N", [1, 5, 32])
+def test_spmm_coo_matches_scipy(N):
+    # unsorted entries, repeated (row, col) pairs, rows without entries
+    rng = np.random.default_rng(100 + N)
+    n_rows, n_cols, nnz = 150, 120, 1800
+    row = rng.integers(0, n_rows - 20, nnz)
+    col = rng.integers(0, n_cols, nnz)
+    row[:100], col[:100] = row[100:200], col[100:200]
+    vals = rng.standard_normal(nnz)
+    B = rng.standard_normal((n_cols, N))
+    ref = sp.coo_matrix((vals, (row, col)), shape=(n_rows, n_cols)) @ B
+    C = oracle.spmm_coo(row, col, vals, B, n_rows)
+    np.testing.assert_allclose(C, ref, rtol=1e-13, atol=1e-13)
+    assert np.all(C[n_rows - 20:] == 0.0)
+
+
+def test_spmm_coo_permutation_and_edges():
+    # A = a permutation matrix in shuffled entry order: C = B[perm], exactly
+    rng = np.random.default_rng(7)
+    perm = rng.permutation(40)
+    order = rng.permutation(40)
+    B = rng.standard_normal((40, 6))
+    C = oracle.spmm_coo(np.arange(40)[order], perm[order], np.ones(40), B, 40)
+    assert np.array_equal(C, B[perm])
+    # a duplicated entry counts twice; an empty matrix / N = 0 give zeros of the right shape
+    C = oracle.spmm_coo([1, 1], [0, 0], [2.0, 3.0], np.array([[1.0, -2.0]]), 3)
+    assert C.tolist() == [[0.0, 0.0], [5.0, -10.0], [0.0, 0.0]]
+    assert oracle.spmm_coo([], [], [], np.ones((4, 3)), 2).tolist() == [[0.0] * 3] * 2
+    assert oracle.spmm_coo([0], [0], [1.0], np.empty((1, 0)), 2).shape == (2, 0)
 
 
 # ------------------------------------------------------------------------------------------

@@ -50,6 +50,8 @@ WORKLOADS = {
     "coo5": "COO SpMM: cfg5's matrix as row-sorted COO (int32 row/col), B row-major 1M x N, "
             "through flagsparse_spmm_coo (per-call row-order check, bincount row pointer and "
             "plan inside the step, as the reference's per-call coalesce/sort)",
+    "sddmm": "CSR SDDMM on cfg5's pattern (1M x 1M, 32 nnz/row), x [1M, K] and y [1M, K] "
+             "row-major ~U(-1,1), alpha 1, beta 0, fp32 accumulation (the reference's baseline)",
     "copy": "plain device copy of 1 GiB (PMC calibration kernel)",
 }
 
@@ -61,8 +63,9 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
     ap.add_argument("--dtype", default=None, choices=("f32", "f64"),
-                    help="value type for cfg5 / coo5 (default f32)")
-    ap.add_argument("--n", type=int, default=64, help="dense columns N for cfg5 / coo5")
+                    help="value type for cfg5 / coo5 / sddmm (default f32)")
+    ap.add_argument("--n", type=int, default=64,
+                    help="dense columns N for cfg5 / coo5, K for sddmm")
     ap.add_argument("--opt", action="store_true",
                     help="SpMV: use_opt=True (native accumulation) instead of the default path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -266,6 +269,53 @@ def _spmm_coo_workload(dev, dtype_name, N, torch, fs, synthetic):
     }
 
 
+def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
+    from flagsparse_amd import sddmm_csr as mod
+
+    vdt = torch.float64 if dtype_name == "f64" else torch.float32
+    _, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
+    x = synthetic.dense_uniform(shape[0], K, dtype=vdt, seed=1, device=dev)
+    y = synthetic.dense_uniform(shape[1], K, dtype=vdt, seed=2, device=dev)
+    prepared = fs.prepare_sddmm_csr(idx, ptr, shape, k_hint=K)
+    out = torch.empty(prepared.nnz, dtype=vdt, device=dev)
+    v = x.element_size()
+    nnz = prepared.nnz
+    # per entry: column, row id, result; x and y rows once each
+    nbytes = nnz * (4 + 4 + v) + shape[0] * K * v + shape[1] * K * v
+    info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "K": K,
+            "path": "flagsparse_sddmm_csr (baseline variant)",
+            "bytes_gather_inclusive": nnz * (4 + 4 + v + 2 * K * v)}
+
+    def cpu(seconds):
+        from oracle import oracle
+
+        rows = max(1, min(shape[0], int(20e6 // max(1, 32 * K))))
+        ip = ptr[:rows + 1].cpu()
+        ix = idx[:int(ip[-1])].cpu()
+        xh, yh = x[:rows].cpu(), y.cpu()
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            oracle.sddmm_csr(ip, ix, xh, yh)
+            passes += 1
+            secs = time.perf_counter() - t0
+            if secs >= seconds or passes >= 1000:
+                break
+        frac = rows / shape[0]
+        return {"value": round(nbytes * frac * passes / secs / 1e9, 3), "unit": "GB/s",
+                "cores": 1, "kind": "port",
+                "sample": f"{passes} passes of the fp64 C oracle SDDMM over the first {rows} rows "
+                          f"in {secs:.1f} s; bytes scaled by the row fraction",
+                "gflops": round(2 * int(ip[-1]) * K * passes / secs / 1e9, 3)}
+
+    return {
+        "step": lambda: fs.flagsparse_sddmm_csr(x=x, y=y, prepared=prepared, out=out),
+        "launch": lambda: mod._launch_sddmm(prepared, x, y, None, 1.0, 0.0, out, False),
+        "nbytes": nbytes, "flops": 2 * nnz * K, "info": info, "cpu": cpu,
+        "dtype": dtype_name, "kernel": "sddmm_csr_kernel",
+        "tag": f"sddmm_csr_kernel_{dtype_name}_k{K}",
+    }
+
+
 def _copy_workload(dev, torch):
     n = (1 << 30) // 4
     src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -291,6 +341,8 @@ def _build(name, args, dev, torch):
         return _spmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
     if name == "coo5":
         return _spmm_coo_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
+    if name == "sddmm":
+        return _sddmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
     return _copy_workload(dev, torch)
 
 
@@ -347,6 +399,8 @@ def main():
     workload = f"{args.workload}: {WORKLOADS[args.workload]}"
     if args.workload in ("cfg5", "coo5"):
         workload = f"{args.workload} ({w['dtype']}, N={args.n}): {WORKLOADS[args.workload]}"
+    if args.workload == "sddmm":
+        workload = f"sddmm ({w['dtype']}, K={args.n}): {WORKLOADS['sddmm']}"
     info, dtype, kernel, tag = dict(w["info"]), w["dtype"], w["kernel"], w["tag"]
     del w
     torch.cuda.empty_cache()

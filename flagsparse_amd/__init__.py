@@ -1,8 +1,9 @@
-"""flagsparse_amd - MI355X (gfx950) CSR/COO SpMV and CSR SpMM behind FlagSparse's API.
+"""flagsparse_amd - MI355X (gfx950) CSR/COO SpMV, CSR/COO SpMM and CSR SDDMM behind FlagSparse's
+API.
 
 Drop-in for the hot path of the reference package ``flagsparse`` (src/flagsparse/__init__.py):
 the names below keep the reference's signatures, defaults, return values and exceptions.
-Names of the reference that lie outside this path (gather/scatter, SpSV, SpGEMM, SDDMM and the
+Names of the reference that lie outside this path (gather/scatter, SpSV, SpGEMM and the
 CuPy-backed format containers) are listed in ``__all__`` as in the reference; calling them
 raises NotImplementedError.
 
@@ -24,6 +25,7 @@ from .spmm_csr import (
     flagsparse_spmm_csr_opt,
     prepare_spmm_csr_opt,
 )
+from .sddmm_csr import SDDMMPrepared, benchmark_sddmm_case, flagsparse_sddmm_csr, prepare_sddmm_csr
 from .spmm_coo import flagsparse_spmm_coo
 from .spmv_coo import PreparedCoo, flagsparse_spmv_coo, prepare_spmv_coo
 from .spmv_csr import (
@@ -48,6 +50,10 @@ HOT_PATH_EXPORTS = (
     "flagsparse_spmm_csr_opt",
     "flagsparse_spmm_csr",
     "flagsparse_spmm_coo",
+    "prepare_sddmm_csr",
+    "flagsparse_sddmm_csr",
+    "SDDMMPrepared",
+    "benchmark_sddmm_case",
     "benchmark_spmm_case",
     "benchmark_spmm_opt_case",
     "comprehensive_spmm_test",
@@ -72,11 +78,7 @@ OUT_OF_SCOPE_EXPORTS = (
     "prepare_spgemm_csr",
     "flagsparse_spgemm_csr",
     "SpGEMMPrepared",
-    "prepare_sddmm_csr",
-    "flagsparse_sddmm_csr",
-    "SDDMMPrepared",
     "benchmark_spgemm_case",
-    "benchmark_sddmm_case",
     "create_csr_matrix",
     "create_coo_matrix",
     "create_csc_matrix",
@@ -104,8 +106,8 @@ __all__ = list(HOT_PATH_EXPORTS) + list(OUT_OF_SCOPE_EXPORTS)
 def _out_of_scope(name):
     def stub(*args, **kwargs):
         raise NotImplementedError(
-            f"flagsparse.{name} is outside the MI355X build, which implements CSR/COO SpMV and "
-            "CSR SpMM only")
+            f"flagsparse.{name} is outside the MI355X build, which implements CSR/COO SpMV, "
+            "CSR/COO SpMM and CSR SDDMM only")
 
     stub.__name__ = name
     stub.__qualname__ = name

@@ -15,13 +15,14 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
 _i64 = ctypes.c_int64
+_f64 = ctypes.c_double
 
 # name -> (restype, argtypes); kept in the order of include/flagsparse_hip.h.
 SIGNATURES = {
@@ -46,6 +47,8 @@ SIGNATURES = {
     "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "fsp_plan_windows_emit": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p,
                                      _p, _p]),
+    "fsp_sddmm_csr": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i32, _i64, _p, _i64, _p, _i64, _i64,
+                             _p, _f64, _f64, _p, _p, _p, _i64, _i32, _i32, _p]),
 }
 
 

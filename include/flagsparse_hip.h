@@ -31,6 +31,8 @@
  *                          long-row split); for row-sorted COO also the row-run launch of
  *                          spmm_coo.py:394-461 (_triton_spmm_coo_rowrun_impl).
  *   fsp_spmm_coo_atomic  - spmm_coo.py:464-523 (_triton_spmm_coo_atomic_impl).
+ *   fsp_sddmm_csr        - sddmm_csr.py:107-151 (_sddmm_csr_real_kernel) and its launch in
+ *                          _run_sddmm_prepared (:271-347).
  */
 #ifndef FLAGSPARSE_HIP_H
 #define FLAGSPARSE_HIP_H
@@ -202,6 +204,30 @@ int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
 int fsp_spmm_coo_atomic(int dtype, int acc_f64, const void* vals, const int32_t* rows,
                         const int32_t* cols, int64_t nnz, const void* B, int64_t ldb, int64_t N,
                         void* C_acc, int64_t ldc, int64_t n_rows, void* stream);
+
+/*
+ * CSR SDDMM: out[p] = alpha * dot(x[row(p), 0..K), y[cols[p], 0..K)) + beta * data_in[p]
+ * for p < nnz (the data_in term only when data_in != NULL), x [.][ldx] and y [.][ldy] row-major.
+ *   dtype            FSP_F32 / FSP_F64 (x, y, data_in)
+ *   acc_f64          fp32 inputs: accumulate in fp64 (the reference's "acc64" variant)
+ *   out_f64          fp32 inputs: out holds fp64 (the "acc64_out64" variant), else the input type
+ *   lanes_per_entry  G in {1,2,4,...,64} lanes share one entry
+ *   vec              elements per lane per load: 4 (fp32) / 2 (fp64) for 16-byte loads, or 1;
+ *                    vec > 1 requires K, ldx, ldy multiples of vec and 16-byte aligned x, y
+ * Two schedules:
+ *   n_desc > 0       a row-block plan (fsp_plan_windows_* or fsp_plan_row_blocks with
+ *                    rows_cap <= 256/G, nnz_cap and chunk <= fsp_spmm_block_nnz_cap()): desc,
+ *                    ranges and the CSR rowptr (int32 or int64, rowptr_bits) of the pattern;
+ *                    needs K <= 4*G*vec and 16-byte aligned cols; row_ids is not read
+ *   n_desc == 0      one lane group per entry; row_ids gives each entry's row
+ * Deterministic: a fixed reduction order per entry.
+ */
+int fsp_sddmm_csr(int dtype, int acc_f64, int out_f64, const int32_t* cols,
+                  const int32_t* row_ids, const void* rowptr, int rowptr_bits, int64_t nnz,
+                  const void* x, int64_t ldx, const void* y, int64_t ldy, int64_t K,
+                  const void* data_in, double alpha, double beta, void* out,
+                  const int32_t* desc, const int64_t* ranges, int64_t n_desc,
+                  int lanes_per_entry, int vec, void* stream);
 
 #ifdef __cplusplus
 }

@@ -84,3 +84,23 @@ void oracle_spmm_coo_f64(int64_t nnz, const int64_t* rows, const int64_t* cols,
     for (int64_t n = 0; n < N; ++n) c[n] += vals[i] * b[n];
   }
 }
+
+/*
+ * SDDMM on a CSR pattern: out[p] = alpha * sum_k x[r, k] * y[cols[p], k] + beta * data[p] for
+ * the entries p of row r, fp64, k in increasing order (the data term only when data != NULL).
+ * Follows sddmm_csr.py:107-151 (_sddmm_csr_real_kernel) and its torch reference
+ * sddmm_csr.py:425-437; x [n_rows][ldx], y [.][ldy] row-major.
+ */
+void oracle_sddmm_csr_f64(int64_t n_rows, const int64_t* rowptr, const int64_t* cols,
+                          const double* x, int64_t ldx, const double* y, int64_t ldy, int64_t K,
+                          const double* data, double alpha, double beta, double* out) {
+  for (int64_t r = 0; r < n_rows; ++r) {
+    const double* xr = x + r * ldx;
+    for (int64_t p = rowptr[r]; p < rowptr[r + 1]; ++p) {
+      const double* yc = y + cols[p] * ldy;
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k) acc += xr[k] * yc[k];
+      out[p] = alpha * acc + (data ? beta * data[p] : 0.0);
+    }
+  }
+}

@@ -7,10 +7,11 @@ TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and bench.py
 Two kinds of restatement live here, each citing the FlagSparse source it follows (paths
 relative to ``src/flagsparse/sparse_operations/`` unless stated):
 
-* fp64 arithmetic (``spmv_csr``, ``spmv_coo``, ``spmm_csr``, ``spmm_coo``): thin ctypes
-  wrappers over ``fsp_oracle.c``, a plain row-by-row fp64 sum - the definition of correctness
-  every reference test of this path uses (tests/test_spmv.py:143-174,
-  tests/test_spmv_coo.py:56-71, tests/test_spmm.py:270-311, tests/test_spmm_coo.py:98-140).
+* fp64 arithmetic (``spmv_csr``, ``spmv_coo``, ``spmm_csr``, ``spmm_coo``, ``sddmm_csr``):
+  thin ctypes wrappers over ``fsp_oracle.c``, a plain row-by-row fp64 sum - the definition of
+  correctness every reference test of this path uses (tests/test_spmv.py:143-174,
+  tests/test_spmv_coo.py:56-71, tests/test_spmm.py:270-311, tests/test_spmm_coo.py:98-140,
+  tests/test_sddmm.py:155-168).
 * integer planning semantics that change results or observable attributes: the SpMV
   ``block_nnz`` doubling, the ``max_segments`` row truncation of both SpMV paths, the SpMM
   ALG1 launch table and its ``max_segments`` ValueError, the SpMM opt buckets and split
@@ -55,6 +56,9 @@ def _load():
         lib.oracle_spmm_csr_f64.restype = None
         lib.oracle_spmm_coo_f64.argtypes = [i64, p, p, p, p, i64, i64, i64, p, i64]
         lib.oracle_spmm_coo_f64.restype = None
+        d = ctypes.c_double
+        lib.oracle_sddmm_csr_f64.argtypes = [i64, p, p, p, i64, p, i64, i64, p, d, d, p]
+        lib.oracle_sddmm_csr_f64.restype = None
         _lib = lib
     return _lib
 
@@ -135,6 +139,24 @@ def spmm_coo(row, col, data, B, n_rows):
         _load().oracle_spmm_coo_f64(r.size, _ptr(r), _ptr(c), _ptr(dv), _ptr(Bv), N, N, n_rows,
                                     _ptr(C), N)
     return C
+
+
+def sddmm_csr(indptr, indices, x, y, data=None, alpha=1.0, beta=0.0):
+    """fp64 SDDMM on a CSR pattern: alpha * dot(x[row], y[col]) + beta * data per entry
+    (oracle_sddmm_csr_f64)."""
+    ip = _np(indptr, np.int64)
+    ix = _np(indices, np.int64)
+    xv = _np(x, np.float64)
+    yv = _np(y, np.float64)
+    n_rows = ip.size - 1
+    K = xv.shape[1] if xv.ndim == 2 else 0
+    out = np.zeros(ix.size, dtype=np.float64)
+    dv = None if data is None else _np(data, np.float64)
+    if ix.size > 0:
+        _load().oracle_sddmm_csr_f64(n_rows, _ptr(ip), _ptr(ix), _ptr(xv), max(K, 1), _ptr(yv),
+                                     max(K, 1), K, None if dv is None else _ptr(dv),
+                                     float(alpha), float(beta), _ptr(out))
+    return out
 
 
 def time_spmv_csr(indptr, indices, data, x, min_seconds=10.0, max_passes=1000):

@@ -20,6 +20,9 @@ Cases:
                    497-503: shape (4, 6), its fixed row/col lists, N = 48), seeded values
   coo_spmm_dups_f32/f64
                    unsorted COO with repeated (row, col) pairs and empty rows @ B, N = 24
+  sddmm_f32_k64 / sddmm_f64_k33
+                   SDDMM on a ragged CSR pattern (empty rows, repeated columns), alpha 1.25,
+                   beta -0.5 with data; expected values from numpy row gathers in float64
   spmm_f32/f64_N   small CSR @ B for N in {1, 3, 4, 16, 64}
 
 Run from the repository root:  python tests/golden/make_golden.py
@@ -118,6 +121,19 @@ def main():
         _save(f"coo_spmm_dups_{tag}", data=_np(vals), row=_np(row).astype(np.int32),
               col=_np(col).astype(np.int32), B=_np(B),
               shape=np.array([n_rows, n_cols], dtype=np.int64), C=C)
+
+    # SDDMM: out[p] = alpha * dot(x[row(p)], y[col(p)]) + beta * data[p]
+    for dtype, tag, K in ((torch.float32, "f32", 64), (torch.float64, "f64", 33)):
+        d, i, p = synthetic.build_random_csr(400, 300, 5000, dtype, torch.int32, "cpu", seed=41)
+        x = synthetic.dense_uniform(400, K, dtype, seed=42)
+        y = synthetic.dense_uniform(300, K, dtype, seed=43)
+        rows = np.repeat(np.arange(400), np.diff(_np(p)))
+        xs, ys = _np(x).astype(np.float64), _np(y).astype(np.float64)
+        out = 1.25 * np.einsum("pk,pk->p", xs[rows], ys[_np(i).astype(np.int64)]) \
+            - 0.5 * _np(d).astype(np.float64)
+        _save(f"sddmm_{tag}_k{K}", data=_np(d), indices=_np(i), indptr=_np(p), x=_np(x),
+              y=_np(y), shape=np.array([400, 300], dtype=np.int64), alpha=np.array(1.25),
+              beta=np.array(-0.5), out=out)
 
     # small SpMM
     for dtype, tag in ((torch.float32, "f32"), (torch.float64, "f64")):

@@ -34,6 +34,34 @@ def test_library_exports_every_declared_symbol():
     assert sorted(_abi.SIGNATURES) == names
 
 
+_CTYPE = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "double": ctypes.c_double}
+
+
+def _declared_signatures():
+    """{name: (return ctype, [argument ctypes])} parsed from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    sigs = {}
+    for ret, name, params in re.findall(r"\b(int|int64_t|const char\*)\s+(fsp_\w+)\s*\(([^)]*)\)\s*;",
+                                        text):
+        args = []
+        params = params.strip()
+        if params and params != "void":
+            for prm in params.split(","):
+                prm = " ".join(prm.split())
+                args.append(ctypes.c_void_p if "*" in prm else _CTYPE[prm.rsplit(" ", 1)[0]])
+        sigs[name] = (ctypes.c_char_p if "char" in ret else _CTYPE[ret], args)
+    return sigs
+
+
+def test_ctypes_table_matches_header_prototypes():
+    sigs = _declared_signatures()
+    assert sorted(sigs) == _declared_functions()
+    for name, (ret, args) in sigs.items():
+        want_ret, want_args = _abi.SIGNATURES[name]
+        assert want_ret == ret, name
+        assert list(want_args) == args, name
+
+
 def test_abi_version_and_caps():
     L = _abi.lib()
     assert L.fsp_abi_version() == _abi.ABI_VERSION

@@ -71,6 +71,14 @@ REFERENCE_SIGNATURES = {
         ("value_dtype", torch.float32), ("index_dtype", torch.int32), ("warmup", 20),
         ("iters", 200), ("block_n", None), ("block_nnz", 256), ("run_cusparse", True),
         ("route", "rowrun"), ("compare_routes", False)],
+    "prepare_sddmm_csr": [("indices", None), ("indptr", None), ("shape", None), ("k_hint", 64)],
+    "flagsparse_sddmm_csr": [("data", None), ("indices", None), ("indptr", None), ("x", None),
+                             ("y", None), ("shape", None), ("alpha", 1.0), ("beta", 0.0),
+                             ("prepared", None), ("out", None), ("return_time", False),
+                             ("return_meta", False), ("allow_fallback", False)],
+    "benchmark_sddmm_case": [("n_rows", 1024), ("n_cols", 1024), ("nnz", 16384), ("k_dim", 64),
+                             ("value_dtype", torch.float32), ("warmup", 10), ("iters", 30),
+                             ("alpha", 1.0), ("beta", 0.0), ("run_cusparse", False)],
     "spmm_coo.comprehensive_spmm_coo_test": [
         ("n_rows", 4096), ("n_cols", 4096), ("nnz", 65536), ("n_dense_cols", 32),
         ("dtype", torch.float32), ("index_dtype", torch.int32), ("warmup", 20), ("iters", 200),
@@ -80,6 +88,7 @@ REFERENCE_SIGNATURES = {
 REQUIRED = {
     "prepare_spmv_csr": 4, "prepare_spmv_coo_tocsr": 4, "prepare_spmv_coo": 4,
     "prepare_spmm_csr_opt": 4, "flagsparse_spmm_csr": 5, "flagsparse_spmm_coo": 5,
+    "prepare_sddmm_csr": 3,
 }
 
 
@@ -237,6 +246,35 @@ def test_spmm_coo_host_validation():
     cfg = spmm_coo._resolve_spmm_coo_launch_config(48, 1000)
     assert (cfg["block_n"], cfg["block_nnz"], cfg["required_nnz_tiles"]) == (64, 256, 4)
     assert (cfg["heuristic_warp_size"], cfg["heuristic_factor"]) == (32, 2)
+
+
+def test_sddmm_host_validation():
+    # sddmm_csr.py:46-66 and :361-373: checks that fail before the device is touched
+    indices = torch.tensor([0, 1, 1], dtype=torch.int32)
+    indptr = torch.tensor([0, 2, 3], dtype=torch.int64)
+    with pytest.raises(ValueError, match="2-tuple"):
+        fs.prepare_sddmm_csr(indices, indptr, (2,))
+    with pytest.raises(ValueError, match="1D"):
+        fs.prepare_sddmm_csr(indices[None], indptr, (2, 2))
+    with pytest.raises(ValueError, match="non-negative"):
+        fs.prepare_sddmm_csr(indices, indptr, (-1, 2))
+    with pytest.raises(ValueError, match="n_rows\\+1=4"):
+        fs.prepare_sddmm_csr(indices, indptr, (3, 2))
+    with pytest.raises(ValueError, match="CUDA"):
+        fs.prepare_sddmm_csr(indices, indptr, (2, 2))
+    with pytest.raises(ValueError, match="required"):
+        fs.flagsparse_sddmm_csr(x=torch.ones(2, 2), y=torch.ones(2, 2))
+    with pytest.raises(TypeError, match="SDDMMPrepared"):
+        fs.flagsparse_sddmm_csr(x=torch.ones(2, 2), y=torch.ones(2, 2), prepared=object())
+    from flagsparse_amd import sddmm_csr
+
+    with pytest.raises(ValueError, match="variant"):
+        sddmm_csr._normalize_sddmm_diagnostic_variant("fast")
+    assert sddmm_csr._normalize_sddmm_diagnostic_variant(None) == "baseline"
+    assert sddmm_csr._normalize_sddmm_diagnostic_variant(" ACC64 ") == "acc64"
+    # the reference's launch table (sddmm_csr.py:36-43)
+    assert [sddmm_csr._resolve_sddmm_launch_config(k) for k in (1, 32, 33, 64, 65, 128, 129)] == \
+        [(32, 2), (32, 2), (64, 4), (64, 4), (64, 4), (64, 4), (128, 8)]
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -22,6 +22,7 @@ CSR_CASES = ["cfg1_csr_f32", "poisson64_f64", "ragged_f32", "ragged_f64"]
 SPMM_CASES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(HERE, "spmm_*.npz")))
 COO_SPMM_CASES = ["coo_spmm_ref_f32", "coo_spmm_ref_f64", "coo_spmm_dups_f32",
                   "coo_spmm_dups_f64"]
+SDDMM_CASES = ["sddmm_f32_k64", "sddmm_f64_k33"]
 
 
 def _load(name):
@@ -31,7 +32,7 @@ def _load(name):
 
 def test_fixture_inventory():
     assert len(SPMM_CASES) == 10
-    for name in CSR_CASES + ["coo_dups_f32", "longrow_spmm_f32"] + COO_SPMM_CASES:
+    for name in CSR_CASES + ["coo_dups_f32", "longrow_spmm_f32"] + COO_SPMM_CASES + SDDMM_CASES:
         assert os.path.exists(os.path.join(HERE, name + ".npz"))
 
 
@@ -61,6 +62,14 @@ def test_oracle_spmm_coo_on_fixture(name):
     g = _load(name)
     C = oracle.spmm_coo(g["row"], g["col"], g["data"], g["B"], int(g["shape"][0]))
     np.testing.assert_allclose(C, g["C"], rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("name", SDDMM_CASES)
+def test_oracle_sddmm_on_fixture(name):
+    g = _load(name)
+    out = oracle.sddmm_csr(g["indptr"], g["indices"], g["x"], g["y"], g["data"],
+                           alpha=float(g["alpha"]), beta=float(g["beta"]))
+    np.testing.assert_allclose(out, g["out"], rtol=1e-12, atol=1e-12)
 
 
 def test_generator_reproduces_cfg1_fixture():
@@ -146,3 +155,18 @@ def test_gpu_spmm_coo_fixture(dev, name, route):
     print(f"fixture {name} route={route}", flush=True)
     C = spmm_coo._run_spmm_coo_route(t["data"], t["row"], t["col"], t["B"], shape, route=route)
     _check(C, g["C"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", SDDMM_CASES)
+def test_gpu_sddmm_fixture(dev, name):
+    import flagsparse_amd as fs
+
+    g = _load(name)
+    t = {k: torch.from_numpy(g[k]).to(dev) for k in ("data", "indices", "indptr", "x", "y")}
+    shape = tuple(int(v) for v in g["shape"])
+    print(f"fixture {name}", flush=True)
+    out = fs.flagsparse_sddmm_csr(data=t["data"], indices=t["indices"], indptr=t["indptr"],
+                                  x=t["x"], y=t["y"], shape=shape, alpha=float(g["alpha"]),
+                                  beta=float(g["beta"]))
+    _check(out, g["out"])

@@ -7,6 +7,8 @@ other than a retyped formula:
   spmv_csr, spmv_coo, spmm_csr,    scipy.sparse (an independent CSR/COO implementation), exact
   spmm_coo                         integer arithmetic, Poisson closed forms, unit vectors,
                                    identity / permutation matrices
+  sddmm_csr                        numpy row gathers + einsum (an independent formulation), the
+                                   dense product (x @ y.T) sampled at the pattern, one-hot rows
   spmv_csr(row_cap=...)            a loop-by-loop emulation of the reference's tile loops
                                    (spmv_csr.py:106-118, 176-190, 240-250) on a dense copy
   spmv_prepare_knobs               brute-force search over block_nnz doublings + known answers
@@ -217,6 +219,36 @@ def test_spmm_coo_permutation_and_edges():
     assert C.tolist() == [[0.0, 0.0], [5.0, -10.0], [0.0, 0.0]]
     assert oracle.spmm_coo([], [], [], np.ones((4, 3)), 2).tolist() == [[0.0] * 3] * 2
     assert oracle.spmm_coo([0], [0], [1.0], np.empty((1, 0)), 2).shape == (2, 0)
+
+
+@pytest.mark.parametrize("K", [1, 7, 64])
+def test_sddmm_matches_sampled_dense_product(K):
+    rng = np.random.default_rng(200 + K)
+    n_rows, n_cols = 90, 70
+    indptr, cols, data = _random_csr(rng, n_rows, n_cols, 1200)
+    x = rng.standard_normal((n_rows, K))
+    y = rng.standard_normal((n_cols, K))
+    rows = np.repeat(np.arange(n_rows), np.diff(indptr))
+    want = 1.5 * np.einsum("pk,pk->p", x[rows], y[cols]) - 0.25 * data
+    got = oracle.sddmm_csr(indptr, cols, x, y, data, alpha=1.5, beta=-0.25)
+    np.testing.assert_allclose(got, want, rtol=1e-13, atol=1e-13)
+    # the same values as the dense product sampled at the pattern
+    np.testing.assert_allclose(oracle.sddmm_csr(indptr, cols, x, y), (x @ y.T)[rows, cols],
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_sddmm_one_hot_and_edges():
+    # x, y one-hot: out[p] = 1 exactly when row(p) and col(p) pick the same k
+    x = np.eye(4)[[0, 1, 2]]
+    y = np.eye(4)[[2, 0, 1, 3]]
+    indptr = np.array([0, 2, 3, 5])
+    cols = np.array([1, 3, 2, 0, 1])
+    assert oracle.sddmm_csr(indptr, cols, x, y).tolist() == [1.0, 0.0, 1.0, 1.0, 0.0]
+    # K = 0 leaves only the beta term; no entries give an empty result
+    data = np.array([1.0, 2.0, 3.0, 4.0, 5.0])
+    assert oracle.sddmm_csr(indptr, cols, x[:, :0], y[:, :0], data, beta=2.0).tolist() == \
+        [2.0, 4.0, 6.0, 8.0, 10.0]
+    assert oracle.sddmm_csr(np.zeros(4, np.int64), np.zeros(0), x, y).size == 0
 
 
 # ------------------------------------------------------------------------------------------

@@ -88,23 +88,45 @@ struct QuadLoader<NT, double> {
   }
 };
 
-// Butterfly sum over aligned groups of g lanes (g a power of two, g <= 64).  Every lane of
-// the group ends with the same value; the pairing order is fixed, so the result is
-// deterministic.  All lanes of a group must be active.
+// Lane permutes through DPP (a VALU modifier, no LDS round trip).  dpp_add<CTRL>(v) adds the
+// value of the lane that the DPP control word CTRL selects; all sources used here lie inside
+// the lane's 16-lane row, so every lane reads a valid source.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
+                                                        false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_add(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffff), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xF, 0xF, false);
+  return v + __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
+}
+
+// Sum over aligned groups of g lanes (g a power of two, g <= 64); every lane of the group ends
+// with the total.  Inside a 16-lane row: quad permutes [1,0,3,2] and [2,3,0,1], then the
+// half-row mirror and the row mirror (DPP); across rows, lane exchanges (ds_bpermute).  The
+// order of the additions is fixed, so the result is deterministic.  All lanes of a group must
+// be active.
 template <typename A>
 __device__ __forceinline__ A group_sum(A v, int g) {
-  for (int off = 1; off < g; off <<= 1) v += __shfl_xor(v, off, kWave);
+  if (g >= 2) v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (g >= 4) v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (g >= 8) v = dpp_add<0x141>(v);  // row_half_mirror
+  if (g >= 16) v = dpp_add<0x140>(v); // row_mirror
+  if (g >= 32) v += __shfl_xor(v, 16, kWave);
+  if (g >= 64) v += __shfl_xor(v, 32, kWave);
   return v;
 }
 
 template <typename A>
 __device__ __forceinline__ A wave_sum(A v) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  return group_sum(v, kWave);
 }
 
-// Workgroup sum in a fixed order: butterfly inside each wave, then waves 0..3 in order.
+// Workgroup sum in a fixed order: group_sum inside each wave, then waves 0..3 in order.
 // Result valid in every thread.  red must hold kWavesPerBlock entries.
 template <typename A>
 __device__ __forceinline__ A block_sum(A v, A* red) {

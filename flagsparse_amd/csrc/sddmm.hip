@@ -16,8 +16,8 @@
 // a time (four y rows in flight per lane); a long row is cut into chunks that all groups of a
 // workgroup share.  Entries are independent, so chunks need no second pass.
 // sddmm_flat_kernel (any K): a group per entry, x and y rows both loaded per entry.
-// Each dot ends with a sum over the G lanes done with DPP row permutes (no LDS round trip) in
-// a fixed order, so results are deterministic.
+// Each dot ends with a sum over the G lanes (group_sum: DPP row permutes, no LDS round trip)
+// in a fixed order, so results are deterministic.
 #include "fsp_device.hpp"
 #include "fsp_internal.hpp"
 
@@ -41,34 +41,6 @@ __device__ __forceinline__ void sload(const T* p, T (&o)[VW]) {
 #pragma unroll
     for (int j = 0; j < VW; ++j) o[j] = v[j];
   }
-}
-
-// Sum over aligned groups of G lanes (G a power of two <= 64); every lane of a group gets the
-// total.  Inside a 16-lane DPP row: quad permutes [1,0,3,2] and [2,3,0,1], then the half-row
-// and row mirrors; across rows a lane exchange (ds_bpermute).  Fixed order: deterministic.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
-                                                        false));
-}
-
-template <int CTRL>
-__device__ __forceinline__ double dpp_add(double v) {
-  const int64_t b = __double_as_longlong(v);
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffff), CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xF, 0xF, false);
-  return v + __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
-}
-
-template <typename A>
-__device__ __forceinline__ A group_sum_dpp(A v, int G) {
-  if (G >= 2) v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
-  if (G >= 4) v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
-  if (G >= 8) v = dpp_add<0x141>(v);  // row_half_mirror
-  if (G >= 16) v = dpp_add<0x140>(v); // row_mirror
-  if (G >= 32) v += __shfl_xor(v, 16, kWave);
-  if (G >= 64) v += __shfl_xor(v, 32, kWave);
-  return v;
 }
 
 constexpr int kSdSlots = (int)kSpmmSlots;  // staged columns per workgroup
@@ -168,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
       }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[q] = group_sum_dpp(acc[q], G);
+    for (int q = 0; q < 4; ++q) acc[q] = group_sum(acc[q], G);
     // Every lane of the group holds the four sums.  With G >= 4, lanes 0..3 store them in one
     // instruction; narrower groups store result q from lane q mod G.
     if (G >= 4) {
@@ -241,7 +213,7 @@ __global__ __launch_bounds__(kBlock) void sddmm_flat_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      acc[u] = group_sum_dpp(acc[u], G);
+      acc[u] = group_sum(acc[u], G);
       if (lane == 0 && ok[u]) {
         const int64_t p = base + u * groups + grp;
         A v = acc[u] * a_alpha;

@@ -104,10 +104,15 @@ __all__ = list(HOT_PATH_EXPORTS) + list(OUT_OF_SCOPE_EXPORTS)
 
 
 def _out_of_scope(name):
+    hint = ""
+    if name == "read_mtx_file":
+        hint = ("; .mtx files load into torch CSR / COO tensors with "
+                "flagsparse_amd.mtx.load_mtx_to_csr_torch / load_mtx_to_coo_torch")
+
     def stub(*args, **kwargs):
         raise NotImplementedError(
             f"flagsparse.{name} is outside the MI355X build, which implements CSR/COO SpMV, "
-            "CSR/COO SpMM and CSR SDDMM only")
+            f"CSR/COO SpMM and CSR SDDMM only{hint}")
 
     stub.__name__ = name
     stub.__qualname__ = name

@@ -47,6 +47,7 @@ SIGNATURES = {
     "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p]),
     "fsp_plan_windows_emit": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p,
                                      _p, _p]),
+    "fsp_mtx_read": (_i32, [ctypes.c_char_p, _p, _p, _p, _p, _i64]),
     "fsp_sddmm_csr": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i32, _i64, _p, _i64, _p, _i64, _i64,
                              _p, _f64, _f64, _p, _p, _p, _i64, _i32, _i32, _p]),
 }

@@ -33,6 +33,8 @@
  *   fsp_spmm_coo_atomic  - spmm_coo.py:464-523 (_triton_spmm_coo_atomic_impl).
  *   fsp_sddmm_csr        - sddmm_csr.py:107-151 (_sddmm_csr_real_kernel) and its launch in
  *                          _run_sddmm_prepared (:271-347).
+ *   fsp_mtx_read         - the .mtx parsing of the reference's test loaders
+ *                          (tests/test_spmv.py:29-103 and its copies).
  */
 #ifndef FLAGSPARSE_HIP_H
 #define FLAGSPARSE_HIP_H
@@ -228,6 +230,20 @@ int fsp_sddmm_csr(int dtype, int acc_f64, int out_f64, const int32_t* cols,
                   const void* data_in, double alpha, double beta, void* out,
                   const int32_t* desc, const int64_t* ranges, int64_t n_desc,
                   int lanes_per_entry, int vec, void* stream);
+
+/*
+ * Matrix Market coordinate file reader (host only, no GPU): the format of the reference's
+ * SuiteSparse test drivers (tests/test_spmv.py:29-103, tests/test_spmm_coo.py:156-249,
+ * tests/test_spmv_coo.py:257-305).  info[0..7) receives n_rows, n_cols, the header nnz, the
+ * field (0 real / integer, 1 pattern, 2 complex), the symmetry (0 general, 1 symmetric,
+ * 2 skew-symmetric, 3 hermitian), the number of entries read and how many lacked a value.
+ * With rows == NULL only the header is read; otherwise up to min(nnz, capacity) entry lines
+ * are returned as 0-based rows / cols and vals (two doubles per entry for complex files), in
+ * file order; lines with fewer than two tokens are skipped.  Expansion of symmetric storage
+ * and duplicate summation are left to the caller.
+ */
+int fsp_mtx_read(const char* path, int64_t* info, int64_t* rows, int64_t* cols, double* vals,
+                 int64_t capacity);
 
 #ifdef __cplusplus
 }

@@ -48,7 +48,10 @@ def _declared_signatures():
         if params and params != "void":
             for prm in params.split(","):
                 prm = " ".join(prm.split())
-                args.append(ctypes.c_void_p if "*" in prm else _CTYPE[prm.rsplit(" ", 1)[0]])
+                if prm.startswith("const char*"):
+                    args.append(ctypes.c_char_p)
+                else:
+                    args.append(ctypes.c_void_p if "*" in prm else _CTYPE[prm.rsplit(" ", 1)[0]])
         sigs[name] = (ctypes.c_char_p if "char" in ret else _CTYPE[ret], args)
     return sigs
 

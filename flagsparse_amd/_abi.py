@@ -101,6 +101,18 @@ def stream_handle(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def raw_stream(device):
+    """The same handle as an int, through torch's C accessor when it exists (a few hundred ns
+    instead of building a Stream object) - for per-call launch paths."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _current_raw_stream is not None:
+        return _current_raw_stream(index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def caps():
     """Kernel capacities compiled into the library."""
     L = lib()

@@ -73,6 +73,8 @@ class RowBlockLayout:
         self.plan = build_row_block_plan(host, data.device, caps["spmv_stream_nnz"],
                                          caps["spmv_stream_rows"], caps["spmv_stream_nnz"],
                                          caps["spmv_chunk_nnz"])
+        self._args = {}
+        self._keep = None
 
     def kernel_name(self):
         return "spmv_rowblock_kernel"
@@ -82,19 +84,30 @@ class RowBlockLayout:
                 "split_rows": self.plan.n_split_rows, "partials": self.plan.n_parts}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
-        plan = self.plan
-        partials = plan.workspace()
-        groups, group_base, split_rows = plan.split_groups()
-        L = _abi.lib()
-        _abi.check(
-            L.fsp_spmv_csr(_abi.dtype_code(self.data.dtype), int(acc_f64), _abi.ptr(self.data),
-                           _abi.ptr(self.cols), _abi.ptr(self.rowptr), self.rowptr_bits,
-                           self.n_rows, self.nnz, _abi.ptr(x), _abi.ptr(y), _abi.ptr(row_map),
-                           n_out, _abi.ptr(plan.desc), _abi.ptr(plan.ranges), plan.n_desc,
-                           plan.chunk, _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
-                           _abi.ptr(split_rows), int(groups.shape[0]), XCD_REMAP_ROWBLOCK,
-                           _abi.stream_handle(y.device)),
-            "fsp_spmv_csr")
+        # The arguments that do not change between calls are converted once (per accumulation
+        # mode); a call fills in x, y, the row map and the stream.
+        args = self._args.get(bool(acc_f64))
+        if args is None:
+            plan = self.plan
+            groups, group_base, split_rows = plan.split_groups()
+            keep = (plan.workspace(), groups, group_base, split_rows)
+            args = [_abi.dtype_code(self.data.dtype), int(acc_f64), self.data.data_ptr(),
+                    self.cols.data_ptr(), self.rowptr.data_ptr(), self.rowptr_bits,
+                    self.n_rows, self.nnz, None, None, None, 0, plan.desc.data_ptr(),
+                    plan.ranges.data_ptr(), plan.n_desc, plan.chunk, keep[0].data_ptr(),
+                    groups.data_ptr() if groups.numel() else None,
+                    group_base.data_ptr() if group_base.numel() else None,
+                    split_rows.data_ptr() if split_rows.numel() else None,
+                    int(groups.shape[0]), 0, None]
+            self._args[bool(acc_f64)] = args
+            self._keep = keep
+        a = list(args)
+        a[8], a[9] = x.data_ptr(), y.data_ptr()
+        a[10] = None if row_map is None else row_map.data_ptr()
+        a[11] = n_out
+        a[21] = XCD_REMAP_ROWBLOCK
+        a[22] = _abi.raw_stream(y.device)
+        _abi.check(_abi.lib().fsp_spmv_csr(*a), "fsp_spmv_csr")
         return y
 
 
@@ -331,16 +344,23 @@ class XcsLayout:
                 "col_bits": self.col_bits, "padded_entries": self.n_entries}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
-        L = _abi.lib()
-        _abi.check(
-            L.fsp_spmv_xcs(_abi.dtype_code(self.vals.dtype), int(acc_f64), _abi.ptr(self.vals),
-                           _abi.ptr(self.pidx), self.n_entries, self.col_bits, _abi.ptr(x),
-                           _abi.ptr(y), _abi.ptr(row_map), n_out, _abi.ptr(self.items),
-                           self.n_slots, _abi.ptr(self.masks), _abi.ptr(self.partials),
-                           _abi.ptr(self.split_rows), _abi.ptr(self.split_ptr),
-                           _abi.ptr(self.slots), self.n_split_rows,
-                           _abi.stream_handle(y.device)),
-            "fsp_spmv_xcs")
+        # static arguments converted once per accumulation mode (see RowBlockLayout.launch)
+        args = self._args.get(bool(acc_f64)) if hasattr(self, "_args") else None
+        if args is None:
+            if not hasattr(self, "_args"):
+                self._args = {}
+            p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
+            args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
+                    self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
+                    self.n_slots, p(self.masks), p(self.partials), p(self.split_rows),
+                    p(self.split_ptr), p(self.slots), self.n_split_rows, None]
+            self._args[bool(acc_f64)] = args
+        a = list(args)
+        a[6], a[7] = x.data_ptr(), y.data_ptr()
+        a[8] = None if row_map is None else row_map.data_ptr()
+        a[9] = n_out
+        a[18] = _abi.raw_stream(y.device)
+        _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 
 

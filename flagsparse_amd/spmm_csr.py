@@ -291,7 +291,8 @@ def _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols=None):
 class _SpmmKernelCsr:
     """Kernel-facing CSR arrays (aligned, int32 offsets when they fit) and plans per G."""
 
-    __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_plans")
+    __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_plans", "_args",
+                 "_keep")
 
     def __init__(self, data, cols, indptr64):
         self.data = _aligned(data)
@@ -303,6 +304,8 @@ class _SpmmKernelCsr:
         else:
             self.rowptr, self.rowptr_bits = indptr64, 64
         self._plans = {}
+        self._args = {}
+        self._keep = []
 
     def kernel_name(self):
         return "spmm_rowblock_kernel"
@@ -331,19 +334,24 @@ def _run_spmm(kc, B, C, acc_f64, tile_cols=None):
         return C
     dtype = B.dtype
     lanes, vec = _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols)
-    plan = kc.plan(lanes)
-    partials = plan.workspace(n_dense_cols)
-    groups, group_base, split_rows = plan.split_groups()
-    L = _abi.lib()
-    _abi.check(
-        L.fsp_spmm_csr(_abi.dtype_code(dtype), 1 if acc_f64 else 0, _abi.ptr(kc.data),
-                       _abi.ptr(kc.cols), _abi.ptr(kc.rowptr), kc.rowptr_bits, kc.n_rows, kc.nnz,
-                       _abi.ptr(B), B.stride(0), n_dense_cols, _abi.ptr(C), C.stride(0),
-                       _abi.ptr(plan.desc), plan.n_desc, plan.chunk, lanes, vec,
-                       _abi.ptr(partials), _abi.ptr(groups), _abi.ptr(group_base),
-                       _abi.ptr(split_rows), int(groups.shape[0]), XCD_REMAP,
-                       _abi.stream_handle(C.device)),
-        "fsp_spmm_csr")
+    key = (lanes, vec, n_dense_cols, bool(acc_f64), dtype)
+    args = kc._args.get(key)
+    if args is None:  # the arguments that do not change between calls, converted once
+        plan = kc.plan(lanes)
+        partials = plan.workspace(n_dense_cols)
+        groups, group_base, split_rows = plan.split_groups()
+        p = lambda t: t.data_ptr() if t.numel() else None  # noqa: E731
+        args = [_abi.dtype_code(dtype), 1 if acc_f64 else 0, p(kc.data), p(kc.cols),
+                p(kc.rowptr), kc.rowptr_bits, kc.n_rows, kc.nnz, None, 0, n_dense_cols, None, 0,
+                p(plan.desc), plan.n_desc, plan.chunk, lanes, vec, p(partials), p(groups),
+                p(group_base), p(split_rows), int(groups.shape[0]), 0, None]
+        kc._args[key] = args
+        kc._keep.append(partials)
+    a = list(args)
+    a[8], a[9], a[11], a[12] = B.data_ptr(), B.stride(0), C.data_ptr(), C.stride(0)
+    a[23] = XCD_REMAP
+    a[24] = _abi.raw_stream(C.device)
+    _abi.check(_abi.lib().fsp_spmm_csr(*a), "fsp_spmm_csr")
     return C
 
 

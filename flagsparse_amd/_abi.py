@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 
@@ -44,9 +44,9 @@ SIGNATURES = {
                             _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),
     "fsp_spmm_coo_atomic": (_i32, [_i32, _i32, _p, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64,
                                    _p]),
-    "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p]),
-    "fsp_plan_windows_emit": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p,
-                                     _p, _p]),
+    "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),
+    "fsp_plan_windows_emit": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p,
+                                     _p, _p, _p]),
     "fsp_mtx_read": (_i32, [ctypes.c_char_p, _p, _p, _p, _p, _i64]),
     "fsp_sddmm_csr": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i32, _i64, _p, _i64, _p, _i64, _i64,
                              _p, _f64, _f64, _p, _p, _p, _i64, _i32, _i32, _p]),

@@ -103,20 +103,22 @@ def build_row_block_plan(rowptr_host, device, nnz_cap, rows_cap, long_threshold,
                         long_threshold, desc_host=desc, ranges=ranges_t)
 
 
-def build_row_block_plan_device(rowptr, nnz_cap, rows_cap, long_threshold, chunk):
+def build_row_block_plan_device(rowptr, nnz_cap, rows_cap, long_threshold, chunk,
+                                window_rows=None):
     """The row-block plan built on the device (fsp_plan_windows_count / _emit): rows cut into
-    windows of ``rows_cap`` rows, each planned like the host planner; one small device-to-host
-    copy (the three totals) between the passes.  ``rowptr`` is an int32 or int64 device
-    tensor."""
+    windows of ``window_rows`` rows (default ``rows_cap``), each planned like the host
+    planner; one small device-to-host copy (the three totals) between the passes.  ``rowptr``
+    is an int32 or int64 device tensor."""
     L = _abi.lib()
     dev = rowptr.device
     bits = 32 if rowptr.dtype == torch.int32 else 64
     rp = rowptr if bits == 32 else rowptr.to(torch.int64)
     rp = rp.contiguous()
     n_rows = int(rp.numel()) - 1
-    args = (_abi.ptr(rp), bits, n_rows, int(nnz_cap), int(rows_cap), int(long_threshold),
+    window = int(rows_cap if window_rows is None else window_rows)
+    args = (_abi.ptr(rp), bits, n_rows, window, int(nnz_cap), int(rows_cap), int(long_threshold),
             int(chunk))
-    n_win = -(-max(n_rows, 0) // int(rows_cap))
+    n_win = -(-max(n_rows, 0) // max(window, 1))
     stream = _abi.stream_handle(dev)
     counts = torch.empty((3, max(n_win, 1)), dtype=torch.int64, device=dev)
     if n_win == 0:
@@ -138,6 +140,39 @@ def build_row_block_plan_device(rowptr, nnz_cap, rows_cap, long_threshold, chunk
                                        _abi.ptr(split_rows), stream), "fsp_plan_windows_emit")
     return RowBlockPlan(desc, n_parts, n_split, chunk, rows_cap, nnz_cap, long_threshold,
                         ranges=ranges, groups=(groups, group_base, split_rows))
+
+
+def build_row_block_plan_windows(rowptr, nnz_cap, rows_cap, long_threshold, chunk,
+                                 window_rows):
+    """The windowed row-block plan for ``rowptr`` wherever it lives: on a GPU tensor the device
+    planner; on a CPU tensor the host planner run window by window (the same table - the
+    device planner's contract - for host-side tests of the layouts built on it)."""
+    if rowptr.is_cuda:
+        return build_row_block_plan_device(rowptr, nnz_cap, rows_cap, long_threshold, chunk,
+                                           window_rows)
+    rp = rowptr_to_host(rowptr)
+    n_rows = rp.size - 1
+    window = max(int(window_rows), 1)
+    tables, ranges, parts, splits = [], [], 0, 0
+    for w0 in range(0, n_rows, window):
+        w1 = min(w0 + window, n_rows)
+        p = build_row_block_plan(rp[w0:w1 + 1] - rp[w0], None, nnz_cap, rows_cap,
+                                 long_threshold, chunk)
+        d = p.desc_host.astype(np.int64)
+        short = d[:, 2] == 0
+        d[:, 0] += w0
+        d[short, 1] += w0
+        d[(~short) & (d[:, 3] >= 0), 3] += parts
+        tables.append(d)
+        ranges.append(p.ranges.numpy() + rp[w0])
+        parts += p.n_parts
+        splits += p.n_split_rows
+    desc = np.concatenate(tables) if tables else np.zeros((0, 4), dtype=np.int64)
+    rng = np.concatenate(ranges) if ranges else np.zeros((0, 2), dtype=np.int64)
+    desc32 = np.ascontiguousarray(desc, dtype=np.int32)
+    return RowBlockPlan(torch.from_numpy(desc32), parts, splits, chunk, rows_cap, nnz_cap,
+                        long_threshold, desc_host=desc32,
+                        ranges=torch.from_numpy(np.ascontiguousarray(rng)))
 
 
 def truncate_rows(data, indices, indptr, caps):

@@ -26,7 +26,7 @@ import torch
 
 from . import _abi
 from ._common import _INDEX_LIMIT_INT32, _aligned
-from ._plan import build_row_block_plan, rowptr_to_host
+from ._plan import build_row_block_plan_windows
 
 XCD_COUNT = 8
 L2_BYTES = 4 << 20
@@ -47,10 +47,11 @@ FORCE = None
 # us; banded and power-law matrices within 1%).
 XCD_REMAP_ROWBLOCK = 0
 FORCE_PANELS_PER_XCD = None
-
-
-def _host_rowptr(rowptr):
-    return rowptr_to_host(rowptr)
+# Plans are built on the device in windows of this many times the block row cap (one thread
+# per window; a block never crosses a window end, so this bounds the blocks cut short to one
+# per window - about 2.5 % more blocks on a 5-point stencil - while keeping thousands of
+# threads busy on large matrices).
+PLAN_WINDOW_BLOCKS = 16
 
 
 class RowBlockLayout:
@@ -58,7 +59,7 @@ class RowBlockLayout:
 
     kind = "rowblock"
 
-    def __init__(self, data, cols, rowptr, rowptr_host=None):
+    def __init__(self, data, cols, rowptr, window_rows=None):
         self.data = _aligned(data)
         self.cols = _aligned(cols)
         nnz = int(data.numel())
@@ -69,10 +70,11 @@ class RowBlockLayout:
         self.nnz = nnz
         self.n_rows = int(rowptr.numel()) - 1
         caps = _abi.caps()
-        host = _host_rowptr(rowptr) if rowptr_host is None else rowptr_host
-        self.plan = build_row_block_plan(host, data.device, caps["spmv_stream_nnz"],
-                                         caps["spmv_stream_rows"], caps["spmv_stream_nnz"],
-                                         caps["spmv_chunk_nnz"])
+        rows_cap = caps["spmv_stream_rows"]
+        window = PLAN_WINDOW_BLOCKS * rows_cap if window_rows is None else int(window_rows)
+        self.plan = build_row_block_plan_windows(self.rowptr, caps["spmv_stream_nnz"], rows_cap,
+                                                 caps["spmv_stream_nnz"], caps["spmv_chunk_nnz"],
+                                                 window)
         self._args = {}
         self._keep = None
 
@@ -120,15 +122,14 @@ class XcsLayout:
 
     kind = "xcs"
 
-    def __init__(self, data, cols, rowptr, n_cols, rowptr_host=None, panels_per_xcd=None):
+    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None):
         dev = data.device
         caps = _abi.caps()
         item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
         nnz = int(data.numel())
         n_rows = int(rowptr.numel()) - 1
         self.n_rows, self.n_cols, self.nnz = n_rows, int(n_cols), nnz
-        host = _host_rowptr(rowptr) if rowptr_host is None else rowptr_host
-        lengths_h = np.diff(host)
+        lengths = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
         cols = cols.to(torch.int32)
 
         # 1. P = 8*m column panels of about equal nnz (m panels per XCD, run one after the
@@ -170,25 +171,24 @@ class XcsLayout:
         #    of <= rows_cap consecutive rows and <= 8 * item_cap entries, in which the long
         #    rows are rows without entries - they do not cut the run of short rows.
         tile_nnz = P * item_cap
-        long_mask = lengths_h > tile_nnz
-        long_rows = np.nonzero(long_mask)[0]
-        short_ptr = np.zeros(n_rows + 1, dtype=np.int64)
-        short_ptr[1:] = np.cumsum(np.where(long_mask, 0, lengths_h))
-        plan = build_row_block_plan(short_ptr, None, tile_nnz, self.rows_cap, tile_nnz, 1)
-        desc = plan.desc.numpy().astype(np.int64)
-        n_long = int(long_rows.size)
-        t_r0 = np.concatenate([long_rows, desc[:, 0]]).astype(np.int64)
-        t_R = np.concatenate([np.ones(n_long, dtype=np.int64), desc[:, 1] - desc[:, 0]])
-        n_tiles = int(t_r0.size)
+        long_mask = lengths > tile_nnz
+        long_rows = torch.nonzero(long_mask).flatten()
+        short_ptr = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(torch.where(long_mask, 0, lengths), 0, out=short_ptr[1:])
+        plan = build_row_block_plan_windows(short_ptr, tile_nnz, self.rows_cap, tile_nnz, 1,
+                                            PLAN_WINDOW_BLOCKS * self.rows_cap)
+        desc = plan.desc.to(device=dev, dtype=torch.int64)
+        n_long = int(long_rows.numel())
+        t_r0_d = torch.cat([long_rows, desc[:, 0]])
+        t_R_d = torch.cat([torch.ones(n_long, dtype=torch.int64, device=dev),
+                           desc[:, 1] - desc[:, 0]])
+        n_tiles = int(t_r0_d.numel())
         self.n_tiles = n_tiles
         self.n_long_tiles = n_long
-        t_r0_d = torch.from_numpy(t_r0).to(dev)
-        t_R_d = torch.from_numpy(t_R).to(dev)
         tile_of_row = torch.repeat_interleave(torch.arange(n_long, n_tiles, device=dev),
                                               t_R_d[n_long:])
         if n_long:
-            tile_of_row[torch.from_numpy(long_rows).to(dev)] = torch.arange(n_long, device=dev)
-        lengths = torch.from_numpy(lengths_h).to(dev)
+            tile_of_row[long_rows] = torch.arange(n_long, device=dev)
 
         # 3. Entry -> (tile, panel); stable sort keeps row order (then original order).
         entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths)
@@ -390,16 +390,15 @@ def build_layout(data, cols, rowptr, n_cols):
     """The layout for one CSR (or COO row-run) matrix: XCS when it pays, else row blocks."""
     mode = FORCE
     nnz = int(data.numel())
-    host = _host_rowptr(rowptr)
     if mode is None:
         mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
     if mode == "xcs" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(n_cols) <= (1 << 27) and \
             int(rowptr.numel()) > 1:
         try:
-            return XcsLayout(data, cols, rowptr, n_cols, host, FORCE_PANELS_PER_XCD)
+            return XcsLayout(data, cols, rowptr, n_cols, FORCE_PANELS_PER_XCD)
         except ValueError:
             pass  # too large for the packing: row blocks
-    return RowBlockLayout(data, cols, rowptr, host)
+    return RowBlockLayout(data, cols, rowptr)
 
 
 __all__ = ["RowBlockLayout", "XcsLayout", "build_layout", "prefers_xcs", "sample_indices",

@@ -2,15 +2,20 @@
 // without a prepared object, COO SpMM) and for the SpMM prepare step: no copy of the row
 // pointers to the host and no host loop over rows.
 //
-// The rows are cut into windows of rows_cap rows, the most one block may hold.  One thread
-// plans its window with the rules of the host planner fsp_plan_row_blocks (abi.cpp): a block
-// takes consecutive rows of at most long_threshold entries while their entries fit nnz_cap; a
-// row longer than long_threshold becomes ceil(len / chunk) chunk descriptors, and when that is
+// The rows are cut into windows of window_rows rows.  One thread plans its window with the
+// rules of the host planner fsp_plan_row_blocks (abi.cpp): a block takes at most rows_cap
+// consecutive rows of at most long_threshold entries while their entries fit nnz_cap; a row
+// longer than long_threshold becomes ceil(len / chunk) chunk descriptors, and when that is
 // more than one it gets a run of partial slots and a combine group.  The one difference is
 // that no block crosses a window boundary.  Pass 1 counts each window's descriptors, partial
 // slots and split rows (three rows of n_win counters); the caller turns each row into
 // exclusive offsets (a prefix sum) and allocates the tables; pass 2 runs the same code and
 // writes at those offsets.
+//
+// When long_threshold == nnz_cap every row that fits a block is short, so a block's end is
+// the last row boundary within nnz_cap entries of its start: a binary search over the row
+// pointers (about log2(rows_cap) loads per block instead of one per row).  That lets a thread
+// plan a wide window quickly, and wide windows cut few blocks short.
 //
 // Reference behaviour replaced: the bucket planning of spmm_csr.py:417-477
 // (_build_spmm_opt_split_metadata's host Python loop over long rows, _build_spmm_opt_buckets).
@@ -22,8 +27,9 @@ namespace {
 
 template <typename P>
 __global__ __launch_bounds__(kBlock) void plan_windows_kernel(
-    const P* __restrict__ rowptr, int64_t n_rows, int64_t n_win, int64_t nnz_cap,
-    int64_t rows_cap, int64_t long_threshold, int64_t chunk, int64_t* __restrict__ counts,
+    const P* __restrict__ rowptr, int64_t n_rows, int64_t n_win, int64_t window,
+    int64_t nnz_cap, int64_t rows_cap, int64_t long_threshold, int64_t chunk,
+    int64_t* __restrict__ counts,
     const int64_t* __restrict__ offsets, i32x4* __restrict__ desc, int64_t* __restrict__ ranges,
     i32x4* __restrict__ groups, int64_t* __restrict__ group_base,
     int32_t* __restrict__ split_rows) {
@@ -33,8 +39,9 @@ __global__ __launch_bounds__(kBlock) void plan_windows_kernel(
   int64_t nd = emit ? offsets[w] : 0;
   int64_t np = emit ? offsets[n_win + w] : 0;
   int64_t ns = emit ? offsets[2 * n_win + w] : 0;
-  int64_t i = w * rows_cap;
-  const int64_t end = (i + rows_cap < n_rows) ? i + rows_cap : n_rows;
+  int64_t i = w * window;
+  const int64_t end = (i + window < n_rows) ? i + window : n_rows;
+  const bool bisect = long_threshold >= nnz_cap;
   while (i < end) {
     const int64_t a = (int64_t)rowptr[i];
     const int64_t len = (int64_t)rowptr[i + 1] - a;
@@ -69,12 +76,24 @@ __global__ __launch_bounds__(kBlock) void plan_windows_kernel(
       continue;
     }
     // Row i is short (len <= long_threshold <= nnz_cap), so it always starts a block.
+    const int64_t jmax = (i + rows_cap < end) ? i + rows_cap : end;
     int64_t j = i + 1, acc = len;
-    while (j < end) {
-      const int64_t l = (int64_t)rowptr[j + 1] - (int64_t)rowptr[j];
-      if (l > long_threshold || acc + l > nnz_cap) break;
-      acc += l;
-      ++j;
+    if (bisect) {
+      // largest j in [i + 1, jmax] with rowptr[j] - a <= nnz_cap (true at j = i + 1)
+      int64_t hi = jmax;
+      while (j < hi) {
+        const int64_t mid = j + (hi - j + 1) / 2;
+        if ((int64_t)rowptr[mid] - a <= nnz_cap) j = mid;
+        else hi = mid - 1;
+      }
+      acc = (int64_t)rowptr[j] - a;
+    } else {
+      while (j < jmax) {
+        const int64_t l = (int64_t)rowptr[j + 1] - (int64_t)rowptr[j];
+        if (l > long_threshold || acc + l > nnz_cap) break;
+        acc += l;
+        ++j;
+      }
     }
     if (emit) {
       i32x4 d;
@@ -95,31 +114,32 @@ __global__ __launch_bounds__(kBlock) void plan_windows_kernel(
   }
 }
 
-int check_plan_args(int rowptr_bits, int64_t n_rows, int64_t nnz_cap, int64_t rows_cap,
-                    int64_t long_threshold, int64_t chunk, const void* rowptr, const char* who) {
+int check_plan_args(int rowptr_bits, int64_t n_rows, int64_t window, int64_t nnz_cap,
+                    int64_t rows_cap, int64_t long_threshold, int64_t chunk, const void* rowptr,
+                    const char* who) {
   if (rowptr_bits != 32 && rowptr_bits != 64)
     return set_error(FSP_EINVAL, std::string(who) + ": rowptr_bits must be 32 or 64");
   if (n_rows < 0 || n_rows >= 0x7fffffffLL)
     return set_error(FSP_EINVAL, std::string(who) + ": n_rows must be in [0, 2^31-1)");
   if (n_rows > 0 && !rowptr) return set_error(FSP_EINVAL, std::string(who) + ": null rowptr");
   if (nnz_cap < 1 || rows_cap < 1 || chunk < 1 || long_threshold < 1 ||
-      long_threshold > nnz_cap)
+      long_threshold > nnz_cap || window < 1)
     return set_error(FSP_EINVAL, std::string(who) +
                                      ": need 1 <= long_threshold <= nnz_cap, rows_cap >= 1, "
-                                     "chunk >= 1");
+                                     "chunk >= 1, window_rows >= 1");
   return FSP_OK;
 }
 
 template <typename P>
-int launch_plan(const void* rowptr, int64_t n_rows, int64_t nnz_cap, int64_t rows_cap,
-                int64_t long_threshold, int64_t chunk, int64_t* counts, const int64_t* offsets,
-                int32_t* desc, int64_t* ranges, int32_t* groups, int64_t* group_base,
-                int32_t* split_rows, hipStream_t st) {
-  const int64_t n_win = (n_rows + rows_cap - 1) / rows_cap;
+int launch_plan(const void* rowptr, int64_t n_rows, int64_t window, int64_t nnz_cap,
+                int64_t rows_cap, int64_t long_threshold, int64_t chunk, int64_t* counts,
+                const int64_t* offsets, int32_t* desc, int64_t* ranges, int32_t* groups,
+                int64_t* group_base, int32_t* split_rows, hipStream_t st) {
+  const int64_t n_win = (n_rows + window - 1) / window;
   if (n_win == 0) return FSP_OK;
   const int64_t blocks = (n_win + kBlock - 1) / kBlock;
   hipLaunchKernelGGL((plan_windows_kernel<P>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                     static_cast<const P*>(rowptr), n_rows, n_win, nnz_cap, rows_cap,
+                     static_cast<const P*>(rowptr), n_rows, n_win, window, nnz_cap, rows_cap,
                      long_threshold, chunk, counts, offsets, reinterpret_cast<i32x4*>(desc),
                      ranges, reinterpret_cast<i32x4*>(groups), group_base, split_rows);
   return check_hip(hipGetLastError(), "plan_windows_kernel launch");
@@ -131,34 +151,38 @@ int launch_plan(const void* rowptr, int64_t n_rows, int64_t nnz_cap, int64_t row
 using namespace fsp;
 
 extern "C" int fsp_plan_windows_count(const void* rowptr, int rowptr_bits, int64_t n_rows,
-                                      int64_t nnz_cap, int64_t rows_cap, int64_t long_threshold,
-                                      int64_t chunk, int64_t* counts, void* stream) {
-  int rc = check_plan_args(rowptr_bits, n_rows, nnz_cap, rows_cap, long_threshold, chunk, rowptr,
-                           "fsp_plan_windows_count");
+                                      int64_t window_rows, int64_t nnz_cap, int64_t rows_cap,
+                                      int64_t long_threshold, int64_t chunk, int64_t* counts,
+                                      void* stream) {
+  int rc = check_plan_args(rowptr_bits, n_rows, window_rows, nnz_cap, rows_cap, long_threshold,
+                           chunk, rowptr, "fsp_plan_windows_count");
   if (rc) return rc;
   if (n_rows > 0 && !counts) return set_error(FSP_EINVAL, "fsp_plan_windows_count: null counts");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rowptr_bits == 32)
-    return launch_plan<int>(rowptr, n_rows, nnz_cap, rows_cap, long_threshold, chunk, counts,
-                            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, st);
-  return launch_plan<int64_t>(rowptr, n_rows, nnz_cap, rows_cap, long_threshold, chunk, counts,
-                              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+    return launch_plan<int>(rowptr, n_rows, window_rows, nnz_cap, rows_cap, long_threshold, chunk,
+                            counts, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+  return launch_plan<int64_t>(rowptr, n_rows, window_rows, nnz_cap, rows_cap, long_threshold,
+                              chunk, counts, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                              st);
 }
 
 extern "C" int fsp_plan_windows_emit(const void* rowptr, int rowptr_bits, int64_t n_rows,
-                                     int64_t nnz_cap, int64_t rows_cap, int64_t long_threshold,
-                                     int64_t chunk, const int64_t* offsets, int32_t* desc,
-                                     int64_t* ranges, int32_t* groups, int64_t* group_base,
-                                     int32_t* split_rows, void* stream) {
-  int rc = check_plan_args(rowptr_bits, n_rows, nnz_cap, rows_cap, long_threshold, chunk, rowptr,
-                           "fsp_plan_windows_emit");
+                                     int64_t window_rows, int64_t nnz_cap, int64_t rows_cap,
+                                     int64_t long_threshold, int64_t chunk,
+                                     const int64_t* offsets, int32_t* desc, int64_t* ranges,
+                                     int32_t* groups, int64_t* group_base, int32_t* split_rows,
+                                     void* stream) {
+  int rc = check_plan_args(rowptr_bits, n_rows, window_rows, nnz_cap, rows_cap, long_threshold,
+                           chunk, rowptr, "fsp_plan_windows_emit");
   if (rc) return rc;
   if (n_rows > 0 && (!offsets || !desc))
     return set_error(FSP_EINVAL, "fsp_plan_windows_emit: null offsets or desc");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rowptr_bits == 32)
-    return launch_plan<int>(rowptr, n_rows, nnz_cap, rows_cap, long_threshold, chunk, nullptr,
-                            offsets, desc, ranges, groups, group_base, split_rows, st);
-  return launch_plan<int64_t>(rowptr, n_rows, nnz_cap, rows_cap, long_threshold, chunk, nullptr,
-                              offsets, desc, ranges, groups, group_base, split_rows, st);
+    return launch_plan<int>(rowptr, n_rows, window_rows, nnz_cap, rows_cap, long_threshold, chunk,
+                            nullptr, offsets, desc, ranges, groups, group_base, split_rows, st);
+  return launch_plan<int64_t>(rowptr, n_rows, window_rows, nnz_cap, rows_cap, long_threshold,
+                              chunk, nullptr, offsets, desc, ranges, groups, group_base,
+                              split_rows, st);
 }

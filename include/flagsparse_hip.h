@@ -1,5 +1,6 @@
 /*
- * flagsparse_hip.h - C ABI of the MI355X (gfx950) CSR/COO SpMV and CSR SpMM library.
+ * flagsparse_hip.h - C ABI of the MI355X (gfx950) sparse-product library: CSR/COO SpMV,
+ * CSR/COO SpMM, CSR SDDMM, and a Matrix Market reader.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t passed as void*.
  * Nothing here allocates device memory: workspaces (partial sums, descriptor tables) are
@@ -88,12 +89,15 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
 
 /*
  * The same plan built on the device in two passes (no host copy of rowptr, no host loop):
- * the rows are cut into windows of rows_cap rows and each window is planned with the rules of
- * fsp_plan_row_blocks, except that no block crosses a window boundary.  Replaces the host loop
- * of spmm_csr.py:417-441 (_build_spmm_opt_split_metadata) and the bucket lists of :444-477 on
- * the paths that plan on every call.
+ * the rows are cut into windows of window_rows rows and each window is planned with the rules
+ * of fsp_plan_row_blocks, except that no block crosses a window boundary.  Replaces the host
+ * loop of spmm_csr.py:417-441 (_build_spmm_opt_split_metadata), the bucket lists of :444-477
+ * and spmv_csr.py:281-327 (_build_spmv_opt_buckets).  One thread plans a window; with
+ * long_threshold == nnz_cap it finds each block's end by binary search, so wide windows
+ * (e.g. 16 * rows_cap rows) stay cheap.
  *   rowptr         device row pointers, int32 (rowptr_bits 32) or int64 (64), n_rows + 1
- *   counts         pass 1 output, device int64 [3][n_win], n_win = ceil(n_rows / rows_cap):
+ *   window_rows    rows per window (>= 1)
+ *   counts         pass 1 output, device int64 [3][n_win], n_win = ceil(n_rows / window_rows):
  *                  per window the number of descriptors, partial slots and split rows
  *   offsets        pass 2 input: the exclusive prefix sum of each of the three rows of counts
  *   desc           [n_desc] int32 quadruples, as fsp_plan_row_blocks writes them
@@ -104,14 +108,14 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
  * Both passes are asynchronous on stream; the caller reads the totals (one small copy) between
  * them to size the tables.
  */
-int fsp_plan_windows_count(const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz_cap,
-                           int64_t rows_cap, int64_t long_threshold, int64_t chunk,
-                           int64_t* counts, void* stream);
-int fsp_plan_windows_emit(const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz_cap,
-                          int64_t rows_cap, int64_t long_threshold, int64_t chunk,
-                          const int64_t* offsets, int32_t* desc, int64_t* ranges,
-                          int32_t* groups, int64_t* group_base, int32_t* split_rows,
-                          void* stream);
+int fsp_plan_windows_count(const void* rowptr, int rowptr_bits, int64_t n_rows,
+                           int64_t window_rows, int64_t nnz_cap, int64_t rows_cap,
+                           int64_t long_threshold, int64_t chunk, int64_t* counts, void* stream);
+int fsp_plan_windows_emit(const void* rowptr, int rowptr_bits, int64_t n_rows,
+                          int64_t window_rows, int64_t nnz_cap, int64_t rows_cap,
+                          int64_t long_threshold, int64_t chunk, const int64_t* offsets,
+                          int32_t* desc, int64_t* ranges, int32_t* groups, int64_t* group_base,
+                          int32_t* split_rows, void* stream);
 
 /*
  * y = A @ x for CSR A (or COO row runs when row_map != NULL).

@@ -162,15 +162,18 @@ def test_planner_rejects_bad_arguments():
 
 def test_device_planner_rejects_bad_arguments():
     L = _abi.lib()
-    # (rowptr, bits, n_rows, nnz_cap, rows_cap, long_threshold, chunk, counts, stream)
-    assert L.fsp_plan_windows_count(None, 16, 0, 10, 4, 5, 5, None, None) == -1
+    # (rowptr, bits, n_rows, window_rows, nnz_cap, rows_cap, long_threshold, chunk, counts,
+    #  stream)
+    assert L.fsp_plan_windows_count(None, 16, 0, 4, 10, 4, 5, 5, None, None) == -1
     assert b"rowptr_bits" in L.fsp_last_error()
-    assert L.fsp_plan_windows_count(None, 32, 0, 10, 4, 11, 5, None, None) == -1
+    assert L.fsp_plan_windows_count(None, 32, 0, 4, 10, 4, 11, 5, None, None) == -1
     assert b"long_threshold" in L.fsp_last_error()
-    assert L.fsp_plan_windows_count(None, 32, 3, 10, 4, 5, 5, None, None) == -1  # null rowptr
-    assert L.fsp_plan_windows_emit(None, 64, -1, 10, 4, 5, 5, None, None, None, None, None,
+    assert L.fsp_plan_windows_count(None, 32, 0, 0, 10, 4, 5, 5, None, None) == -1
+    assert b"window_rows" in L.fsp_last_error()
+    assert L.fsp_plan_windows_count(None, 32, 3, 4, 10, 4, 5, 5, None, None) == -1  # null rowptr
+    assert L.fsp_plan_windows_emit(None, 64, -1, 4, 10, 4, 5, 5, None, None, None, None, None,
                                    None, None) == -1
-    assert L.fsp_plan_windows_count(None, 32, 0, 10, 4, 5, 5, None, None) == 0  # nothing to do
+    assert L.fsp_plan_windows_count(None, 32, 0, 4, 10, 4, 5, 5, None, None) == 0  # nothing
 
 
 def test_kernel_entry_points_reject_before_any_hip_call():

@@ -1,9 +1,11 @@
 """The device row-block planner (fsp_plan_windows_count / _emit) on the GPU.
 
-Its contract: the rows are cut into windows of rows_cap rows and each window is planned with
-the host planner's rules (fsp_plan_row_blocks).  So the device table must equal, exactly, the
-concatenation of host-planner tables of the windows (row ids and partial-slot bases shifted),
-and its entry ranges and combine groups must match the descriptors.
+Its contract: the rows are cut into windows of window_rows rows and each window is planned
+with the host planner's rules (fsp_plan_row_blocks).  So the device table must equal, exactly,
+the concatenation of host-planner tables of the windows (row ids and partial-slot bases
+shifted), and its entry ranges and combine groups must match the descriptors.  Windows wider
+than rows_cap with long_threshold == nnz_cap take the binary-search block end; with
+long_threshold < nnz_cap the row-by-row scan; a single window reproduces the host plan.
 """
 
 import ctypes
@@ -36,11 +38,12 @@ def _host_plan(rowptr, nnz_cap, rows_cap, thr, chunk):
     return desc, npart.value, nsplit.value
 
 
-def _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk):
+def _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk, window=None):
     n = rowptr.size - 1
+    window = rows_cap if window is None else window
     tables, parts, splits = [], 0, 0
-    for w0 in range(0, n, rows_cap):
-        w1 = min(w0 + rows_cap, n)
+    for w0 in range(0, n, window):
+        w1 = min(w0 + window, n)
         desc, np_w, ns_w = _host_plan(rowptr[w0:w1 + 1] - rowptr[w0], nnz_cap, rows_cap, thr,
                                       chunk)
         short = desc[:, 2] == 0
@@ -65,14 +68,16 @@ def _lengths(seed, n):
 @pytest.mark.parametrize("seed", [0, 1])
 @pytest.mark.parametrize("caps", CAPS)
 @pytest.mark.parametrize("bits", [32, 64])
-def test_device_plan_matches_windowed_host_plan(dev, seed, caps, bits):
+@pytest.mark.parametrize("wmul", [1, 3, 100])
+def test_device_plan_matches_windowed_host_plan(dev, seed, caps, bits, wmul):
     nnz_cap, rows_cap, thr, chunk = caps
+    window = rows_cap * wmul
     lengths = _lengths(seed, 3000)
     rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
     rp_dev = torch.from_numpy(rowptr).to(dev).to(torch.int32 if bits == 32 else torch.int64)
-    print(f"device plan seed={seed} caps={caps} bits={bits}", flush=True)
-    plan = build_row_block_plan_device(rp_dev, nnz_cap, rows_cap, thr, chunk)
-    want, parts, splits = _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk)
+    print(f"device plan seed={seed} caps={caps} bits={bits} window={window}", flush=True)
+    plan = build_row_block_plan_device(rp_dev, nnz_cap, rows_cap, thr, chunk, window)
+    want, parts, splits = _windowed_expectation(rowptr, nnz_cap, rows_cap, thr, chunk, window)
     got = plan.desc.cpu().numpy().astype(np.int64)
     assert np.array_equal(got, want)
     assert (plan.n_parts, plan.n_split_rows) == (parts, splits)
@@ -99,7 +104,24 @@ def test_device_plan_edges(dev):
         rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
         rp_dev = torch.from_numpy(rowptr).to(dev)
         for caps in ((2045, 16, 128, 2045), (2045, 1024, 2045, 4093)):
-            plan = build_row_block_plan_device(rp_dev, *caps)
-            want, parts, splits = _windowed_expectation(rowptr, *caps)
-            assert np.array_equal(plan.desc.cpu().numpy().astype(np.int64), want)
-            assert (plan.n_parts, plan.n_split_rows) == (parts, splits)
+            for window in (None, 16 * caps[1]):
+                plan = build_row_block_plan_device(rp_dev, *caps, window_rows=window)
+                want, parts, splits = _windowed_expectation(rowptr, *caps, window=window)
+                assert np.array_equal(plan.desc.cpu().numpy().astype(np.int64), want)
+                assert (plan.n_parts, plan.n_split_rows) == (parts, splits)
+
+
+def test_device_plan_bisect_on_uniform_rows(dev):
+    # a Poisson-like pattern (rows of 3..5 entries) in one window equals the host plan, and in
+    # windows of 16 * rows_cap differs from it only by blocks cut at window ends
+    n = 70000
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(3, 6, n).astype(np.int64)
+    rowptr = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    rp_dev = torch.from_numpy(rowptr).to(dev).to(torch.int32)
+    caps = (2045, 1024, 2045, 4093)
+    whole = build_row_block_plan_device(rp_dev, *caps, window_rows=n)
+    want, _, _ = _host_plan(rowptr, *caps)
+    assert np.array_equal(whole.desc.cpu().numpy().astype(np.int64), want)
+    wide = build_row_block_plan_device(rp_dev, *caps, window_rows=16 * 1024)
+    assert wide.n_desc <= want.shape[0] + -(-n // (16 * 1024))

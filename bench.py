@@ -101,6 +101,11 @@ def _event_loop(fn, count, torch):
     return start.elapsed_time(end) / count
 
 
+def _tag(kernel):
+    """File-name form of a kernel label ("a+b" for a path of two main kernels)."""
+    return kernel.replace("+", "_")
+
+
 def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
     if name == "cfg1":
         data, idx, ptr, x, shape = synthetic.csr_uniform_rows(device=dev)
@@ -141,7 +146,7 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
         "dtype": "f64" if data.dtype == torch.float64 else "f32",
-        "kernel": kc.kernel_name(), "tag": f"{kc.kernel_name()}_{name}",
+        "kernel": kc.kernel_name(), "tag": f"{_tag(kc.kernel_name())}_{name}",
     }
 
 
@@ -174,7 +179,7 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
         "step": lambda: fs.flagsparse_spmv_coo(x=x, prepared=prepared, out=y),
         "launch": lambda: mod._run_spmv_coo(prepared, x, y, 256),
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu, "dtype": "f32",
-        "kernel": prepared._kernel_name(), "tag": f"{prepared._kernel_name()}_cfg4",
+        "kernel": prepared._kernel_name(), "tag": f"{_tag(prepared._kernel_name())}_cfg4",
     }
 
 

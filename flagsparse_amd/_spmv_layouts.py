@@ -15,11 +15,19 @@ Two layouts, chosen once per matrix at prepare time:
     (uniform random columns, power-law graphs).  Rows whose entries fall in several workgroups
     are summed through partials in a fixed order (deterministic).
 
+``PanelLayout`` (csrc/spmv_xcs.hip, ``spmv_panel_kernel``)
+    The long rows of a power-law matrix: x cut into panels of 64 KiB, the rows' entries ordered
+    by (panel, row); a workgroup copies one panel into LDS and its waves gather from there, so
+    these gathers run at LDS speed instead of the L2 request rate.  One partial per (row,
+    chunk of 512 entries), added per row in a fixed order.
+
+``XcsHybridLayout``
+    ``PanelLayout`` for the rows long enough to put several entries in every panel,
+    ``XcsLayout`` for the others; two launches one after the other on the same stream.
+
 Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produce the same
 row sums up to floating-point summation order.
 """
-
-import ctypes
 
 import numpy as np
 import torch
@@ -39,8 +47,9 @@ PANEL_BYTES = 3 << 20
 NEAR_COLUMNS = 1 << 16
 SAMPLE = 1 << 20
 
-# Test hooks: layout (None: choose per matrix, "rowblock" or "xcs"); panels per XCD (None:
-# from the size of x).
+# Test hooks: layout (None: choose per matrix, "rowblock", "xcs" - hybrid when the long rows
+# qualify -, "xcs-l2" - never hybrid - or "xcs-hybrid" - hybrid whenever there is a long row);
+# panels per XCD (None: from the size of x).
 FORCE = None
 # Row-block SpMV launches in hardware order (workgroup i on XCD i % 8): on MI355X this streamed
 # faster than one contiguous descriptor range per XCD (cfg2 60.5 vs 64.7 us, cfg1 9.7 vs 12.0
@@ -52,6 +61,15 @@ FORCE_PANELS_PER_XCD = None
 # per window - about 2.5 % more blocks on a 5-point stencil - while keeping thousands of
 # threads busy on large matrices).
 PLAN_WINDOW_BLOCKS = 16
+# Panel layout: chunks per job at most (a job copies its panel of x into LDS once), and the
+# long-row rule of the hybrid - rows with at least PANEL_RUNS entries per x panel go to the
+# panel layout when they hold at least PANEL_MIN_SHARE of the entries.  Measured on MI355X
+# for cfg3: PANEL_RUNS 8 (rows >= 4096 entries, 62 % of nnz) 466 us, 4: 498 us, 16: 474 us;
+# 256 chunks per job (one job per panel) 466 us, 128: 476 us.
+PANEL_JOB_CHUNKS = 256
+PANEL_RUNS = 8
+PANEL_MIN_SHARE = 0.25
+FORCE_PANEL_ROW_MIN = None
 
 
 class RowBlockLayout:
@@ -122,7 +140,9 @@ class XcsLayout:
 
     kind = "xcs"
 
-    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None):
+    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None, skip_rows=None):
+        """``skip_rows``: optional bool mask of rows (without entries here) that another layout
+        writes; they are left alone instead of being written as 0."""
         dev = data.device
         caps = _abi.caps()
         item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
@@ -270,6 +290,8 @@ class XcsLayout:
             row_max.scatter_reduce_(0, er, item_of, reduce="amax")
         del entry_row, perm, key_sorted
         empty = lengths == 0
+        if skip_rows is not None:
+            empty &= ~skip_rows
         split = (row_max > row_min) & ~empty
         sel = split[er]  # sorted entries of split rows, in (item, row) order
         pair_key = torch.unique_consecutive(item_of[sel] * max(n_rows, 1) + er[sel])
@@ -364,6 +386,163 @@ class XcsLayout:
         return y
 
 
+def _panel_col_bits(n_cols, value_bytes):
+    """Bits of a column inside its panel: 2^bits values fit the LDS copy (and no more than x
+    needs)."""
+    fit = (_abi.caps()["panel_bytes"] // value_bytes).bit_length() - 1
+    return max(1, min(fit, _ceil_log2(max(int(n_cols), 2))))
+
+
+def panel_row_min(n_cols, value_bytes):
+    """Row length from which a row puts about PANEL_RUNS entries in every x panel."""
+    if FORCE_PANEL_ROW_MIN is not None:
+        return int(FORCE_PANEL_ROW_MIN)
+    n_panels = -(-int(n_cols) >> _panel_col_bits(n_cols, value_bytes))
+    return PANEL_RUNS * max(1, n_panels)
+
+
+class PanelLayout:
+    """Rows whose x gathers are served from LDS copies of 64 KiB x panels (module docstring).
+    ``rows`` are the output rows of the CSR rows given; built on the device."""
+
+    kind = "panels"
+
+    def __init__(self, data, cols, rowptr, n_cols, rows):
+        dev = data.device
+        caps = _abi.caps()
+        chunk = caps["panel_chunk"]
+        self.n_cols, self.nnz = int(n_cols), int(data.numel())
+        n_rows = int(rowptr.numel()) - 1
+        cb = _panel_col_bits(n_cols, data.element_size())
+        if n_rows >= (1 << (32 - cb)):
+            raise ValueError("too many rows for the panel packing")
+        self.col_bits = cb
+        self.rows = rows.to(torch.int32).contiguous()
+        rp = rowptr.to(torch.int64)
+        row = torch.repeat_interleave(torch.arange(n_rows, device=dev), rp[1:] - rp[:-1])
+        c64 = cols.to(torch.int64)
+        # entries by (panel, row): a stable sort by panel keeps each row's entries in order
+        panel = c64 >> cb
+        n_panels = max(1, -(-self.n_cols >> cb))
+        order = torch.sort(panel, stable=True)[1]
+        panel = panel[order]
+        cnt = torch.bincount(panel, minlength=n_panels)
+        padded = (cnt + chunk - 1) // chunk * chunk
+        seg = torch.cumsum(padded, 0) - padded
+        first = torch.cumsum(cnt, 0) - cnt
+        n_entries = int(padded.sum().item())
+        dest = seg[panel] + torch.arange(self.nnz, device=dev) - first[panel]
+        row_s = row[order]
+        self.vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
+        self.vals[dest] = data[order]
+        # padding: value 0 in the last row of its panel, so it adds no run
+        last = torch.zeros(n_panels, dtype=torch.int64, device=dev)
+        has = cnt > 0
+        last[has] = row_s[(first + cnt - 1)[has]]
+        pidx = torch.repeat_interleave(last, padded) << cb
+        pidx[dest] = (row_s << cb) | (c64[order] & ((1 << cb) - 1))
+        del order, row, row_s, c64, dest
+        self.n_entries = n_entries
+        # one partial slot per (chunk, run): runs start at a chunk start or a row change
+        n_chunks = n_entries // chunk
+        rowpos = pidx >> cb
+        starts = torch.ones(n_entries, dtype=torch.bool, device=dev)
+        starts[1:] = rowpos[1:] != rowpos[:-1]
+        starts[::chunk] = True
+        runs = starts.view(n_chunks, chunk).sum(1)
+        self.chunk_slot = (torch.cumsum(runs, 0) - runs).to(torch.int32).contiguous()
+        slot_row = rowpos[starts]
+        self.n_partials = int(slot_row.numel())
+        self.slots = torch.sort(slot_row, stable=True)[1].to(torch.int32).contiguous()
+        row_ptr = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(torch.bincount(slot_row, minlength=n_rows), 0, out=row_ptr[1:])
+        self.row_ptr = row_ptr.to(torch.int32).contiguous()
+        self.n_rows = n_rows
+        self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
+        if self.pidx.numel() < 4:
+            self.pidx = torch.zeros(4, dtype=torch.int32, device=dev)
+        del pidx, rowpos, starts, slot_row
+        # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
+        # sizes keep the rounds of workgroups even)
+        per_panel = padded // chunk
+        n_jobs_p = (per_panel + PANEL_JOB_CHUNKS - 1) // PANEL_JOB_CHUNKS
+        self.job_panel = torch.repeat_interleave(torch.arange(n_panels, device=dev), n_jobs_p)
+        job_first = torch.cumsum(n_jobs_p, 0) - n_jobs_p
+        k = torch.arange(self.job_panel.numel(), device=dev) - job_first[self.job_panel]
+        starts_c = (seg // chunk)[self.job_panel] + \
+            k * per_panel[self.job_panel] // n_jobs_p[self.job_panel]
+        self.jobs = torch.cat([starts_c, torch.tensor([n_chunks], device=dev)]).to(
+            torch.int32).contiguous()
+        self.job_panel = self.job_panel.to(torch.int32).contiguous()
+        self.n_jobs = int(self.job_panel.numel())
+        self.n_panels = n_panels
+        self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+        self._args = {}
+
+    def kernel_name(self):
+        return "spmv_panel_kernel"
+
+    def describe(self):
+        return {"layout": self.kind, "rows": self.n_rows, "panels": self.n_panels,
+                "col_bits": self.col_bits, "jobs": self.n_jobs,
+                "chunks": self.n_entries // _abi.caps()["panel_chunk"],
+                "partials": self.n_partials, "padded_entries": self.n_entries}
+
+    def launch(self, x, y, acc_f64, row_map=None):
+        args = self._args.get(bool(acc_f64))
+        if args is None:  # static arguments converted once per accumulation mode
+            p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
+            args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
+                    self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
+                    p(self.job_panel), self.n_jobs, p(self.chunk_slot), p(self.partials),
+                    p(self.rows), p(self.row_ptr), p(self.slots), self.n_rows, None]
+            self._args[bool(acc_f64)] = args
+        a = list(args)
+        a[6], a[8] = x.data_ptr(), y.data_ptr()
+        a[9] = None if row_map is None else row_map.data_ptr()
+        a[19] = _abi.raw_stream(y.device)
+        _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
+        return y
+
+
+class XcsHybridLayout:
+    """Long rows in a PanelLayout, the rest in an XcsLayout (module docstring).  The XCS part
+    sees the long rows as rows without entries and leaves them alone; the panel part writes
+    them.  The two parts run one after the other: run concurrently on two streams they were
+    slower on MI355X (cfg3 510 us vs 465 us) - the panel part's entry stream evicts the x
+    panels the XCS part keeps in L2."""
+
+    kind = "xcs-hybrid"
+
+    def __init__(self, data, cols, rowptr, n_cols, long_mask, panels_per_xcd=None):
+        dev = data.device
+        rp = rowptr.to(torch.int64)
+        lengths = rp[1:] - rp[:-1]
+        self.n_rows, self.n_cols, self.nnz = int(lengths.numel()), int(n_cols), int(data.numel())
+        entry_long = torch.repeat_interleave(long_mask, lengths)
+        short_ptr = torch.zeros_like(rp)
+        torch.cumsum(torch.where(long_mask, 0, lengths), 0, out=short_ptr[1:])
+        self.short = XcsLayout(data[~entry_long], cols[~entry_long], short_ptr, n_cols,
+                               panels_per_xcd, skip_rows=long_mask)
+        long_rows = torch.nonzero(long_mask).flatten()
+        long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
+        self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
+
+    def kernel_name(self):
+        return "spmv_xcs_kernel+spmv_panel_kernel"
+
+    def describe(self):
+        return {"layout": self.kind, "long_rows": self.long.n_rows,
+                "long_entries": self.long.nnz, "xcs_part": self.short.describe(),
+                "panel_part": self.long.describe()}
+
+    def launch(self, x, y, acc_f64, row_map=None, n_out=0):
+        self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
+        self.long.launch(x, y, acc_f64, row_map)
+        return y
+
+
 def sample_indices(n, k, device):
     """min(n, k) indices spread evenly over [0, n), computed in exact int64 arithmetic."""
     if n <= k:
@@ -392,15 +571,22 @@ def build_layout(data, cols, rowptr, n_cols):
     nnz = int(data.numel())
     if mode is None:
         mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
-    if mode == "xcs" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(n_cols) <= (1 << 27) and \
-            int(rowptr.numel()) > 1:
+    if mode in ("xcs", "xcs-l2", "xcs-hybrid") and nnz <= _INDEX_LIMIT_INT32 // 2 and \
+            int(n_cols) <= (1 << 27) and int(rowptr.numel()) > 1:
         try:
+            if mode != "xcs-l2":
+                rp = rowptr.to(torch.int64)
+                lengths = rp[1:] - rp[:-1]
+                long_mask = lengths >= panel_row_min(n_cols, data.element_size())
+                long_nnz = int(lengths[long_mask].sum().item())
+                if long_nnz > 0 and (mode == "xcs-hybrid" or long_nnz >= PANEL_MIN_SHARE * nnz):
+                    return XcsHybridLayout(data, cols, rowptr, n_cols, long_mask,
+                                           FORCE_PANELS_PER_XCD)
             return XcsLayout(data, cols, rowptr, n_cols, FORCE_PANELS_PER_XCD)
         except ValueError:
             pass  # too large for the packing: row blocks
     return RowBlockLayout(data, cols, rowptr)
 
 
-__all__ = ["RowBlockLayout", "XcsLayout", "build_layout", "prefers_xcs", "sample_indices",
-           "FORCE"]
-del ctypes
+__all__ = ["RowBlockLayout", "XcsLayout", "PanelLayout", "XcsHybridLayout", "build_layout",
+           "prefers_xcs", "sample_indices", "FORCE"]

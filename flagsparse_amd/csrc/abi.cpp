@@ -27,7 +27,7 @@ using namespace fsp;
 
 extern "C" const char* fsp_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int fsp_abi_version(void) { return 3; }
+extern "C" int fsp_abi_version(void) { return 4; }
 
 extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }
@@ -35,6 +35,8 @@ extern "C" int64_t fsp_spmv_chunk_nnz_cap(void) { return kSpmvChunkCap; }
 extern "C" int64_t fsp_spmm_block_nnz_cap(void) { return kSpmmNnzCap; }
 extern "C" int64_t fsp_xcs_item_cap(void) { return kXcsItemCap; }
 extern "C" int64_t fsp_xcs_rows_cap(void) { return kXcsRowsCap; }
+extern "C" int64_t fsp_panel_bytes_cap(void) { return kPanelBytes; }
+extern "C" int64_t fsp_panel_chunk(void) { return kPanelChunk; }
 
 extern "C" int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
                                    int64_t rows_cap, int64_t long_threshold, int64_t chunk,

@@ -20,6 +20,8 @@ constexpr int64_t kSpmmSlots = 2048;                     // LDS (col, val) slots
 constexpr int64_t kSpmmNnzCap = kSpmmSlots - 3;
 constexpr int64_t kXcsItemCap = 2048;                    // entries of one XCS item
 constexpr int64_t kXcsRowsCap = 8192;                    // rows of one XCS tile
+constexpr int64_t kPanelBytes = 65536;                   // x panel copied to LDS (panel SpMV)
+constexpr int64_t kPanelChunk = 512;                     // entries per wave chunk (panel SpMV)
 
 // Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).
 int fill_zero_f32(float* y, int64_t n, hipStream_t st);

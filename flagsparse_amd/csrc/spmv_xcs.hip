@@ -25,6 +25,18 @@
 //           No workgroup waits for or signals another: a device-scope fence would write back
 //           and invalidate the XCD's L2, which holds the x panel this layout exists to keep.
 //
+// Long rows of power-law matrices also have a second layout, "panels" (spmv_panel_kernel):
+// x is cut into panels of 2^col_bits columns, at most 64 KiB each, and a row with many entries
+// per panel gets them gathered from an LDS copy of the panel instead of from L2:
+//   entries  the long rows' entries ordered by (panel, row), each panel's run padded with
+//            zero entries of its last row to a multiple of kPanelChunk (pidx as above, the row
+//            being the index in the list of long rows)
+//   chunks   kPanelChunk consecutive entries, one wave's unit of work; chunk_slot[c] is the
+//            first partial slot of chunk c, which has one slot per run (row) it holds
+//   jobs     workgroup j copies panel job_panel[j] into LDS and its waves take the chunks
+//            [jobs[j], jobs[j+1]) in turn; no barrier after the copy
+// Each long row's slots are then added by panel_combine_kernel (one wave per row, fixed order).
+//
 // Reference behaviour followed (src/flagsparse/sparse_operations/): spmv_csr.py:94-120 (row
 // sums; fp32 summed in fp64 on the default path, :498-536) and :161-279 (opt path, native
 // accumulation); spmv_coo.py:51-108 (one output per row run).
@@ -280,6 +292,109 @@ __global__ __launch_bounds__(kBlock) void xcs_split_combine_kernel(
   y[row_map ? row_map[row] : row] = T(acc);
 }
 
+// Panel layout (see the file comment): one workgroup per job, waves independent after the
+// panel copy.  A wave's chunk: lane L holds entries [8L, 8L + 8), their rows non-decreasing;
+// the runs that end in a lane are emitted by it, the first one with the carry from the lanes
+// before (a segmented wave scan), into consecutive slots from chunk_slot[c] in entry order.
+constexpr int kPanelBlock = 512;
+constexpr int kPanelPerLane = (int)kPanelChunk / kWave;
+static_assert(kPanelPerLane == 8, "eight entries per lane");
+
+template <typename T, typename A>
+__global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
+    const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
+    const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
+    const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
+    A* __restrict__ partials) {
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  T* const sx = reinterpret_cast<T*>(s_dyn);
+  const int job = blockIdx.x;
+  const int64_t pbase = (int64_t)job_panel[job] << col_bits;
+  const int64_t rest = x_len - pbase;
+  const int width = rest < ((int64_t)1 << col_bits) ? (int)rest : (1 << col_bits);
+  for (int i = threadIdx.x; i < width; i += kPanelBlock) sx[i] = x[pbase + i];
+  __syncthreads();
+
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  const uint32_t cmask = (1u << col_bits) - 1u;
+  const int c_hi = jobs[job + 1];
+  for (int ch = jobs[job] + wid; ch < c_hi; ch += kPanelBlock / kWave) {
+    const int64_t e = (int64_t)ch * kPanelChunk + kPanelPerLane * lane;
+    T v[kPanelPerLane];
+    uint32_t c[kPanelPerLane];
+#pragma unroll
+    for (int h = 0; h < kPanelPerLane / 4; ++h) {
+      if constexpr (sizeof(T) == 4) {
+        const f32x4 vv = *reinterpret_cast<const f32x4*>(vals + e + 4 * h);
+        v[4 * h] = vv.x; v[4 * h + 1] = vv.y; v[4 * h + 2] = vv.z; v[4 * h + 3] = vv.w;
+      } else {
+        const f64x2 a = *reinterpret_cast<const f64x2*>(vals + e + 4 * h);
+        const f64x2 b = *reinterpret_cast<const f64x2*>(vals + e + 4 * h + 2);
+        v[4 * h] = a.x; v[4 * h + 1] = a.y; v[4 * h + 2] = b.x; v[4 * h + 3] = b.y;
+      }
+      const i32x4 cc = *reinterpret_cast<const i32x4*>(pidx + e + 4 * h);
+      c[4 * h] = (uint32_t)cc.x; c[4 * h + 1] = (uint32_t)cc.y;
+      c[4 * h + 2] = (uint32_t)cc.z; c[4 * h + 3] = (uint32_t)cc.w;
+    }
+    A prod[kPanelPerLane];
+    int row[kPanelPerLane];
+#pragma unroll
+    for (int q = 0; q < kPanelPerLane; ++q) {
+      prod[q] = A(v[q]) * A(sx[c[q] & cmask]);
+      row[q] = (int)(c[q] >> col_bits);
+    }
+    constexpr int kLast = kPanelPerLane - 1;
+    int prev_row = __shfl_up(row[kLast], 1, kWave);
+    if (lane == 0) prev_row = -1;  // a chunk starts a run
+    int next_row = __shfl_down(row[0], 1, kWave);
+    if (lane == kWave - 1) next_row = -1;  // and ends one
+    const bool cont = row[0] == prev_row;
+    int has_head = cont ? 0 : 1;
+    int n_end = row[kLast] != next_row ? 1 : 0;
+    A piece = A(0);
+#pragma unroll
+    for (int q = 0; q < kPanelPerLane; ++q) {
+      if (q > 0 && row[q] != row[q - 1]) {
+        has_head = 1;
+        ++n_end;
+        piece = A(0);
+      }
+      piece += prod[q];
+    }
+    // segmented scan of (has_head, last piece) and a plain scan of n_end over the wave
+    int h_in = has_head;
+    A v_in = piece;
+    int c_in = n_end;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int ho = __shfl_up(h_in, off, kWave);
+      const A vo = __shfl_up(v_in, off, kWave);
+      const int co = __shfl_up(c_in, off, kWave);
+      if (lane >= off) {
+        if (!h_in) v_in = vo + v_in;
+        h_in |= ho;
+        c_in += co;
+      }
+    }
+    A carry = __shfl_up(v_in, 1, kWave);
+    int slot = __shfl_up(c_in, 1, kWave);
+    if (lane == 0) { carry = A(0); slot = 0; }
+    A* out = partials + chunk_slot[ch] + slot;
+    bool first = true;
+    A run = A(0);
+#pragma unroll
+    for (int q = 0; q < kPanelPerLane; ++q) {
+      if (q > 0 && row[q] != row[q - 1]) {
+        *out++ = (first && cont) ? carry + run : run;
+        first = false;
+        run = A(0);
+      }
+      run += prod[q];
+    }
+    if (row[kLast] != next_row) *out = (first && cont) ? carry + run : run;
+  }
+}
+
 template <typename T, typename A>
 int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
                const int32_t* row_map, const int32_t* items, int64_t n_slots,
@@ -297,6 +412,58 @@ int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void*
                      st, split_rows, split_ptr, slots, static_cast<const A*>(partials),
                      static_cast<T*>(y), row_map, (int)n_split);
   return check_hip(hipGetLastError(), "xcs_split_combine_kernel launch");
+}
+
+// Second pass of the panel layout: its rows have hundreds of slots each, so one wave adds a
+// row's slots - lane l the slots k = l, l + 64, ... in order, then a fixed wave tree.
+template <typename T, typename A>
+__global__ __launch_bounds__(kBlock) void panel_combine_kernel(
+    const int* __restrict__ rows, const int* __restrict__ row_ptr, const int* __restrict__ slots,
+    const A* __restrict__ partials, T* __restrict__ y, const int* __restrict__ row_map,
+    int n_rows) {
+  const int i = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x / kWave);
+  if (i >= n_rows) return;  // whole waves leave together
+  const int lane = threadIdx.x & (kWave - 1);
+  const int a = row_ptr[i], b = row_ptr[i + 1];
+  A acc = A(0);
+  constexpr int kU = 4;  // slot indices, then partials, requested kU at a time
+  for (int k0 = a + lane; k0 < b; k0 += kU * kWave) {
+    int sl[kU];
+    A pv[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) sl[u] = k0 + u * kWave < b ? slots[k0 + u * kWave] : -1;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) pv[u] = sl[u] >= 0 ? partials[sl[u]] : A(0);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) acc += pv[u];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    const int row = rows[i];
+    y[row_map ? row_map[row] : row] = T(acc);
+  }
+}
+
+template <typename T, typename A>
+int launch_panels(const void* vals, const uint32_t* pidx, int col_bits, const void* x,
+                  int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
+                  const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_slot,
+                  void* partials, const int32_t* rows, const int32_t* row_ptr,
+                  const int32_t* slots, int64_t n_rows, hipStream_t st) {
+  if (n_jobs > 0) {
+    hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
+                       ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
+                       pidx, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
+                       chunk_slot, static_cast<A*>(partials));
+    int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
+    if (rc) return rc;
+  }
+  if (n_rows == 0) return FSP_OK;
+  const int64_t blocks = (n_rows + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL((panel_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                     rows, row_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
+                     row_map, (int)n_rows);
+  return check_hip(hipGetLastError(), "panel_combine_kernel launch");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -342,4 +509,45 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
   }
   return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
                                     partials, split_rows, split_ptr, slots, n_split, st);
+}
+
+extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
+                               int64_t n_entries, int col_bits, const void* x, int64_t x_len,
+                               void* y, const int32_t* row_map, const int32_t* jobs,
+                               const int32_t* job_panel, int64_t n_jobs,
+                               const int32_t* chunk_slot, void* partials, const int32_t* rows,
+                               const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                               void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64)
+    return set_error(FSP_ENOTSUP, "fsp_spmv_panels: dtype");
+  const int64_t vsize = dtype == FSP_F32 ? 4 : 8;
+  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: negative size");
+  if (n_entries % kPanelChunk != 0 || n_entries / kPanelChunk > 0x7fffffffLL ||
+      n_jobs > 0x7fffffffLL || n_rows > 0x7fffffffLL - kBlock)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: n_entries must be a multiple of " +
+                                     std::to_string(kPanelChunk) + " and sizes within int32");
+  if (col_bits < 1 || (vsize << col_bits) > kPanelBytes)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: a panel of 2^col_bits values must fit " +
+                                     std::to_string(kPanelBytes) + " bytes of LDS");
+  if (n_jobs > 0 && (!vals || !pidx || !x || !jobs || !job_panel || !chunk_slot || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: null pointer");
+  if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: null row pointer");
+  if (!aligned16(vals) || !aligned16(pidx))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: vals and pidx must be 16-byte aligned");
+  if (n_jobs == 0 && n_rows == 0) return FSP_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == FSP_F32) {
+    if (acc_f64)
+      return launch_panels<float, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+                                          job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
+                                          slots, n_rows, st);
+    return launch_panels<float, float>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+                                       job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
+                                       slots, n_rows, st);
+  }
+  return launch_panels<double, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+                                       job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
+                                       slots, n_rows, st);
 }

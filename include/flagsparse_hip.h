@@ -26,6 +26,8 @@
  *                          spmv_coo.py:254-268) for matrices whose x does not fit one XCD's L2:
  *                          columns split into one panel per XCD (layout built by the prepare
  *                          step, flagsparse_amd/_spmv_layouts.py).
+ *   fsp_spmv_panels      - the same launches, for the long rows of power-law matrices (x panels
+ *                          copied to LDS); used together with fsp_spmv_xcs.
  *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
  *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
  *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
@@ -70,6 +72,8 @@ int64_t fsp_spmv_chunk_nnz_cap(void);    /* max nnz of one long-row chunk       
 int64_t fsp_spmm_block_nnz_cap(void);    /* max nnz of one SpMM row block / row part  */
 int64_t fsp_xcs_item_cap(void);          /* max entries of one XCS item               */
 int64_t fsp_xcs_rows_cap(void);          /* max rows of one XCS tile                  */
+int64_t fsp_panel_bytes_cap(void);       /* max bytes of one x panel (panel SpMV)     */
+int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)            */
 
 /*
  * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
@@ -169,6 +173,33 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
                  const uint32_t* masks, void* partials, const int32_t* split_rows,
                  const int32_t* split_ptr, const int32_t* slots, int64_t n_split, void* stream);
+
+/*
+ * y[rows[i]] (y[row_map[rows[i]]] when row_map != NULL) = row i of A @ x for the long rows of
+ * a matrix in the panel layout: x is cut into panels of 2^col_bits columns, copied one at a
+ * time into LDS, and the gathers read LDS.  Same reference launches as fsp_spmv_csr; used
+ * beside fsp_spmv_xcs for power-law matrices, whose long rows put many entries in every panel.
+ *   vals, pidx   n_entries entries (a multiple of fsp_panel_chunk(), 16-byte aligned) in
+ *                (panel, row) order, each panel's run padded with val 0 entries of its last
+ *                row: pidx = (i << col_bits) | (column - panel * 2^col_bits), i the index of
+ *                the row in rows
+ *   col_bits     2^col_bits values must fit fsp_panel_bytes_cap() bytes
+ *   jobs         n_jobs + 1 increasing chunk indices: workgroup j copies panel job_panel[j] of
+ *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])
+ *   chunk_slot   per chunk the first partial slot (8 bytes each); a chunk writes one slot per
+ *                row it holds, in entry order
+ *   rows, row_ptr, slots
+ *                n_rows long rows; rows[i] gets the sum of partials[slots[k]], k in
+ *                [row_ptr[i], row_ptr[i+1]) (a second launch, one wave per row: lane l adds
+ *                k = l, l + 64, ... in order, then a fixed tree).  Calls sharing partials must
+ *                not overlap.  Other rows of y are not written.
+ */
+int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
+                    int64_t n_entries, int col_bits, const void* x, int64_t x_len, void* y,
+                    const int32_t* row_map, const int32_t* jobs, const int32_t* job_panel,
+                    int64_t n_jobs, const int32_t* chunk_slot, void* partials,
+                    const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
+                    int64_t n_rows, void* stream);
 
 /*
  * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)

@@ -198,3 +198,18 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert L.fsp_spmv_xcs(0, 0, None, None, 0, 25, None, None, None, 0, None, 0, None, None, None,
                           None, None, 0, None) == -1  # col_bits > 24
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1
+
+    def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0):
+        return L.fsp_spmv_panels(dtype, 0, None, None, n_entries, col_bits, None, 1, None, None,
+                                 None, None, n_jobs, None, None, None, None, None, n_rows, None)
+
+    assert panels() == 0                          # nothing to run
+    assert panels(dtype=5) == -3
+    assert panels(n_entries=100) == -1            # not a whole number of chunks
+    assert b"multiple" in L.fsp_last_error()
+    assert panels(col_bits=15) == -1              # 2^15 fp32 > 64 KiB of LDS
+    assert panels(dtype=1, col_bits=14) == -1     # 2^14 fp64 > 64 KiB
+    assert b"LDS" in L.fsp_last_error()
+    assert panels(n_entries=512, n_jobs=1) == -1  # jobs without arrays
+    assert panels(n_rows=3) == -1                 # combine without its arrays
+    assert b"null" in L.fsp_last_error()

@@ -1,6 +1,7 @@
 """SpMV through the XCD column-split layout on the GPU (spmv_xcs_kernel), forced for every
-matrix here, against the fp64 CPU oracle; the automatic choice is checked to pick it for
-random-column matrices and to keep row blocks for banded ones.
+matrix here - alone, and as the hybrid with the long rows in the panel layout - against the fp64
+CPU oracle; the automatic choice is checked to pick it for random-column matrices (the hybrid
+for a power law) and to keep row blocks for banded ones.
 
 Bars as for the row-block kernel: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
 allclose ratio, and for the default float32 path at most 1 ulp from float32(fp64 oracle).
@@ -17,12 +18,18 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def force_xcs():
-    old = _spmv_layouts.FORCE
-    _spmv_layouts.FORCE = "xcs"
-    yield
-    _spmv_layouts.FORCE = old
+@pytest.fixture(params=["xcs-l2", "xcs-hybrid"])
+def force_xcs(request, monkeypatch):
+    # the hybrid with rows of >= 32 entries in the panel part, so that these small matrices
+    # have long rows in every case that checks the layout kind
+    monkeypatch.setattr(_spmv_layouts, "FORCE", request.param)
+    if request.param == "xcs-hybrid":
+        monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    return request.param
+
+
+def _kind(mode):
+    return "xcs" if mode == "xcs-l2" else "xcs-hybrid"
 
 
 def _ulp(a, b):
@@ -56,9 +63,9 @@ def _csr_from_lengths(lengths, n_cols, seed, dtype):
 @pytest.mark.parametrize("use_opt", [False, True])
 def test_powerlaw(dev, force_xcs, dtype, use_opt):
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 17, cap=60000, dtype=dtype)
-    print(f"xcs powerlaw {dtype} use_opt={use_opt}", flush=True)
+    print(f"xcs powerlaw {force_xcs} {dtype} use_opt={use_opt}", flush=True)
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
-    assert p._kernel(use_opt).kind == "xcs"
+    assert p._kernel(use_opt).kind == _kind(force_xcs)
     y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
     _check(y, oracle.spmv_csr(ptr, idx, data, x),
            exact_fp32=(dtype == torch.float32 and not use_opt))
@@ -100,7 +107,7 @@ def test_coo_runs(dev, force_xcs, dtype):
     data, row, col, x, shape = synthetic.coo_uniform(1 << 17, 40 << 16, dtype=dtype)
     ref = oracle.spmv_coo(row, col, data, x, shape[0])
     p = fs.prepare_spmv_coo(data.to(dev), row.to(dev), col.to(dev), shape)
-    assert p._run_layout().kind == "xcs"
+    assert p._run_layout().kind == _kind(force_xcs)
     _check(fs.flagsparse_spmv_coo(x=x.to(dev), prepared=p), ref)
     # rows without entries (run -> row map path)
     keep = (row % 3) != 0
@@ -113,9 +120,15 @@ def test_coo_runs(dev, force_xcs, dtype):
 def test_automatic_choice(dev):
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=5000)  # x: 8 MiB
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
-    assert p._kernel(False).kind == "xcs"
+    assert p._kernel(False).kind in ("xcs", "xcs-hybrid")
     _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
            exact_fp32=True)
     d, i, pp, xx, sh = synthetic.csr_poisson2d(1024)
     p = fs.prepare_spmv_csr(d.to(dev), i.to(dev), pp.to(dev), sh)
     assert p._kernel(False).kind == "rowblock"
+    # a heavier tail (cap 200000 as cfg3): most entries in long rows -> the hybrid
+    data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=200000)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
+    assert p._kernel(False).kind == "xcs-hybrid"
+    _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
+           exact_fp32=True)

@@ -1,15 +1,20 @@
-"""The XCD column-split SpMV layout (flagsparse_amd/_spmv_layouts.py), built on the CPU and
-checked without a GPU: structural invariants the kernel relies on (every entry exactly once,
-item capacity and alignment, in-bounds packed indices, panel-to-XCD slot order), and a
-step-by-step emulation of spmv_xcs_kernel's semantics over the layout (direct rows, split-row
-partials added in item order, empty rows) against the fp64 oracle."""
+"""The XCD column-split and panel SpMV layouts (flagsparse_amd/_spmv_layouts.py), built on the
+CPU and checked without a GPU: structural invariants the kernels rely on (every entry exactly
+once, item capacity and alignment, in-bounds packed indices, panel-to-XCD slot order; for
+panels, chunk-aligned panel runs padded with zero entries of their last row, jobs inside one
+panel, chunk slot offsets), and step-by-step emulations of spmv_xcs_kernel's and
+spmv_panel_kernel's semantics over the layouts (direct rows, split-row partials added in
+order, empty rows) - for the hybrid, the XCS part and then the panel part - against the fp64
+oracle."""
 
 import numpy as np
 import pytest
 import torch
 
 from flagsparse_amd import _abi, synthetic
-from flagsparse_amd._spmv_layouts import XcsLayout, prefers_xcs, sample_indices
+from flagsparse_amd import _spmv_layouts
+from flagsparse_amd._spmv_layouts import (PanelLayout, XcsHybridLayout, XcsLayout,
+                                          panel_row_min, prefers_xcs, sample_indices)
 from oracle import oracle
 
 
@@ -25,14 +30,16 @@ def _item_positions(e0, ln):
     return e0 + 4 * (lq // qp + nt * (lq % qp)) + o % 4
 
 
-def _emulate(layout, x, acc=np.float64):
-    """numpy restatement of spmv_xcs_kernel + xcs_split_combine_kernel over the layout."""
+def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
+    """numpy restatement of spmv_xcs_kernel + xcs_split_combine_kernel over the layout; layout
+    row r is written to y[row_map[r]] when a row map is given."""
     items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
     masks = layout.masks.numpy().view(np.uint32)
     vals = layout.vals.numpy().astype(acc)
     pidx = layout.pidx.numpy().view(np.uint32)
     cbits = layout.col_bits
-    y = np.full(layout.n_rows, np.nan)
+    out = (lambda r: r) if row_map is None else (lambda r: int(row_map[r]))  # noqa: E731
+    y = np.full(layout.n_rows, np.nan) if y is None else y
     partials = np.full(max(layout.n_partials, 1), np.nan)
     written = np.zeros(max(layout.n_partials, 1), dtype=bool)
     for e0, ln, k, _, r0, R, cbase, moff, plo, phi, tile, _ in items:
@@ -51,7 +58,7 @@ def _emulate(layout, x, acc=np.float64):
         for r in range(R):
             if empty(r):
                 if k == 0:
-                    y[r0 + r] = 0.0
+                    y[out(r0 + r)] = 0.0
                 continue
             sel = prod[lrow == r]
             if not sel.size:
@@ -65,8 +72,8 @@ def _emulate(layout, x, acc=np.float64):
                 written[slot] = True
                 slot += 1
             else:
-                assert np.isnan(y[r0 + r])  # a direct row is written by one item only
-                y[r0 + r] = s
+                assert np.isnan(y[out(r0 + r)])  # a direct row is written by one item only
+                y[out(r0 + r)] = s
     assert written[:layout.n_partials].all()
     # second pass: each split row sums its slots in the listed (item) order
     split_rows = layout.split_rows.numpy()
@@ -76,7 +83,7 @@ def _emulate(layout, x, acc=np.float64):
         s = acc(0)
         for j in range(sptr[i], sptr[i + 1]):
             s = acc(s + partials[slots[j]])
-        y[row] = s
+        y[out(row)] = s
     return y
 
 
@@ -114,6 +121,76 @@ def _check_structure(layout, data, cols, rowptr):
     rp = rowptr.numpy()
     want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
             for i in range(rp[r], rp[r + 1])]
+    assert sorted(got) == sorted(want)
+
+
+def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
+    """numpy restatement of spmv_panel_kernel + the combine over a PanelLayout: each chunk's
+    runs (a chunk start or a row change starts one) go to consecutive slots from
+    chunk_slot[c]; row i of the layout then gets its slots' sum in slot order."""
+    chunk = _abi.caps()["panel_chunk"]
+    cb = layout.col_bits
+    vals = layout.vals.numpy().astype(acc)[:layout.n_entries]
+    pidx = layout.pidx.numpy().view(np.uint32)[:layout.n_entries].astype(np.int64)
+    jobs = layout.jobs.numpy()
+    jp = layout.job_panel.numpy()
+    cslot = layout.chunk_slot.numpy()
+    partials = np.full(max(layout.n_partials, 1), np.nan)
+    for j in range(layout.n_jobs):
+        base = int(jp[j]) << cb
+        for c in range(jobs[j], jobs[j + 1]):
+            sl = int(cslot[c])
+            e = np.arange(c * chunk, (c + 1) * chunk)
+            rows = pidx[e] >> cb
+            cols = base + (pidx[e] & ((1 << cb) - 1))
+            prod = vals[e] * x[np.minimum(cols, x.size - 1)].astype(acc)
+            assert np.all(cols[vals[e] != 0] < x.size)
+            s = acc(0)
+            for q in range(chunk):
+                if q > 0 and rows[q] != rows[q - 1]:
+                    partials[sl] = s
+                    sl += 1
+                    s = acc(0)
+                s = acc(s + prod[q])
+            partials[sl] = s
+            assert c + 1 == len(cslot) or sl + 1 == cslot[c + 1]
+    out = layout.rows.numpy() if row_map is None else row_map[layout.rows.numpy()]
+    rp = layout.row_ptr.numpy()
+    slots = layout.slots.numpy()
+    for i in range(layout.n_rows):
+        s = acc(0)
+        for k in range(rp[i], rp[i + 1]):
+            s = acc(s + partials[slots[k]])
+        y[out[i]] = s
+    return y
+
+
+def _check_panels(layout, data, cols, rowptr):
+    """Panel runs chunk-aligned and padded with zero entries of their last row; jobs of one
+    panel covering every chunk once; every entry exactly once; the x panel fits the LDS copy."""
+    caps = _abi.caps()
+    chunk = caps["panel_chunk"]
+    cb = layout.col_bits
+    assert (1 << cb) * layout.vals.element_size() <= caps["panel_bytes"]
+    assert layout.n_entries % chunk == 0
+    jobs, jp = layout.jobs.numpy().astype(np.int64), layout.job_panel.numpy()
+    assert jobs[0] == 0 and jobs[-1] == layout.n_entries // chunk
+    assert np.all(np.diff(jobs) >= 1)
+    assert np.all(np.diff(jobs) <= _spmv_layouts.PANEL_JOB_CHUNKS)
+    assert np.all(np.diff(jp) >= 0)
+    pidx = layout.pidx.numpy().view(np.uint32)[:layout.n_entries].astype(np.int64)
+    vals = layout.vals.numpy()[:layout.n_entries]
+    got = []
+    for j in range(layout.n_jobs):
+        e = np.arange(jobs[j] * chunk, jobs[j + 1] * chunk)
+        rows = pidx[e] >> cb
+        assert np.all(np.diff(rows) >= 0)  # a job lies in one panel, whose rows ascend
+        cols_e = (int(jp[j]) << cb) + (pidx[e] & ((1 << cb) - 1))
+        real = vals[e] != 0
+        got += list(zip(rows[real].tolist(), cols_e[real].tolist(), vals[e][real].tolist()))
+    rp = rowptr.numpy()
+    want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
+            for i in range(rp[r], rp[r + 1]) if float(data[i]) != 0.0]
     assert sorted(got) == sorted(want)
 
 
@@ -173,6 +250,54 @@ def test_xcs_skewed_columns_and_empty_matrix():
     ip0 = torch.zeros(5001, dtype=torch.int64)
     lay = XcsLayout(torch.empty(0), torch.empty(0, dtype=torch.int32), ip0, 100)
     assert np.all(_emulate(lay, np.ones(100)) == 0.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_panel_layout(dtype, monkeypatch):
+    # long rows over 200k columns (13 or 12 bits per panel), jobs cut at PANEL_JOB_CHUNKS
+    monkeypatch.setattr(_spmv_layouts, "PANEL_JOB_CHUNKS", 3)
+    lengths = [9000, 20000, 5000, 0, 12000, 30000, 7]
+    vals, cols, ip, x = _case(lengths, 200000, 6, dtype)
+    rows = torch.arange(len(lengths)) * 3 + 1  # output rows of the layout's rows
+    lay = PanelLayout(vals, cols, ip, 200000, rows)
+    assert lay.n_jobs > lay.n_panels
+    _check_panels(lay, vals, cols, ip)
+    y = np.full(3 * len(lengths) + 1, np.nan)
+    _emulate_panels(lay, x.numpy(), y)
+    np.testing.assert_allclose(y[rows.numpy()], oracle.spmv_csr(ip, cols, vals, x),
+                               rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_xcs_hybrid(seed):
+    rng = np.random.default_rng(seed)
+    n_cols = 300000
+    lengths = rng.zipf(1.6, 5000).clip(max=40000)
+    lengths[rng.integers(0, 5000, 300)] = 0
+    vals, cols, ip, x = _case(lengths, n_cols, seed)
+    long_mask = torch.as_tensor(lengths >= panel_row_min(n_cols, 4))
+    assert 0 < int(long_mask.sum()) < 5000
+    h = XcsHybridLayout(vals, cols, ip, n_cols, long_mask)
+    assert h.short.nnz + h.long.nnz == vals.numel()
+    _check_panels(h.long, *_long_part(vals, cols, ip, long_mask))
+    y = _emulate(h.short, x.numpy())
+    assert np.all(np.isnan(y[long_mask.numpy()]))  # long rows: left to the panel part
+    y = _emulate_panels(h.long, x.numpy(), y)
+    np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
+    # through a row map (COO row runs): layout row r is output row map[r]
+    rmap = np.arange(5000) * 2
+    y2 = _emulate(h.short, x.numpy(), y=np.full(10000, np.nan), row_map=rmap)
+    y2 = _emulate_panels(h.long, x.numpy(), y2, row_map=rmap)
+    np.testing.assert_array_equal(y2[rmap], y)
+
+
+def _long_part(vals, cols, ip, long_mask):
+    """The compacted CSR of the long rows (the panel part's input)."""
+    lengths = ip[1:] - ip[:-1]
+    entry_long = torch.repeat_interleave(long_mask, lengths)
+    lp = torch.zeros(int(long_mask.sum()) + 1, dtype=torch.int64)
+    lp[1:] = torch.cumsum(lengths[long_mask], 0)
+    return vals[entry_long], cols[entry_long], lp
 
 
 def test_layout_choice():

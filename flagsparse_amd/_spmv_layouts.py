@@ -401,6 +401,14 @@ def panel_row_min(n_cols, value_bytes):
     return PANEL_RUNS * max(1, n_panels)
 
 
+def panel_storage_positions(n_entries, chunk, device):
+    """Memory position of each logical entry of the panel layout: inside a chunk, lane L's
+    h-th quad (logical quad 2L + h) is stored at quad 64h + L."""
+    p = torch.arange(n_entries, device=device)
+    lq = (p % chunk) // 4
+    return (p // chunk) * chunk + ((lq % 2) * (chunk // 8) + lq // 2) * 4 + p % 4
+
+
 class PanelLayout:
     """Rows whose x gathers are served from LDS copies of 64 KiB x panels (module docstring).
     ``rows`` are the output rows of the CSR rows given; built on the device."""
@@ -433,8 +441,8 @@ class PanelLayout:
         n_entries = int(padded.sum().item())
         dest = seg[panel] + torch.arange(self.nnz, device=dev) - first[panel]
         row_s = row[order]
-        self.vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
-        self.vals[dest] = data[order]
+        vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
+        vals[dest] = data[order]
         # padding: value 0 in the last row of its panel, so it adds no run
         last = torch.zeros(n_panels, dtype=torch.int64, device=dev)
         has = cnt > 0
@@ -458,10 +466,14 @@ class PanelLayout:
         torch.cumsum(torch.bincount(slot_row, minlength=n_rows), 0, out=row_ptr[1:])
         self.row_ptr = row_ptr.to(torch.int32).contiguous()
         self.n_rows = n_rows
-        self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
-        if self.pidx.numel() < 4:
-            self.pidx = torch.zeros(4, dtype=torch.int32, device=dev)
-        del pidx, rowpos, starts, slot_row
+        # storage order inside a chunk: logical quad 2L + h at quad 64h + L
+        mem = panel_storage_positions(n_entries, chunk, dev)
+        self.vals = torch.zeros_like(vals)
+        self.vals[mem] = vals[:n_entries]
+        packed = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
+        self.pidx = torch.zeros(max(n_entries, 4), dtype=torch.int32, device=dev)
+        self.pidx[mem] = packed
+        del pidx, rowpos, starts, slot_row, vals, packed, mem
         # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
         # sizes keep the rounds of workgroups even)
         per_panel = padded // chunk

@@ -30,7 +30,9 @@
 // per panel gets them gathered from an LDS copy of the panel instead of from L2:
 //   entries  the long rows' entries ordered by (panel, row), each panel's run padded with
 //            zero entries of its last row to a multiple of kPanelChunk (pidx as above, the row
-//            being the index in the list of long rows)
+//            being the index in the list of long rows); inside a chunk, logical quad 2L + h
+//            (lane L's h-th quad) is stored at quad h * 64 + L, so each 16-byte load of a
+//            wave reads one contiguous kilobyte
 //   chunks   kPanelChunk consecutive entries, one wave's unit of work; chunk_slot[c] is the
 //            first partial slot of chunk c, which has one slot per run (row) it holds
 //   jobs     workgroup j copies panel job_panel[j] into LDS and its waves take the chunks
@@ -318,24 +320,40 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const uint32_t cmask = (1u << col_bits) - 1u;
   const int c_hi = jobs[job + 1];
-  for (int ch = jobs[job] + wid; ch < c_hi; ch += kPanelBlock / kWave) {
-    const int64_t e = (int64_t)ch * kPanelChunk + kPanelPerLane * lane;
-    T v[kPanelPerLane];
-    uint32_t c[kPanelPerLane];
+  // The entries are streamed once with non-temporal loads, and the next chunk's loads are
+  // issued before the current chunk is reduced, so a wave keeps two chunks in flight.
+  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], uint32_t (&c)[kPanelPerLane]) {
+    const int64_t e0 = (int64_t)chunk * kPanelChunk;
 #pragma unroll
     for (int h = 0; h < kPanelPerLane / 4; ++h) {
+      const int64_t m = e0 + 4 * (h * kWave + lane);  // logical quad 2 * lane + h
       if constexpr (sizeof(T) == 4) {
-        const f32x4 vv = *reinterpret_cast<const f32x4*>(vals + e + 4 * h);
+        const f32x4 vv = ld_stream<true>(reinterpret_cast<const f32x4*>(vals + m));
         v[4 * h] = vv.x; v[4 * h + 1] = vv.y; v[4 * h + 2] = vv.z; v[4 * h + 3] = vv.w;
       } else {
-        const f64x2 a = *reinterpret_cast<const f64x2*>(vals + e + 4 * h);
-        const f64x2 b = *reinterpret_cast<const f64x2*>(vals + e + 4 * h + 2);
+        const f64x2 a = ld_stream<true>(reinterpret_cast<const f64x2*>(vals + m));
+        const f64x2 b = ld_stream<true>(reinterpret_cast<const f64x2*>(vals + m + 2));
         v[4 * h] = a.x; v[4 * h + 1] = a.y; v[4 * h + 2] = b.x; v[4 * h + 3] = b.y;
       }
-      const i32x4 cc = *reinterpret_cast<const i32x4*>(pidx + e + 4 * h);
+      const i32x4 cc = ld_stream<true>(reinterpret_cast<const i32x4*>(pidx + m));
       c[4 * h] = (uint32_t)cc.x; c[4 * h + 1] = (uint32_t)cc.y;
       c[4 * h + 2] = (uint32_t)cc.z; c[4 * h + 3] = (uint32_t)cc.w;
     }
+  };
+  constexpr int kStride = kPanelBlock / kWave;
+  T vn[kPanelPerLane];
+  uint32_t cn[kPanelPerLane];
+  int ch = jobs[job] + wid;
+  if (ch < c_hi) load_chunk(ch, vn, cn);
+  for (; ch < c_hi; ch += kStride) {
+    T v[kPanelPerLane];
+    uint32_t c[kPanelPerLane];
+#pragma unroll
+    for (int q = 0; q < kPanelPerLane; ++q) {
+      v[q] = vn[q];
+      c[q] = cn[q];
+    }
+    if (ch + kStride < c_hi) load_chunk(ch + kStride, vn, cn);
     A prod[kPanelPerLane];
     int row[kPanelPerLane];
 #pragma unroll

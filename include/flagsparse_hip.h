@@ -182,7 +182,8 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  *   vals, pidx   n_entries entries (a multiple of fsp_panel_chunk(), 16-byte aligned) in
  *                (panel, row) order, each panel's run padded with val 0 entries of its last
  *                row: pidx = (i << col_bits) | (column - panel * 2^col_bits), i the index of
- *                the row in rows
+ *                the row in rows; inside each chunk the quad (4 entries) at logical position
+ *                2L + h is stored at quad position 64h + L (L < 64, h < 2)
  *   col_bits     2^col_bits values must fit fsp_panel_bytes_cap() bytes
  *   jobs         n_jobs + 1 increasing chunk indices: workgroup j copies panel job_panel[j] of
  *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])

@@ -130,8 +130,8 @@ def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
     chunk_slot[c]; row i of the layout then gets its slots' sum in slot order."""
     chunk = _abi.caps()["panel_chunk"]
     cb = layout.col_bits
-    vals = layout.vals.numpy().astype(acc)[:layout.n_entries]
-    pidx = layout.pidx.numpy().view(np.uint32)[:layout.n_entries].astype(np.int64)
+    vals, pidx = _panel_logical(layout)
+    vals = vals.astype(acc)
     jobs = layout.jobs.numpy()
     jp = layout.job_panel.numpy()
     cslot = layout.chunk_slot.numpy()
@@ -165,6 +165,18 @@ def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
     return y
 
 
+def _panel_logical(layout):
+    """(vals, pidx as int64) of a PanelLayout in logical order: inside a chunk of 512, lane
+    L's quad h (logical quad 2L + h) is read from quad 64h + L."""
+    n = layout.n_entries
+    p = np.arange(n)
+    lq = (p % 512) // 4
+    mem = (p // 512) * 512 + ((lq % 2) * 64 + lq // 2) * 4 + p % 4
+    return (layout.vals.numpy()[:n][mem] if n else layout.vals.numpy()[:0],
+            layout.pidx.numpy().view(np.uint32)[:n][mem].astype(np.int64) if n else
+            np.zeros(0, np.int64))
+
+
 def _check_panels(layout, data, cols, rowptr):
     """Panel runs chunk-aligned and padded with zero entries of their last row; jobs of one
     panel covering every chunk once; every entry exactly once; the x panel fits the LDS copy."""
@@ -178,8 +190,9 @@ def _check_panels(layout, data, cols, rowptr):
     assert np.all(np.diff(jobs) >= 1)
     assert np.all(np.diff(jobs) <= _spmv_layouts.PANEL_JOB_CHUNKS)
     assert np.all(np.diff(jp) >= 0)
-    pidx = layout.pidx.numpy().view(np.uint32)[:layout.n_entries].astype(np.int64)
-    vals = layout.vals.numpy()[:layout.n_entries]
+    vals, pidx = _panel_logical(layout)
+    assert np.array_equal(np.sort(_spmv_layouts.panel_storage_positions(
+        layout.n_entries, chunk, "cpu").numpy()), np.arange(layout.n_entries))  # a permutation
     got = []
     for j in range(layout.n_jobs):
         e = np.arange(jobs[j] * chunk, jobs[j + 1] * chunk)

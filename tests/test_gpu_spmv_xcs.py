@@ -87,6 +87,28 @@ def test_edges(dev, force_xcs, lengths, dtype):
                exact_fp32=(dtype == torch.float32 and not use_opt))
 
 
+@pytest.mark.parametrize("lengths,n_cols", [
+    ([40] * 3000, 1 << 20),                              # every row long: empty XCS part
+    ([40, 0, 3, 100, 1] * 600, 5000),                    # x of one small panel (13 bits)
+    ([33] * 1000 + [31] * 1000 + [32] * 1000, 70001),    # rows at the threshold; ragged panels
+    ([5000] + [0] * 3000 + [2] * 3000 + [7000], 300000),  # two long rows, short rows between
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype):
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 21, dtype)
+    print(f"hybrid edges rows={len(lengths)} n_cols={n_cols} {dtype}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    assert p._kernel(False).kind == "xcs-hybrid"
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
+        _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))
+    # a second call on the same layout reuses its partial buffers: same result, bit for bit
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=True))
+
+
 def test_unsorted_duplicates_and_truncation(dev, force_xcs):
     data, idx, ptr = synthetic.build_random_csr(60000, 3000000, 400000, torch.float32,
                                                 torch.int64, "cpu", seed=4)

@@ -140,9 +140,7 @@ class XcsLayout:
 
     kind = "xcs"
 
-    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None, skip_rows=None):
-        """``skip_rows``: optional bool mask of rows (without entries here) that another layout
-        writes; they are left alone instead of being written as 0."""
+    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None):
         dev = data.device
         caps = _abi.caps()
         item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
@@ -224,9 +222,6 @@ class XcsLayout:
         cnt = torch.bincount(key_sorted, minlength=n_pieces) if nnz else \
             torch.zeros(n_pieces, dtype=torch.int64, device=dev)
         n_sub = (cnt + item_cap - 1) // item_cap
-        tile_tot = cnt.view(n_tiles, P).sum(1)
-        empty_tiles = tile_tot == 0
-        n_sub.view(n_tiles, P)[:, 0] += empty_tiles.to(n_sub.dtype)  # one dummy item
         n_items = int(n_sub.sum().item())
         piece_first_item = torch.cumsum(n_sub, 0) - n_sub
         base = torch.where(n_sub > 0, cnt // n_sub.clamp(min=1), torch.zeros_like(cnt))
@@ -280,22 +275,12 @@ class XcsLayout:
         self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
         del packed, colp, pan, loc_row, pidx, dest
 
-        # 6. Direct / split / empty rows, the per-tile masks, and the split-row slots: one
-        #    per (item, split row it holds), an item's slots consecutive in row order.
-        row_min = torch.full((n_rows,), n_items, dtype=torch.int64, device=dev)
-        row_max = torch.full((n_rows,), -1, dtype=torch.int64, device=dev)
+        # 6. Partial slots: one per (item, row run it holds), an item's slots consecutive in
+        #    row order; per row its slots in item order (the combine's summation order).
         er = entry_row[perm]
-        if nnz:
-            row_min.scatter_reduce_(0, er, item_of, reduce="amin")
-            row_max.scatter_reduce_(0, er, item_of, reduce="amax")
         del entry_row, perm, key_sorted
-        empty = lengths == 0
-        if skip_rows is not None:
-            empty &= ~skip_rows
-        split = (row_max > row_min) & ~empty
-        sel = split[er]  # sorted entries of split rows, in (item, row) order
-        pair_key = torch.unique_consecutive(item_of[sel] * max(n_rows, 1) + er[sel])
-        del sel, er, item_of
+        pair_key = torch.unique_consecutive(item_of * max(n_rows, 1) + er)  # sorted entries
+        del er, item_of
         pair_item = pair_key // max(n_rows, 1)
         pair_row = pair_key % max(n_rows, 1)
         n_pairs = int(pair_key.numel())
@@ -303,27 +288,15 @@ class XcsLayout:
             torch.zeros(n_items, dtype=torch.int64, device=dev)
         item_slot = torch.cumsum(per_item, 0) - per_item
         by_row = torch.sort(pair_row, stable=True)[1]  # item order kept within a row
-        self.slots = by_row.to(torch.int32).contiguous()
-        self.split_rows = torch.nonzero(split).flatten().to(torch.int32).contiguous()
-        counts = torch.bincount(pair_row, minlength=n_rows)[split.nonzero().flatten()] \
-            if n_pairs else torch.zeros(0, dtype=torch.int64, device=dev)
-        sp = torch.zeros(counts.numel() + 1, dtype=torch.int64, device=dev)
-        sp[1:] = torch.cumsum(counts, 0)
-        self.split_ptr = sp.to(torch.int32).contiguous()
-        self.n_split_rows = int(self.split_rows.numel())
+        self.slots = by_row.to(torch.int32).contiguous() if n_pairs else \
+            torch.zeros(1, dtype=torch.int32, device=dev)
+        rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
+        if n_pairs:
+            torch.cumsum(torch.bincount(pair_row, minlength=n_rows), 0, out=rp[1:])
+        self.row_ptr = rp.to(torch.int32).contiguous()
         self.n_partials = n_pairs
-        del pair_key, pair_item, pair_row, by_row, counts
-        W = (t_R_d + 31) // 32
-        mask_off = torch.cumsum(2 * W, 0) - 2 * W
-        n_words = int((2 * W).sum().item())
-        rows = torch.arange(n_rows, device=dev)
-        lr = rows - t_r0_d[tile_of_row]
-        word = mask_off[tile_of_row] + lr // 32
-        bit = torch.ones_like(lr) << (lr % 32)
-        masks = torch.zeros(max(n_words, 1), dtype=torch.int64, device=dev)
-        masks.scatter_add_(0, word[split], bit[split])
-        masks.scatter_add_(0, (word + W[tile_of_row])[empty], bit[empty])
-        self.masks = torch.where(masks >= (1 << 31), masks - (1 << 32), masks).to(torch.int32)
+        self.n_split_rows = int(((rp[1:] - rp[:-1]) > 1).sum().item()) if n_rows else 0
+        del pair_key, pair_item, pair_row, by_row, rp
 
         # 7. Launch order: XCD x runs the items of panels x, x + 8, x + 16, ... (one panel
         #    after the other, each in tile order); lists padded to the same length q so that
@@ -346,7 +319,7 @@ class XcsLayout:
         d[slot_of] = torch.stack([item_start[it], item_len[it], item_k[it], torch.zeros_like(t),
                                   t_r0_d[t],
                                   t_R_d[t], self.panel_base.to(torch.int64)[item_panel[it]],
-                                  mask_off[t], pb & 0xFFFFFFFF, pb >> 32, t,
+                                  torch.zeros_like(t), pb & 0xFFFFFFFF, pb >> 32, t,
                                   torch.zeros_like(it)], 1)
         d = torch.where(d >= (1 << 31), d - (1 << 32), d)
         self.items = d.to(torch.int32).contiguous()
@@ -374,14 +347,14 @@ class XcsLayout:
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
-                    self.n_slots, p(self.masks), p(self.partials), p(self.split_rows),
-                    p(self.split_ptr), p(self.slots), self.n_split_rows, None]
+                    self.n_slots, p(self.partials), None, p(self.row_ptr), p(self.slots),
+                    self.n_rows, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[7] = x.data_ptr(), y.data_ptr()
         a[8] = None if row_map is None else row_map.data_ptr()
         a[9] = n_out
-        a[18] = _abi.raw_stream(y.device)
+        a[17] = _abi.raw_stream(y.device)
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 
@@ -519,10 +492,10 @@ class PanelLayout:
 
 class XcsHybridLayout:
     """Long rows in a PanelLayout, the rest in an XcsLayout (module docstring).  The XCS part
-    sees the long rows as rows without entries and leaves them alone; the panel part writes
-    them.  The two parts run one after the other: run concurrently on two streams they were
-    slower on MI355X (cfg3 510 us vs 465 us) - the panel part's entry stream evicts the x
-    panels the XCS part keeps in L2."""
+    sees the long rows as rows without entries and writes them as 0; the panel part, launched
+    after it on the same stream, then writes their sums.  Run concurrently on two streams the
+    parts were slower on MI355X (cfg3 510 us vs 465 us): the panel part's entry stream evicts
+    the x panels the XCS part keeps in L2."""
 
     kind = "xcs-hybrid"
 
@@ -535,7 +508,7 @@ class XcsHybridLayout:
         short_ptr = torch.zeros_like(rp)
         torch.cumsum(torch.where(long_mask, 0, lengths), 0, out=short_ptr[1:])
         self.short = XcsLayout(data[~entry_long], cols[~entry_long], short_ptr, n_cols,
-                               panels_per_xcd, skip_rows=long_mask)
+                               panels_per_xcd)
         long_rows = torch.nonzero(long_mask).flatten()
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])

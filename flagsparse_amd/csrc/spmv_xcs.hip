@@ -14,14 +14,15 @@
 //           qp*t + u is at memory quad t + nt*u (coalesced loads, contiguous rows per thread)
 //   pidx    (local row << col_bits) | (column - the panel's first column)
 //   slots   one item descriptor per workgroup in launch order, 12 int32:
-//           {entry start, count, rank k in tile, 0, r0, rows R, panel first column,
-//            mask word offset, first partial slot (2 x int32), tile (-1: empty slot), 0}
-//   rows    "direct" when all of a row's entries lie in one item: that item writes y;
-//           "split" otherwise: every item holding entries of a split row writes that row's sum
-//           to a slot of its own (an item's slots are consecutive, in row order), and a
-//           second launch (xcs_split_combine_kernel) adds each split row's slots in item order
-//           - a fixed order, so the result does not depend on timing; "empty" rows are
-//           written as 0 by the tile's first item.
+//           {entry start, count, rank k in tile, 0, r0, rows R, panel first column, 0,
+//            first partial slot (2 x int32), tile (-1: empty slot), 0}
+//   rows    every item writes the sum of each row run it holds to a partial slot of its own
+//           (an item's slots are consecutive, in row order); a second launch
+//           (xcs_row_combine_kernel) gives every row the sum of its slots in item order - a
+//           fixed order, so the result does not depend on timing - and writes y in row order.
+//           Items never write y themselves: a y line would then be written piecewise by items
+//           on several XCDs, and those partial-line writes cost more than the extra slots
+//           (measured on MI355X: cfg3's short rows 323 -> 243 us without them).
 //           No workgroup waits for or signals another: a device-scope fence would write back
 //           and invalidate the XCD's L2, which holds the x panel this layout exists to keep.
 //
@@ -59,10 +60,6 @@ static_assert(kRowsCap % 32 == 0 && kRowsCap <= 65535, "row ids are kept as 16-b
 // floor(160 KiB / (static + reserve)) = 5.
 constexpr unsigned kXcsLdsReserve = 28u * 1024u;
 
-__device__ __forceinline__ bool mask_bit(const uint32_t* m, int r) {
-  return (m[r >> 5] >> (r & 31)) & 1u;
-}
-
 // Segmented sums over an item: thread t owns a contiguous run of the item's entries, which
 // holds whole runs (rows) and pieces of runs that continue from or into its neighbours.  A
 // workgroup-wide segmented scan over (has a run start, sum of the last run piece) - combine(a,
@@ -71,14 +68,11 @@ __device__ __forceinline__ bool mask_bit(const uint32_t* m, int r) {
 template <typename T, typename A, bool NT>
 __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
-    const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
-    const i32x4* __restrict__ items, int n_slots, const uint32_t* __restrict__ masks,
+    const T* __restrict__ x, const i32x4* __restrict__ items, int n_slots,
     A* __restrict__ partials) {
   constexpr int kPer = kItemCap / kBlock;  // entries per thread at most
   constexpr int kQuads = kPer / 4;
   static_assert(kQuads * 4 == kPer, "whole quads of entries per thread");
-  __shared__ uint32_t s_split[kRowsCap / 32];
-  __shared__ uint32_t s_empty[kRowsCap / 32];
   __shared__ int s_first_row[kWavesPerBlock];
   __shared__ int s_last_row[kWavesPerBlock];
   __shared__ int s_wh[kWavesPerBlock];
@@ -92,17 +86,10 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   const i32x4 d1 = items[3 * slot + 1];
   const i32x4 d2 = items[3 * slot + 2];
   if (d2.z < 0) return;  // empty slot
-  const int e0 = d0.x, len = d0.y, k = d0.z;
-  const int r0 = d1.x, R = d1.y, cbase = d1.z, mask_off = d1.w;
+  const int e0 = d0.x, len = d0.y;
+  const int R = d1.y, cbase = d1.z;
   const int64_t sbase = (int64_t)(((uint64_t)(uint32_t)d2.y << 32) | (uint32_t)d2.x);
   if (R <= 0 || R > kRowsCap || len < 0 || len > kItemCap) return;  // not a planner item
-  const int W = (R + 31) >> 5;
-
-  // Split / empty row masks of the tile, published by the first barrier below.
-  for (int w = tid; w < W; w += kBlock) {
-    s_split[w] = masks[mask_off + w];
-    s_empty[w] = masks[mask_off + W + w];
-  }
 
   // Entries [i0, i0 + nm) of this thread (thread-major storage, see the file comment).
   const int q_tot = (len + 3) >> 2;
@@ -152,7 +139,7 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     if (q < nm) my_last = row[q];
   if (lane == 0) s_first_row[wid] = my_first;
   if (lane == kWave - 1) s_last_row[wid] = my_last;
-  __syncthreads();  // also publishes the masks
+  __syncthreads();
   int prev_row = __shfl_up(my_last, 1, kWave);
   if (lane == 0) prev_row = wid > 0 ? s_last_row[wid - 1] : -1;
   if (tid == 0) prev_row = -1;
@@ -166,33 +153,32 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   // sum of its entries before this chunk - from the scan below.
   //
   // Pass 1 (before the scan): whether a run starts here, the sum of the last run piece (the
-  // scan's input) and how many emitted runs are split rows (each takes one partial slot).
-  // Pass 2 (after it) sums the runs again and emits them.  Nothing but prod and row stays
+  // scan's input) and how many runs end here (each takes one partial slot).  Pass 2 (after
+  // it) sums the runs again and emits them.  Nothing but prod and row stays
   // live across the scan, which keeps the register count, and with it the number of waves in
   // flight per SIMD, up.
   const bool cont = nm > 0 && my_first == prev_row;
   const bool last_ends = nm > 0 && next_row != my_last;
   int has_head = (nm > 0 && !cont) ? 1 : 0;
-  int n_split = 0;
+  int n_end = last_ends ? 1 : 0;
   A piece = A(0);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     if (q < nm) {
       if (q > 0 && row[q] != row[q - 1]) {
         has_head = 1;
-        if (mask_bit(s_split, row[q - 1])) ++n_split;
+        ++n_end;
         piece = A(0);
       }
       piece += prod[q];
     }
   }
-  if (last_ends && mask_bit(s_split, my_last)) ++n_split;
 
   // Workgroup scans, one barrier: segmented scan of (has_head, last piece) gives the carry,
-  // and a plain scan of n_split gives this thread's first slot.
+  // and a plain scan of n_end gives this thread's first slot.
   int h_in = has_head;
   A v_in = piece;
-  int c_in = n_split;
+  int c_in = n_end;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
     const int ho = __shfl_up(h_in, off, kWave);
@@ -224,57 +210,39 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   const A carry = h_ex ? v_ex : pv + v_ex;
   int next_slot = pc + c_ex;
 
-  // Pass 2, in row order: direct rows go to y, split rows to the item's next slot.
-  auto emit = [&](int r, A sum) {
-    if (mask_bit(s_split, r)) {
-      partials[sbase + next_slot] = sum;
-      ++next_slot;
-    } else {
-      const int row_o = r0 + r;
-      y[row_map ? row_map[row_o] : row_o] = T(sum);
-    }
-  };
+  // Pass 2, in row order: each run to the item's next slot.
+  A* out = partials + sbase + next_slot;
   bool first = true;
   A run = A(0);
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     if (q < nm) {
       if (q > 0 && row[q] != row[q - 1]) {
-        emit(row[q - 1], (first && cont) ? carry + run : run);
+        *out++ = (first && cont) ? carry + run : run;
         first = false;
         run = A(0);
       }
       run += prod[q];
     }
   }
-  if (last_ends) emit(my_last, (first && cont) ? carry + run : run);
-
-  // Empty rows: the tile's first item writes y = 0.
-  if (k == 0) {
-    for (int w = tid; w < W; w += kBlock) {
-      uint32_t e = s_empty[w];
-      while (e) {
-        const int b = __ffs(e) - 1;
-        e &= e - 1u;
-        const int row_e = r0 + w * 32 + b;
-        y[row_map ? row_map[row_e] : row_e] = T(0);
-      }
-    }
-  }
+  if (last_ends) *out = (first && cont) ? carry + run : run;
 }
 
-// Second pass: split row i gets y[split_rows[i]] = sum of partials[slots[j]] for j in
-// [split_ptr[i], split_ptr[i+1]), j increasing (slots listed in item order, a fixed order).
-// A separate launch: the kernel boundary makes the first pass's partials visible on every
-// XCD, so neither pass needs a device-scope fence.
+// Second pass: row i (rows[i] when rows is given) gets y = the sum of partials[slots[j]] for j
+// in [row_ptr[i], row_ptr[i+1]), j increasing (slots listed in item order, a fixed order); a
+// row without slots gets 0.  Consecutive threads take consecutive rows, so y is written in
+// whole lines, and each XCD takes one contiguous range of rows: a tile's slots are one
+// contiguous range, so its partial lines are fetched into one L2 rather than several.  A
+// separate launch: the kernel boundary makes the first pass's partials visible on every XCD,
+// so neither pass needs a device-scope fence.
 template <typename T, typename A>
-__global__ __launch_bounds__(kBlock) void xcs_split_combine_kernel(
-    const int* __restrict__ split_rows, const int* __restrict__ split_ptr,
+__global__ __launch_bounds__(kBlock) void xcs_row_combine_kernel(
+    const int* __restrict__ rows, const int* __restrict__ row_ptr,
     const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
-    const int* __restrict__ row_map, int n_split) {
-  const int i = blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n_split) return;
-  const int a = split_ptr[i], b = split_ptr[i + 1];
+    const int* __restrict__ row_map, int n_rows) {
+  const int i = xcd_logical_block(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
+  if (i >= n_rows) return;
+  const int a = row_ptr[i], b = row_ptr[i + 1];
   // Eight slots per round: all slot indices, then all partials, are requested before the
   // first is used, so a row costs two memory round trips per eight slots, not two per slot.
   constexpr int kU = 8;
@@ -290,7 +258,7 @@ __global__ __launch_bounds__(kBlock) void xcs_split_combine_kernel(
     for (int u = 0; u < kU; ++u)
       if (j0 + u < b) acc += pv[u];
   }
-  const int row = split_rows[i];
+  const int row = rows ? rows[i] : i;
   y[row_map ? row_map[row] : row] = T(acc);
 }
 
@@ -415,21 +383,23 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
 
 template <typename T, typename A>
 int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
-               const int32_t* row_map, const int32_t* items, int64_t n_slots,
-               const uint32_t* masks, void* partials, const int32_t* split_rows,
-               const int32_t* split_ptr, const int32_t* slots, int64_t n_split, hipStream_t st) {
-  hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
-                     kXcsLdsReserve, st,
-                     static_cast<const T*>(vals), pidx, col_bits, static_cast<const T*>(x),
-                     static_cast<T*>(y), row_map, reinterpret_cast<const i32x4*>(items),
-                     (int)n_slots, masks, static_cast<A*>(partials));
-  int rc = check_hip(hipGetLastError(), "spmv_xcs_kernel launch");
-  if (rc || n_split == 0) return rc;
-  const int64_t blocks = (n_split + kBlock - 1) / kBlock;
-  hipLaunchKernelGGL((xcs_split_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0,
-                     st, split_rows, split_ptr, slots, static_cast<const A*>(partials),
-                     static_cast<T*>(y), row_map, (int)n_split);
-  return check_hip(hipGetLastError(), "xcs_split_combine_kernel launch");
+               const int32_t* row_map, const int32_t* items, int64_t n_slots, void* partials,
+               const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
+               int64_t n_rows, hipStream_t st) {
+  if (n_slots > 0) {
+    hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
+                       kXcsLdsReserve, st, static_cast<const T*>(vals), pidx, col_bits,
+                       static_cast<const T*>(x), reinterpret_cast<const i32x4*>(items),
+                       (int)n_slots, static_cast<A*>(partials));
+    int rc = check_hip(hipGetLastError(), "spmv_xcs_kernel launch");
+    if (rc) return rc;
+  }
+  if (n_rows == 0) return FSP_OK;
+  const int64_t blocks = (n_rows + kBlock - 1) / kBlock;
+  hipLaunchKernelGGL((xcs_row_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                     rows, row_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
+                     row_map, (int)n_rows);
+  return check_hip(hipGetLastError(), "xcs_row_combine_kernel launch");
 }
 
 // Second pass of the panel layout: its rows have hundreds of slots each, so one wave adds a
@@ -494,21 +464,21 @@ using namespace fsp;
 extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                             int64_t n_entries, int col_bits, const void* x, void* y,
                             const int32_t* row_map, int64_t n_out, const int32_t* items,
-                            int64_t n_slots, const uint32_t* masks, void* partials,
-                            const int32_t* split_rows, const int32_t* split_ptr,
-                            const int32_t* slots, int64_t n_split, void* stream) {
+                            int64_t n_slots, void* partials, const int32_t* rows,
+                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                            void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
-  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_split < 0)
+  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_rows < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: negative size");
   if (n_entries > 0x7fffffffLL - kXcsItemCap || n_slots > 0x3fffffffLL ||
-      n_split > 0x7fffffffLL - kBlock)
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or split rows");
+      n_rows > 0x7fffffffLL - kBlock)
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or rows");
   if (col_bits < 1 || col_bits > 24)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: col_bits outside [1, 24]");
-  if (n_slots > 0 && (!vals || !pidx || !x || !y || !items || !masks))
+  if (n_slots > 0 && (!vals || !pidx || !x || !items || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null pointer");
-  if (n_split > 0 && (!split_rows || !split_ptr || !slots || !partials))
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: null split-row pointer");
+  if (n_rows > 0 && (!y || !row_ptr || !slots || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: null row pointer");
   if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: vals, pidx and items must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -517,16 +487,15 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
                                 : fill_zero<double>(static_cast<double*>(y), n_out, st);
     if (rc) return rc;
   }
-  if (n_slots == 0) return FSP_OK;
   if (dtype == FSP_F32) {
     if (acc_f64)
-      return launch_xcs<float, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
-                                       partials, split_rows, split_ptr, slots, n_split, st);
-    return launch_xcs<float, float>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
-                                    partials, split_rows, split_ptr, slots, n_split, st);
+      return launch_xcs<float, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
+                                       partials, rows, row_ptr, slots, n_rows, st);
+    return launch_xcs<float, float>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
+                                    partials, rows, row_ptr, slots, n_rows, st);
   }
-  return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots, masks,
-                                    partials, split_rows, split_ptr, slots, n_split, st);
+  return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
+                                    partials, rows, row_ptr, slots, n_rows, st);
 }
 
 extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,

@@ -155,24 +155,24 @@ int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
  *   vals, pidx   n_entries padded entries (16-byte aligned): pidx = (local row << col_bits) |
  *                (column - the panel's first column); every item starts on a multiple of 4
  *   col_bits     in [1, 24]
- *   row_map      NULL: tile row r0 + r is y[r0 + r]; else y[row_map[r0 + r]] and y[0..n_out)
- *                is zeroed first
+ *   row_map      NULL: layout row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
  *   items        n_slots slots of 12 int32 in launch order (slot j runs on XCD j / (n_slots/8)
  *                when n_slots is a multiple of 8): {entry start, count, rank k in tile, 0, r0,
- *                rows, panel first column, mask word offset, first partial slot as two int32
- *                (low, high), tile (-1 marks an empty slot), 0}
- *   masks        per tile W = ceil(rows/32) split-row words then W empty-row words
- *   partials     one slot of 8 bytes per (item, split row it holds); an item's slots are
+ *                rows, panel first column, 0, first partial slot as two int32 (low, high),
+ *                tile (-1 marks an empty slot), 0}
+ *   partials     one slot of 8 bytes per (item, row run it holds); an item's slots are
  *                consecutive in row order
- *   split_rows   n_split rows summed over several items; row split_rows[i] gets the sum of
- *                partials[slots[j]], j in [split_ptr[i], split_ptr[i+1]) increasing (a second
- *                launch on the same stream).  Calls sharing partials must not overlap.
+ *   rows, row_ptr, slots
+ *                n_rows output rows: row i (rows[i], or i when rows is NULL) gets the sum of
+ *                partials[slots[j]], j in [row_ptr[i], row_ptr[i+1]) increasing, or 0 (a second
+ *                launch on the same stream; y written in row order).  Calls sharing partials
+ *                must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  int64_t n_entries, int col_bits, const void* x, void* y,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
-                 const uint32_t* masks, void* partials, const int32_t* split_rows,
-                 const int32_t* split_ptr, const int32_t* slots, int64_t n_split, void* stream);
+                 void* partials, const int32_t* rows, const int32_t* row_ptr,
+                 const int32_t* slots, int64_t n_rows, void* stream);
 
 /*
  * y[rows[i]] (y[row_map[rows[i]]] when row_map != NULL) = row i of A @ x for the long rows of

@@ -195,8 +195,14 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert b"split-row" in L.fsp_last_error()
     assert spmm(lanes=3) == -1                    # lanes_per_row not a power of two
     assert spmm(dtype=1, lanes=4, vec=4) == -1    # 4-wide vectors are fp32 only
-    assert L.fsp_spmv_xcs(0, 0, None, None, 0, 25, None, None, None, 0, None, 0, None, None, None,
-                          None, None, 0, None) == -1  # col_bits > 24
+    def xcs(col_bits=10, n_rows=0):
+        return L.fsp_spmv_xcs(0, 0, None, None, 0, col_bits, None, None, None, 0, None, 0, None,
+                              None, None, None, n_rows, None)
+
+    assert xcs() == 0                             # nothing to run
+    assert xcs(col_bits=25) == -1                 # col_bits > 24
+    assert xcs(n_rows=4) == -1                    # combine without its arrays
+    assert b"null" in L.fsp_last_error()
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1
 
     def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0):

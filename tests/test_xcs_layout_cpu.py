@@ -3,9 +3,9 @@ CPU and checked without a GPU: structural invariants the kernels rely on (every 
 once, item capacity and alignment, in-bounds packed indices, panel-to-XCD slot order; for
 panels, chunk-aligned panel runs padded with zero entries of their last row, jobs inside one
 panel, chunk slot offsets), and step-by-step emulations of spmv_xcs_kernel's and
-spmv_panel_kernel's semantics over the layouts (direct rows, split-row partials added in
-order, empty rows) - for the hybrid, the XCS part and then the panel part - against the fp64
-oracle."""
+spmv_panel_kernel's semantics over the layouts (one partial slot per run, each row's slots
+added in order, rows without entries written as 0) - for the hybrid, the XCS part and then
+the panel part - against the fp64 oracle."""
 
 import numpy as np
 import pytest
@@ -31,10 +31,11 @@ def _item_positions(e0, ln):
 
 
 def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
-    """numpy restatement of spmv_xcs_kernel + xcs_split_combine_kernel over the layout; layout
-    row r is written to y[row_map[r]] when a row map is given."""
+    """numpy restatement of spmv_xcs_kernel + xcs_row_combine_kernel over the layout: every
+    item writes each row run it holds to its next slot (in row order); row r then gets the sum
+    of its slots in the listed (item) order, 0 without any, at y[row_map[r]] when a row map is
+    given."""
     items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
-    masks = layout.masks.numpy().view(np.uint32)
     vals = layout.vals.numpy().astype(acc)
     pidx = layout.pidx.numpy().view(np.uint32)
     cbits = layout.col_bits
@@ -42,48 +43,32 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
     y = np.full(layout.n_rows, np.nan) if y is None else y
     partials = np.full(max(layout.n_partials, 1), np.nan)
     written = np.zeros(max(layout.n_partials, 1), dtype=bool)
-    for e0, ln, k, _, r0, R, cbase, moff, plo, phi, tile, _ in items:
+    for e0, ln, k, _, r0, R, cbase, _, plo, phi, tile, _ in items:
         if tile < 0:
             continue
         slot = (plo & 0xFFFFFFFF) | (phi << 32)
-        W = (R + 31) // 32
-        split = lambda r: (masks[moff + r // 32] >> (r % 32)) & 1  # noqa: E731
-        empty = lambda r: (masks[moff + W + r // 32] >> (r % 32)) & 1  # noqa: E731
         pos = _item_positions(e0, ln)
         p = pidx[pos]
         lrow = (p >> cbits).astype(np.int64)
         col = cbase + (p & ((1 << cbits) - 1)).astype(np.int64)
         prod = vals[pos] * x[col].astype(acc)
-        assert np.all(np.diff(lrow) >= 0)
-        for r in range(R):
-            if empty(r):
-                if k == 0:
-                    y[out(r0 + r)] = 0.0
-                continue
-            sel = prod[lrow == r]
-            if not sel.size:
-                continue
+        assert np.all(np.diff(lrow) >= 0) and np.all(lrow < R)
+        for r in np.unique(lrow):  # runs in row order
             s = acc(0)
-            for v in sel:
+            for v in prod[lrow == r]:
                 s = acc(s + v)
-            if split(r):  # the item's next slot, in row order
-                assert not written[slot]
-                partials[slot] = s
-                written[slot] = True
-                slot += 1
-            else:
-                assert np.isnan(y[out(r0 + r)])  # a direct row is written by one item only
-                y[out(r0 + r)] = s
+            assert not written[slot]
+            partials[slot] = s
+            written[slot] = True
+            slot += 1
     assert written[:layout.n_partials].all()
-    # second pass: each split row sums its slots in the listed (item) order
-    split_rows = layout.split_rows.numpy()
-    sptr = layout.split_ptr.numpy()
+    rp = layout.row_ptr.numpy()
     slots = layout.slots.numpy()
-    for i, row in enumerate(split_rows):
+    for r in range(layout.n_rows):
         s = acc(0)
-        for j in range(sptr[i], sptr[i + 1]):
+        for j in range(rp[r], rp[r + 1]):
             s = acc(s + partials[slots[j]])
-        y[out(row)] = s
+        y[out(r)] = s
     return y
 
 
@@ -294,7 +279,7 @@ def test_xcs_hybrid(seed):
     assert h.short.nnz + h.long.nnz == vals.numel()
     _check_panels(h.long, *_long_part(vals, cols, ip, long_mask))
     y = _emulate(h.short, x.numpy())
-    assert np.all(np.isnan(y[long_mask.numpy()]))  # long rows: left to the panel part
+    assert np.all(y[long_mask.numpy()] == 0.0)  # long rows: no entries in the XCS part
     y = _emulate_panels(h.long, x.numpy(), y)
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
     # through a row map (COO row runs): layout row r is output row map[r]

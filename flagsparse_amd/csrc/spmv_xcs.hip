@@ -231,16 +231,16 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
 // Second pass: row i (rows[i] when rows is given) gets y = the sum of partials[slots[j]] for j
 // in [row_ptr[i], row_ptr[i+1]), j increasing (slots listed in item order, a fixed order); a
 // row without slots gets 0.  Consecutive threads take consecutive rows, so y is written in
-// whole lines, and each XCD takes one contiguous range of rows: a tile's slots are one
-// contiguous range, so its partial lines are fetched into one L2 rather than several.  A
-// separate launch: the kernel boundary makes the first pass's partials visible on every XCD,
-// so neither pass needs a device-scope fence.
+// whole lines.  A separate launch: the kernel boundary makes the first pass's partials
+// visible on every XCD, so neither pass needs a device-scope fence.  (Giving each XCD one
+// contiguous range of rows, so that a tile's slot range is read into one L2, measured no
+// faster: the slot gathers, one L2 request each, bound this pass.)
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void xcs_row_combine_kernel(
     const int* __restrict__ rows, const int* __restrict__ row_ptr,
     const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int n_rows) {
-  const int i = xcd_logical_block(blockIdx.x, gridDim.x) * kBlock + threadIdx.x;
+  const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= n_rows) return;
   const int a = row_ptr[i], b = row_ptr[i + 1];
   // Eight slots per round: all slot indices, then all partials, are requested before the

@@ -327,11 +327,35 @@ class _SpmmKernelCsr:
         return p
 
 
+# B larger than this is read in column tiles of at most this many bytes (the kernel walks the
+# tiles in launch order, so one tile's rows of B are gathered at a time and stay in the
+# 256 MiB MALL for longer).  Measured on MI355X, cfg5's matrix: fp32 N=256 3.34 -> 2.86 ms
+# (tiles of 128 columns, the rule's choice; 64: 3.01, 32: 2.92), fp64 N=256 6.69 -> 5.82 ms
+# (64, the rule's choice); fp32 N=64 (B of 256 MiB) is fastest untiled; fp64 N=64 (B of
+# exactly 512 MiB, left untiled by the rule) gained 5 % with tiles of 32.
+SPMM_B_TILE_BYTES = 512 << 20
+
+
+def _auto_tile_cols(B):
+    """Column tile for a large B (None: no tiling): the widest power of two whose slice of B
+    stays within SPMM_B_TILE_BYTES."""
+    rows, n = int(B.shape[0]), int(B.shape[1])
+    if rows * n * B.element_size() < SPMM_B_TILE_BYTES:
+        return None
+    t = _next_pow2(n)
+    while t > 4 and rows * t * B.element_size() > SPMM_B_TILE_BYTES:
+        t >>= 1
+    return t if t < n else None
+
+
 def _run_spmm(kc, B, C, acc_f64, tile_cols=None):
-    """Launch fsp_spmm_csr: C[n_rows, N] = A @ B (B, C contiguous row-major)."""
+    """Launch fsp_spmm_csr: C[n_rows, N] = A @ B (B, C contiguous row-major).  Without an
+    explicit tile (the reference's block_n), a B over SPMM_B_TILE_BYTES is tiled by columns."""
     n_dense_cols = int(B.shape[1])
     if kc.n_rows == 0 or n_dense_cols == 0:
         return C
+    if tile_cols is None:
+        tile_cols = _auto_tile_cols(B)
     dtype = B.dtype
     lanes, vec = _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols)
     key = (lanes, vec, n_dense_cols, bool(acc_f64), dtype)

@@ -47,6 +47,26 @@ def test_banded_random_like_cfg5(dev, dtype, N):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("N", [24, 64, 130])
+def test_large_b_column_tiles(dev, monkeypatch, dtype, N):
+    # the automatic column tiling of a B over SPMM_B_TILE_BYTES, with the threshold lowered so
+    # that a small B takes it (tiles of 16 fp32 / 8 fp64 columns; ragged last tiles for N = 24
+    # and 130)
+    from flagsparse_amd import spmm_csr as mod
+
+    monkeypatch.setattr(mod, "SPMM_B_TILE_BYTES", 256 << 10)
+    data, idx, ptr, shape = synthetic.csr_banded_random(1 << 12, band_nnz=8, rand_nnz=8,
+                                                        dtype=dtype)
+    B = synthetic.dense_uniform(shape[1], N, dtype=dtype, seed=3)
+    assert mod._auto_tile_cols(B) is not None
+    print(f"column tiles N={N} {dtype} tile={mod._auto_tile_cols(B)}", flush=True)
+    ref = oracle.spmm_csr(ptr, idx, data, B)
+    d, i, p, Bd = data.to(dev), idx.to(dev), ptr.to(dev), B.to(dev)
+    _check(fs.flagsparse_spmm_csr_opt(d, i, p, Bd, shape), ref)
+    _check(fs.flagsparse_spmm_csr(d, i, p, Bd, shape), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("N", [1, 2, 3, 5, 7, 12, 24, 33, 48, 96, 130])
 def test_widths_and_long_rows(dev, dtype, N):
     # short rows, rows around the part threshold (128) and block capacity (2045), split rows

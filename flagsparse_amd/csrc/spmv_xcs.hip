@@ -51,9 +51,8 @@ namespace {
 
 constexpr int kItemCap = (int)kXcsItemCap;
 constexpr int kRowsCap = (int)kXcsRowsCap;
-static_assert(kRowsCap % 32 == 0 && kRowsCap <= 65535, "row ids are kept as 16-bit values");
 
-// Occupancy cap.  The kernel needs about 2 KiB of LDS and 64 VGPRs, so up to 8 workgroups
+// Occupancy cap.  The kernel needs well under 1 KiB of LDS and 64 VGPRs, so up to 8 workgroups
 // would share a CU; measured on MI355X, 5 per CU gathers fastest (cfg3: 562 us at 5, 574 at 6
 // and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue more x requests at the XCD's
 // L2.  The launch reserves this much dynamic LDS per workgroup (unused) so that

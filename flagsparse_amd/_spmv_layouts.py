@@ -40,8 +40,10 @@ XCD_COUNT = 8
 L2_BYTES = 4 << 20
 # Bytes of x one panel may span: leaves room in the 4 MiB L2 for the entry stream.  More
 # panels also split more rows (more partial slots), so this is a balance measured on MI355X:
-# 8.4 MB of x (2M fp32 columns) runs best as 8 panels, 33.5 MB (8M columns) as 16.
+# 8.4 MB of x (2M fp32 columns, cfg4) runs best as 4 panels each shared by 2 XCDs (231 us vs
+# 243 us as 8), 33.5 MB (8M columns) as 16.
 PANEL_BYTES = 3 << 20
+MIN_PANELS = 4
 # A column counts as "near" its row when within this many columns of the row's position on
 # the diagonal; the row-block layout is kept when most entries are near (x reuse in L2).
 NEAR_COLUMNS = 1 << 16
@@ -154,12 +156,15 @@ class XcsLayout:
         #    other, so that one panel of x - at most PANEL_BYTES - sits in the XCD's L2), each
         #    at most 2^b columns wide with b the fewest bits that can cover n_cols in P panels
         #    (more bits for the row in pidx).
-        m = panels_per_xcd
-        if m is None:
-            m = 1
-            while m < 8 and self.n_cols * data.element_size() > XCD_COUNT * m * PANEL_BYTES:
-                m *= 2
-        P = XCD_COUNT * m
+        #    An x of at most XCD_COUNT / 2 panels' worth gets fewer panels than XCDs, each panel
+        #    then shared by XCD_COUNT / P XCDs (fewer row splits, so fewer partial slots).
+        if panels_per_xcd is not None:
+            P = XCD_COUNT * int(panels_per_xcd)
+        else:
+            P = MIN_PANELS
+            while P < XCD_COUNT * 8 and self.n_cols * data.element_size() > P * PANEL_BYTES:
+                P *= 2
+        m = max(1, P // XCD_COUNT)
         self.n_panels = P
         hist = torch.bincount(cols, minlength=self.n_cols) if nnz else \
             torch.zeros(self.n_cols, dtype=torch.int64, device=dev)
@@ -299,10 +304,20 @@ class XcsLayout:
         del pair_key, pair_item, pair_row, by_row, rp
 
         # 7. Launch order: XCD x runs the items of panels x, x + 8, x + 16, ... (one panel
-        #    after the other, each in tile order); lists padded to the same length q so that
-        #    slot x*q + j lands on XCD x.
-        xcd = item_panel % XCD_COUNT
-        phase = item_panel // XCD_COUNT
+        #    after the other, each in tile order); with P < 8 panel p's items are dealt in turn
+        #    to XCDs p, p + P, p + 2P, ...; lists padded to the same length q so that slot
+        #    x*q + j lands on XCD x.
+        if P >= XCD_COUNT:
+            xcd = item_panel % XCD_COUNT
+            phase = item_panel // XCD_COUNT
+        else:
+            by_panel = torch.sort(item_panel, stable=True)[1]
+            pcount = torch.bincount(item_panel, minlength=P)
+            rank_in_panel = torch.empty_like(item_panel)
+            rank_in_panel[by_panel] = torch.arange(n_items, device=dev) - \
+                (torch.cumsum(pcount, 0) - pcount)[item_panel[by_panel]]
+            xcd = item_panel + P * (rank_in_panel % (XCD_COUNT // P))
+            phase = torch.zeros_like(item_panel)
         per_xcd = torch.bincount(xcd, minlength=XCD_COUNT)
         q = int(per_xcd.max().item()) if n_items else 0
         self.n_slots = XCD_COUNT * q

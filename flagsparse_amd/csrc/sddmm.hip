@@ -57,6 +57,12 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
     int xcd_remap) {
   __shared__ int s_col[kSdSlots];
   __shared__ P s_ptr[kBlock + 1];
+  // Results are collected in LDS and written out together at the end, in whole lines: written
+  // straight from the groups, 16 bytes at a time, partial lines were evicted by the y gathers
+  // before they filled (cfg5 pattern, K = 64: 935 -> 789 us without those stores).  A 4-byte
+  // result takes the slot of the column it came from; wider ones get their own array.
+  __shared__ O s_out_wide[sizeof(O) == sizeof(int) ? 1 : kSdSlots];
+  O* const s_out = sizeof(O) == sizeof(int) ? reinterpret_cast<O*>(s_col) : s_out_wide;
   const int tid = threadIdx.x;
   int b = blockIdx.x;
   if (xcd_remap) b = xcd_logical_block(b, n_desc);
@@ -91,16 +97,16 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
   for (int i = tid; i <= R; i += kBlock) s_ptr[i] = rowptr[d.x + i];
   __syncthreads();
 
-  // This group's row and entry range (relative to lo), entries visited with stride `step`.
-  int row, a, e, step;
+  // This group's row and entry range (relative to lo), entries visited with stride `step`;
+  // groups without a row get an empty range (no early exit: the block meets a barrier below).
+  int row = d.x, a = 0, e = 0, step = 4;
   if (d.z == 0) {
-    if (grp >= R) return;
-    row = d.x + grp;
-    a = (int)(s_ptr[grp] - lo);
-    e = (int)(s_ptr[grp + 1] - lo);
-    step = 4;
+    if (grp < R) {
+      row = d.x + grp;
+      a = (int)(s_ptr[grp] - lo);
+      e = (int)(s_ptr[grp + 1] - lo);
+    }
   } else {
-    row = d.x;
     a = 4 * grp;
     e = (int)(hi - lo);
     step = 4 * ngrp;
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     const int k = (lane + c * G) * VW;
-    if (k < K) {
+    if (k < K && a < e) {
       sload<T, VW>(xp + k, xr[c]);
     } else {
 #pragma unroll
@@ -141,28 +147,29 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[q] = group_sum(acc[q], G);
-    // Every lane of the group holds the four sums.  With G >= 4, lanes 0..3 store them in one
-    // instruction; narrower groups store result q from lane q mod G.
+    // Every lane of the group holds the four sums.  With G >= 4, lanes 0..3 keep them; with
+    // narrower groups lane q mod G keeps result q.  A slot's column was read above by this
+    // group only, so its result may take the slot (the group's lanes run in lockstep).
     if (G >= 4) {
       if (lane < 4 && i + lane < e) {
         A v = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
-        const int64_t p = lo + i + lane;
         v *= a_alpha;
-        if (in) v += A(in[p]) * a_beta;
-        out[p] = O(v);
+        if (in) v += A(in[lo + i + lane]) * a_beta;
+        s_out[i + lane] = O(v);
       }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if ((q & (G - 1)) == lane && i + q < e) {
-          const int64_t p = lo + i + q;
           A v = acc[q] * a_alpha;
-          if (in) v += A(in[p]) * a_beta;
-          out[p] = O(v);
+          if (in) v += A(in[lo + i + q]) * a_beta;
+          s_out[i + q] = O(v);
         }
       }
     }
   }
+  __syncthreads();
+  for (int i = tid; i < (int)(hi - lo); i += kBlock) out[lo + i] = s_out[i];
 }
 
 template <typename T, typename A, typename O, int VW>

@@ -52,12 +52,16 @@ namespace {
 constexpr int kItemCap = (int)kXcsItemCap;
 constexpr int kRowsCap = (int)kXcsRowsCap;
 
-// Occupancy cap.  The kernel needs well under 1 KiB of LDS and 64 VGPRs, so up to 8 workgroups
-// would share a CU; measured on MI355X, 5 per CU gathers fastest (cfg3: 562 us at 5, 574 at 6
-// and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue more x requests at the XCD's
-// L2.  The launch reserves this much dynamic LDS per workgroup (unused) so that
-// floor(160 KiB / (static + reserve)) = 5.
-constexpr unsigned kXcsLdsReserve = 28u * 1024u;
+// Occupancy cap.  The kernel needs at most 16 KiB of LDS (its partial-sum buffer) and 64
+// VGPRs, so up to 8 workgroups would share a CU; measured on MI355X, 5 per CU gathers fastest
+// (cfg3: 562 us at 5, 574 at 6 and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue
+// more x requests at the XCD's L2.  The launch adds unused dynamic LDS up to this many bytes
+// per workgroup, so that floor(160 KiB / kXcsLdsPerWorkgroup) = 5.
+constexpr unsigned kXcsLdsPerWorkgroup = 28u * 1024u;
+template <typename A>
+constexpr unsigned xcs_lds_reserve() {
+  return kXcsLdsPerWorkgroup - (unsigned)(kItemCap * sizeof(A));
+}
 
 // Segmented sums over an item: thread t owns a contiguous run of the item's entries, which
 // holds whole runs (rows) and pieces of runs that continue from or into its neighbours.  A
@@ -77,6 +81,9 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   __shared__ int s_wh[kWavesPerBlock];
   __shared__ int s_wc[kWavesPerBlock];
   __shared__ A s_wv[kWavesPerBlock];
+  // The item's run sums, written out together at the end in whole lines (stored one by one
+  // from the threads, partial lines could leave L2 before they filled).
+  __shared__ A s_part[kItemCap];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
@@ -200,17 +207,19 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   if (lane == 0) { h_ex = 0; v_ex = A(0); c_ex = 0; }
   __syncthreads();
   A pv = A(0);
-  int pc = 0;
-  for (int j = 0; j < wid; ++j) {  // waves before this one, in order
-    const A wv = s_wv[j];
-    if (!s_wh[j]) pv = pv + wv; else pv = wv;
-    pc += s_wc[j];
+  int pc = 0, n_runs = 0;
+  for (int j = 0; j < kWavesPerBlock; ++j) {
+    if (j < wid) {  // waves before this one, in order
+      const A wv = s_wv[j];
+      if (!s_wh[j]) pv = pv + wv; else pv = wv;
+      pc += s_wc[j];
+    }
+    n_runs += s_wc[j];
   }
   const A carry = h_ex ? v_ex : pv + v_ex;
-  int next_slot = pc + c_ex;
 
   // Pass 2, in row order: each run to the item's next slot.
-  A* out = partials + sbase + next_slot;
+  A* out = s_part + pc + c_ex;
   bool first = true;
   A run = A(0);
 #pragma unroll
@@ -225,6 +234,8 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     }
   }
   if (last_ends) *out = (first && cont) ? carry + run : run;
+  __syncthreads();
+  for (int i = tid; i < n_runs; i += kBlock) partials[sbase + i] = s_part[i];
 }
 
 // Second pass: row i (rows[i] when rows is given) gets y = the sum of partials[slots[j]] for j
@@ -387,7 +398,7 @@ int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void*
                int64_t n_rows, hipStream_t st) {
   if (n_slots > 0) {
     hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
-                       kXcsLdsReserve, st, static_cast<const T*>(vals), pidx, col_bits,
+                       xcs_lds_reserve<A>(), st, static_cast<const T*>(vals), pidx, col_bits,
                        static_cast<const T*>(x), reinterpret_cast<const i32x4*>(items),
                        (int)n_slots, static_cast<A*>(partials));
     int rc = check_hip(hipGetLastError(), "spmv_xcs_kernel launch");

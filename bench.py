@@ -15,6 +15,10 @@ roofline     the same bytes / the dominant kernel's average duration, timed with
              committed rocprofv3 PMC summary (profiles/<kernel tag>_traffic.txt), or null.
 cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
              (a bounded row sample for SpMM), reported only, never a target
+cpu_reference_path
+             the reference's own CPU path - scipy.sparse (one core) and torch's CPU sparse
+             product (torch's thread count) - on the same matrix, a few seconds each, with
+             the same byte and flop counts; reported only
 targets      north_star's two targets measured in the same run (kernel time only): CSR SpMV
              fp32 on the 8M power-law matrix (>= 70% of HBM peak) and CSR SpMM fp32 N=64
              (>= 60%); omitted with --no-targets
@@ -106,6 +110,63 @@ def _tag(kernel):
     return kernel.replace("+", "_")
 
 
+def _time_passes(fn, seconds, max_passes=10000):
+    fn()  # warm-up (first-touch, library set-up)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        passes += 1
+        secs = time.perf_counter() - t0
+        if secs >= seconds or passes >= max_passes:
+            return passes, secs
+
+
+def _cpu_reference_path(fmt, mats, rhs, shape, seconds, nbytes, flops, torch):
+    """The reference's CPU path for the product: scipy.sparse (single-threaded) and torch's CPU
+    sparse tensors (torch.get_num_threads() threads), each on the host copy of the same
+    matrix and right-hand side.  fmt "csr": mats = (indptr, indices, data); "coo": (row, col,
+    data)."""
+    import warnings
+
+    import numpy as np
+    import scipy.sparse as sp
+
+    warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
+    a, b, data = (t.detach().cpu() for t in mats)
+    r = rhs.detach().cpu()
+    out = {}
+    try:
+        if fmt == "csr":
+            A = sp.csr_matrix((data.numpy(), b.numpy(), a.numpy()), shape=shape)
+        else:
+            A = sp.coo_matrix((data.numpy(), (a.numpy(), b.numpy())), shape=shape).tocsr()
+        rn = np.ascontiguousarray(r.numpy())
+        passes, secs = _time_passes(lambda: A @ rn, seconds)
+        out["scipy"] = {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
+                        "gflops": round(flops * passes / secs / 1e9, 3), "cores": 1,
+                        "sample": f"{passes} full products (scipy.sparse csr_matrix @ dense, "
+                                  f"{data.dtype}) in {secs:.1f} s"
+                                  + ("; COO converted to CSR first" if fmt == "coo" else "")}
+    except Exception as exc:  # report, never fail the benchmark
+        out["scipy"] = {"error": f"{type(exc).__name__}: {exc}"}
+    try:
+        if fmt == "csr":
+            At = torch.sparse_csr_tensor(a.to(torch.int64), b.to(torch.int64), data, size=shape)
+        else:
+            At = torch.sparse_coo_tensor(torch.stack([a, b]).to(torch.int64), data,
+                                         size=shape).coalesce()
+        rt = r if r.dim() == 2 else r.unsqueeze(1)
+        passes, secs = _time_passes(lambda: torch.sparse.mm(At, rt), seconds)
+        out["torch"] = {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
+                        "gflops": round(flops * passes / secs / 1e9, 3),
+                        "cores": torch.get_num_threads(),
+                        "sample": f"{passes} full products (torch.sparse.mm, {fmt.upper()} "
+                                  f"on the CPU, {data.dtype}) in {secs:.1f} s"}
+    except Exception as exc:
+        out["torch"] = {"error": f"{type(exc).__name__}: {exc}"}
+    return out
+
+
 def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
     if name == "cfg1":
         data, idx, ptr, x, shape = synthetic.csr_uniform_rows(device=dev)
@@ -145,6 +206,8 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         "step": lambda: fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y),
         "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
+        "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), x, shape,
+                                                       seconds, nbytes, 2 * nnz, torch),
         "dtype": "f64" if data.dtype == torch.float64 else "f32",
         "kernel": kc.kernel_name(), "tag": f"{_tag(kc.kernel_name())}_{name}",
     }
@@ -179,6 +242,8 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
         "step": lambda: fs.flagsparse_spmv_coo(x=x, prepared=prepared, out=y),
         "launch": lambda: mod._run_spmv_coo(prepared, x, y, 256),
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu, "dtype": "f32",
+        "cpu_lib": lambda seconds: _cpu_reference_path("coo", (row, col, data), x, shape,
+                                                       seconds, nbytes, 2 * nnz, torch),
         "kernel": prepared._kernel_name(), "tag": f"{_tag(prepared._kernel_name())}_cfg4",
     }
 
@@ -218,6 +283,8 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
         "step": lambda: fs.flagsparse_spmm_csr_opt(B=B, prepared=prepared, out=C),
         "launch": lambda: mod._run_spmm(kc, B, C, acc_f64=vdt == torch.float64),
         "nbytes": nbytes, "flops": 2 * nnz * N, "info": info, "cpu": cpu,
+        "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), B, shape,
+                                                       seconds, nbytes, 2 * nnz * N, torch),
         "dtype": dtype_name, "kernel": kc.kernel_name(),
         "tag": f"{kc.kernel_name()}_cfg5_{dtype_name}_n{N}",
     }
@@ -398,9 +465,11 @@ def main():
     nbytes, flops = w["nbytes"], w["flops"]
     value = nbytes / (ms_step * 1e-3) / 1e9
     achieved = nbytes / (ms_kernel * 1e-3) / 1e9
-    cpu = None
+    cpu = cpu_lib = None
     if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
         cpu = w["cpu"](args.cpu_seconds)
+        if w.get("cpu_lib") is not None:
+            cpu_lib = w["cpu_lib"](args.cpu_seconds / 2)
     workload = f"{args.workload}: {WORKLOADS[args.workload]}"
     if args.workload in ("cfg5", "coo5"):
         workload = f"{args.workload} ({w['dtype']}, N={args.n}): {WORKLOADS[args.workload]}"
@@ -434,6 +503,7 @@ def main():
                      "traffic": _traffic_from_profile(tag), "kernel": kernel,
                      "kernel_ms": round(ms_kernel, 6), "profile_tag": tag},
         "cpu_baseline": cpu,
+        "cpu_reference_path": cpu_lib,
         "targets": targets,
     }
     print(json.dumps(out), flush=True)

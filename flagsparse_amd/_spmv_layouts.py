@@ -293,15 +293,30 @@ class XcsLayout:
             torch.zeros(n_items, dtype=torch.int64, device=dev)
         item_slot = torch.cumsum(per_item, 0) - per_item
         by_row = torch.sort(pair_row, stable=True)[1]  # item order kept within a row
-        self.slots = by_row.to(torch.int32).contiguous() if n_pairs else \
-            torch.zeros(1, dtype=torch.int32, device=dev)
+        count = torch.bincount(pair_row, minlength=n_rows) if n_pairs else \
+            torch.zeros(n_rows, dtype=torch.int64, device=dev)
         rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
-        if n_pairs:
-            torch.cumsum(torch.bincount(pair_row, minlength=n_rows), 0, out=rp[1:])
-        self.row_ptr = rp.to(torch.int32).contiguous()
+        torch.cumsum(count, 0, out=rp[1:])
+        # The combine's row table: head[r] = the slot of a row with exactly one slot (most
+        # rows: one load to find it); otherwise -(k + 1), k the row's place in the list of
+        # the other rows, whose slots are slots[split_ptr[k] .. split_ptr[k + 1]) (none: 0).
+        one = count == 1
+        multi = ~one
+        head = torch.empty(n_rows, dtype=torch.int64, device=dev)
+        head[one] = by_row[rp[:-1][one]]
+        head[multi] = -(torch.cumsum(multi.to(torch.int64), 0)[multi])
+        self.head = head.to(torch.int32).contiguous()
+        sp = torch.zeros(int(multi.sum().item()) + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(count[multi], 0, out=sp[1:])
+        self.split_ptr = sp.to(torch.int32).contiguous()
+        keep = multi[torch.sort(pair_row, stable=True)[0]] if n_pairs else \
+            torch.zeros(0, dtype=torch.bool, device=dev)
+        split_slots = by_row[keep]
+        self.slots = split_slots.to(torch.int32).contiguous() if split_slots.numel() else \
+            torch.zeros(1, dtype=torch.int32, device=dev)
         self.n_partials = n_pairs
-        self.n_split_rows = int(((rp[1:] - rp[:-1]) > 1).sum().item()) if n_rows else 0
-        del pair_key, pair_item, pair_row, by_row, rp
+        self.n_split_rows = int((count > 1).sum().item()) if n_rows else 0
+        del pair_key, pair_item, pair_row, by_row, rp, count, head, keep, split_slots
 
         # 7. Launch order: XCD x runs the items of panels x, x + 8, x + 16, ... (one panel
         #    after the other, each in tile order); with P < 8 panel p's items are dealt in turn
@@ -362,8 +377,8 @@ class XcsLayout:
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
-                    self.n_slots, p(self.partials), None, p(self.row_ptr), p(self.slots),
-                    self.n_rows, None]
+                    self.n_slots, p(self.partials), p(self.head), p(self.split_ptr),
+                    p(self.slots), self.n_rows, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[7] = x.data_ptr(), y.data_ptr()

@@ -238,38 +238,42 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   for (int i = tid; i < n_runs; i += kBlock) partials[sbase + i] = s_part[i];
 }
 
-// Second pass: row i (rows[i] when rows is given) gets y = the sum of partials[slots[j]] for j
-// in [row_ptr[i], row_ptr[i+1]), j increasing (slots listed in item order, a fixed order); a
-// row without slots gets 0.  Consecutive threads take consecutive rows, so y is written in
-// whole lines.  A separate launch: the kernel boundary makes the first pass's partials
-// visible on every XCD, so neither pass needs a device-scope fence.  (Giving each XCD one
-// contiguous range of rows, so that a tile's slot range is read into one L2, measured no
-// faster: the slot gathers, one L2 request each, bound this pass.)
+// Second pass: row i gets y = the sum of its slots in item order (a fixed order), 0 without
+// any.  head[i] >= 0 is the slot of a row with exactly one (most rows: one load to find it);
+// head[i] = -(k + 1) points to slots[split_ptr[k] .. split_ptr[k+1]) (on cfg3's short rows,
+// 6 us less than a row pointer and a slot list for every row).  Consecutive threads take
+// consecutive rows, so y is written in whole lines.  A separate launch: the kernel boundary
+// makes the first pass's partials visible on every XCD, so neither pass needs a device-scope
+// fence.
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void xcs_row_combine_kernel(
-    const int* __restrict__ rows, const int* __restrict__ row_ptr,
+    const int* __restrict__ head, const int* __restrict__ split_ptr,
     const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int n_rows) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i >= n_rows) return;
-  const int a = row_ptr[i], b = row_ptr[i + 1];
-  // Eight slots per round: all slot indices, then all partials, are requested before the
-  // first is used, so a row costs two memory round trips per eight slots, not two per slot.
-  constexpr int kU = 8;
+  const int h = head[i];
   A acc = A(0);
-  for (int j0 = a; j0 < b; j0 += kU) {
-    int sl[kU];
-    A pv[kU];
+  if (h >= 0) {
+    acc += partials[h];
+  } else {
+    const int a = split_ptr[-h - 1], b = split_ptr[-h];
+    // Eight slots per round: all slot indices, then all partials, are requested before the
+    // first is used, so a row costs two memory round trips per eight slots, not two per slot.
+    constexpr int kU = 8;
+    for (int j0 = a; j0 < b; j0 += kU) {
+      int sl[kU];
+      A pv[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) sl[u] = j0 + u < b ? slots[j0 + u] : -1;
+      for (int u = 0; u < kU; ++u) sl[u] = j0 + u < b ? slots[j0 + u] : -1;
 #pragma unroll
-    for (int u = 0; u < kU; ++u) pv[u] = sl[u] >= 0 ? partials[sl[u]] : A(0);
+      for (int u = 0; u < kU; ++u) pv[u] = sl[u] >= 0 ? partials[sl[u]] : A(0);
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      if (j0 + u < b) acc += pv[u];
+      for (int u = 0; u < kU; ++u)
+        if (j0 + u < b) acc += pv[u];
+    }
   }
-  const int row = rows ? rows[i] : i;
-  y[row_map ? row_map[row] : row] = T(acc);
+  y[row_map ? row_map[i] : i] = T(acc);
 }
 
 // Panel layout (see the file comment): one workgroup per job, waves independent after the
@@ -394,7 +398,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
 template <typename T, typename A>
 int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
                const int32_t* row_map, const int32_t* items, int64_t n_slots, void* partials,
-               const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
+               const int32_t* head, const int32_t* split_ptr, const int32_t* slots,
                int64_t n_rows, hipStream_t st) {
   if (n_slots > 0) {
     hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
@@ -407,7 +411,7 @@ int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void*
   if (n_rows == 0) return FSP_OK;
   const int64_t blocks = (n_rows + kBlock - 1) / kBlock;
   hipLaunchKernelGGL((xcs_row_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                     rows, row_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
+                     head, split_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
                      row_map, (int)n_rows);
   return check_hip(hipGetLastError(), "xcs_row_combine_kernel launch");
 }
@@ -474,8 +478,8 @@ using namespace fsp;
 extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                             int64_t n_entries, int col_bits, const void* x, void* y,
                             const int32_t* row_map, int64_t n_out, const int32_t* items,
-                            int64_t n_slots, void* partials, const int32_t* rows,
-                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                            int64_t n_slots, void* partials, const int32_t* head,
+                            const int32_t* split_ptr, const int32_t* slots, int64_t n_rows,
                             void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
   if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_rows < 0)
@@ -487,7 +491,7 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: col_bits outside [1, 24]");
   if (n_slots > 0 && (!vals || !pidx || !x || !items || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null pointer");
-  if (n_rows > 0 && (!y || !row_ptr || !slots || !partials))
+  if (n_rows > 0 && (!y || !head || !split_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null row pointer");
   if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: vals, pidx and items must be 16-byte aligned");
@@ -500,12 +504,12 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
   if (dtype == FSP_F32) {
     if (acc_f64)
       return launch_xcs<float, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                       partials, rows, row_ptr, slots, n_rows, st);
+                                       partials, head, split_ptr, slots, n_rows, st);
     return launch_xcs<float, float>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                    partials, rows, row_ptr, slots, n_rows, st);
+                                    partials, head, split_ptr, slots, n_rows, st);
   }
   return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                    partials, rows, row_ptr, slots, n_rows, st);
+                                    partials, head, split_ptr, slots, n_rows, st);
 }
 
 extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,

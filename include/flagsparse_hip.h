@@ -162,16 +162,16 @@ int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
  *                tile (-1 marks an empty slot), 0}
  *   partials     one slot of 8 bytes per (item, row run it holds); an item's slots are
  *                consecutive in row order
- *   rows, row_ptr, slots
- *                n_rows output rows: row i (rows[i], or i when rows is NULL) gets the sum of
- *                partials[slots[j]], j in [row_ptr[i], row_ptr[i+1]) increasing, or 0 (a second
- *                launch on the same stream; y written in row order).  Calls sharing partials
- *                must not overlap.
+ *   head, split_ptr, slots
+ *                n_rows rows, each given y (a second launch on the same stream, y written in
+ *                row order): head[i] >= 0 - the row's only slot, partials[head[i]]; head[i] =
+ *                -(k + 1) - the sum of partials[slots[j]], j in [split_ptr[k], split_ptr[k+1])
+ *                increasing, 0 for an empty range.  Calls sharing partials must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  int64_t n_entries, int col_bits, const void* x, void* y,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
-                 void* partials, const int32_t* rows, const int32_t* row_ptr,
+                 void* partials, const int32_t* head, const int32_t* split_ptr,
                  const int32_t* slots, int64_t n_rows, void* stream);
 
 /*

@@ -4,7 +4,7 @@ once, item capacity and alignment, in-bounds packed indices, panel-to-XCD slot o
 panels, chunk-aligned panel runs padded with zero entries of their last row, jobs inside one
 panel, chunk slot offsets), and step-by-step emulations of spmv_xcs_kernel's and
 spmv_panel_kernel's semantics over the layouts (one partial slot per run, each row's slots
-added in order, rows without entries written as 0) - for the hybrid, the XCS part and then
+added in order through the combine's row table, rows without entries written as 0) - for the hybrid, the XCS part and then
 the panel part - against the fp64 oracle."""
 
 import numpy as np
@@ -62,13 +62,25 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
             written[slot] = True
             slot += 1
     assert written[:layout.n_partials].all()
-    rp = layout.row_ptr.numpy()
+    # the combine's row table: head >= 0 is a row's only slot, else -(k + 1) points to the
+    # k-th slot list; every slot is used by exactly one row
+    head = layout.head.numpy().astype(np.int64)
+    sp = layout.split_ptr.numpy()
     slots = layout.slots.numpy()
+    used = np.zeros(max(layout.n_partials, 1), dtype=np.int64)
     for r in range(layout.n_rows):
         s = acc(0)
-        for j in range(rp[r], rp[r + 1]):
-            s = acc(s + partials[slots[j]])
+        if head[r] >= 0:
+            s = acc(s + partials[head[r]])
+            used[head[r]] += 1
+        else:
+            k = -head[r] - 1
+            assert sp[k + 1] - sp[k] != 1  # one-slot rows use head
+            for j in range(sp[k], sp[k + 1]):
+                s = acc(s + partials[slots[j]])
+                used[slots[j]] += 1
         y[out(r)] = s
+    assert np.all(used[:layout.n_partials] == 1)
     return y
 
 

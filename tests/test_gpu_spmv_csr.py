@@ -74,6 +74,26 @@ def test_poisson_fp64(dev, use_opt):
     _check(y, oracle.spmv_csr(ptr, idx, data, x), torch.float64)
 
 
+@pytest.mark.parametrize("grid", [1024, 1536])
+def test_poisson_band_launch_order(dev, monkeypatch, grid):
+    # a stencil's far diagonals (+-grid rows, 2.5 and 3.75 blocks of ~409 rows here) are
+    # detected and the descriptors reordered; the order changes nothing in the result, bit for
+    # bit
+    from flagsparse_amd import _spmv_layouts
+
+    data, idx, ptr, x, shape = synthetic.csr_poisson2d(grid)
+    d, i, p, xd = data.to(dev), idx.to(dev), ptr.to(dev), x.to(dev)
+    prep = fs.prepare_spmv_csr(d, i, p, shape)
+    lay = prep._kernel(False)
+    assert lay.kind == "rowblock" and lay.band_offset is not None
+    y = fs.flagsparse_spmv_csr(x=xd, prepared=prep)
+    _check(y, oracle.spmv_csr(ptr, idx, data, x), torch.float64)
+    monkeypatch.setattr(_spmv_layouts, "BAND_ORDER", False)
+    plain = fs.prepare_spmv_csr(d, i, p, shape)
+    assert plain._kernel(False).band_offset is None
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=xd, prepared=plain))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("use_opt", [False, True])
 def test_powerlaw_split_rows(dev, dtype, use_opt):

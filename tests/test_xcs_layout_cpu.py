@@ -312,6 +312,30 @@ def _long_part(vals, cols, ip, long_mask):
     return vals[entry_long], cols[entry_long], lp
 
 
+@pytest.mark.parametrize("n,off", [(10494, 5), (777, 3), (4096, 17), (129, 2)])
+def test_band_launch_order(n, off):
+    # a permutation; launch slot i lands on the XCD its block was given (i mod 8) except in the
+    # tail where the XCDs' lists have unequal lengths; a block and its +-off neighbours in
+    # the same chain segment share an XCD
+    order = _spmv_layouts.band_launch_order(n, off, "cpu").numpy()
+    assert sorted(order.tolist()) == list(range(n))
+    c, k = order % off, order // off
+    xcd = (c + off * (k // _spmv_layouts.BAND_SEGMENT)) % 8
+    assert np.mean(xcd == np.arange(n) % 8) > 0.97
+    b = np.arange(n - off)
+    same = (b // off // _spmv_layouts.BAND_SEGMENT) == ((b + off) // off // _spmv_layouts.BAND_SEGMENT)
+    xb = ((b % off) + off * (b // off // _spmv_layouts.BAND_SEGMENT)) % 8
+    xb2 = (((b + off) % off) + off * ((b + off) // off // _spmv_layouts.BAND_SEGMENT)) % 8
+    assert np.all(xb[same] == xb2[same])
+
+
+def test_band_offset_detection():
+    d, i, p, _, shape = synthetic.csr_poisson2d(2048)
+    assert _spmv_layouts.band_block_offset(i, p, 10494) == 5  # far diagonals 2048 rows away
+    _, cols, ip, _ = _case([12] * 20000, 4 << 20, 2)
+    assert _spmv_layouts.band_block_offset(cols, ip, 200) is None  # uniform random columns
+
+
 def test_layout_choice():
     # uniform random columns over a large x -> XCS; a banded matrix -> row blocks
     vals, cols, ip, _ = _case([12] * 20000, 4 << 20, 2)

@@ -10,8 +10,8 @@ reference's default use_opt=False path); --workload selects the others.
 
 value        algorithmic bytes per step / time per step (HIP events around the K steps)
 roofline     the same bytes / the dominant kernel's average duration, timed with HIP events
-             around K back-to-back launches on the stream the kernel runs on, against the
-             8 TB/s HBM3E peak.  ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the
+             around K back-to-back launches on the stream the kernel runs on (the median of 5
+             such trials; all five in ``kernel_ms_trials``), against the 8 TB/s HBM3E peak.  ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the
              committed rocprofv3 PMC summary (profiles/<kernel tag>_traffic.txt), or null.
 cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
              (a bounded row sample for SpMM), reported only, never a target
@@ -19,6 +19,9 @@ cpu_reference_path
              the reference's own CPU path - scipy.sparse (one core) and torch's CPU sparse
              product (torch's thread count) - on the same matrix, a few seconds each, with
              the same byte and flop counts; reported only
+config       also ``prepare_ms`` (the prepare call, synchronised), ``first_call_ms`` (the first
+             step after prepare, cold) and ``inputs_sha256`` (SHA-256 of every generated input
+             array, so that runs on different machines provably use the same data)
 targets      north_star's two targets measured in the same run (kernel time only): CSR SpMV
              fp32 on the 8M power-law matrix (>= 70% of HBM peak) and CSR SpMM fp32 N=64
              (>= 60%); omitted with --no-targets
@@ -105,6 +108,32 @@ def _event_loop(fn, count, torch):
     return start.elapsed_time(end) / count
 
 
+def _timed_prepare(fn, torch):
+    """(result, milliseconds) of a prepare call, synchronised on both sides."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = fn()
+    torch.cuda.synchronize()
+    return out, round((time.perf_counter() - t0) * 1000.0, 3)
+
+
+def _digests(arrays, synthetic):
+    """{name: SHA-256 of the array's bytes} for the generated inputs."""
+    return {name: synthetic.sha256(t) for name, t in arrays.items()}
+
+
+def _host_info(torch):
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            m = re.search(r"^model name\s*:\s*(.+)$", fh.read(), re.M)
+            model = m.group(1).strip() if m else None
+    except OSError:
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
+
+
 def _tag(kernel):
     """File-name form of a kernel label ("a+b" for a path of two main kernels)."""
     return kernel.replace("+", "_")
@@ -176,8 +205,11 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         data, idx, ptr, x, shape = synthetic.csr_powerlaw(device=dev)
     from flagsparse_amd import spmv_csr as mod
 
-    prepared = fs.prepare_spmv_csr(data, idx, ptr, shape)
+    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmv_csr(data, idx, ptr, shape), torch)
     use_opt = bool(opt and prepared.supports_opt)
+    # the layout and launch arguments are built on first use; count them as prepare work
+    _, kernel_ms0 = _timed_prepare(lambda: prepared._kernel(use_opt), torch)
+    prep_ms = round(prep_ms + kernel_ms0, 3)
     y = torch.empty(shape[0], dtype=data.dtype, device=dev)
     kc = prepared._kernel(use_opt)
     v = data.element_size()
@@ -190,7 +222,8 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
             "path": "use_opt=True" if use_opt else "default (use_opt=False)",
             "bytes_as_supplied": nnz * (v + idx.element_size()) +
             (shape[0] + 1) * ptr.element_size() + shape[1] * v + shape[0] * v,
-            "plan": kc.describe()}
+            "plan": kc.describe(), "prepare_ms": prep_ms,
+            "inputs": {"data": data, "indices": idx, "indptr": ptr, "x": x}}
 
     def cpu(seconds):
         from oracle import oracle
@@ -217,7 +250,7 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
     from flagsparse_amd import spmv_coo as mod
 
     data, row, col, x, shape = synthetic.coo_uniform(device=dev)
-    prepared = fs.prepare_spmv_coo(data, row, col, shape)
+    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmv_coo(data, row, col, shape), torch)
     y = torch.empty(shape[0], dtype=data.dtype, device=dev)
     v = data.element_size()
     nnz = int(data.numel())
@@ -227,7 +260,8 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
         nbytes += runs * 4 + shape[0] * v
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "row_runs": runs,
             "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * v + shape[0] * v,
-            "plan": prepared._kernel_plan_description()}
+            "plan": prepared._kernel_plan_description(), "prepare_ms": prep_ms,
+            "inputs": {"data": data, "row": row, "col": col, "x": x}}
 
     def cpu(seconds):
         from oracle import oracle
@@ -254,9 +288,10 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
     vdt = torch.float64 if dtype_name == "f64" else torch.float32
     data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
     B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
-    prepared = fs.prepare_spmm_csr_opt(data, idx, ptr, shape)
+    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmm_csr_opt(data, idx, ptr, shape), torch)
     C = torch.empty((shape[0], N), dtype=vdt, device=dev)
-    kc = prepared._kernel_csr()
+    kc, kernel_ms0 = _timed_prepare(prepared._kernel_csr, torch)
+    prep_ms = round(prep_ms + kernel_ms0, 3)
     v = data.element_size()
     nnz = int(data.numel())
     p_k = 4 if kc.rowptr_bits == 32 else 8
@@ -264,7 +299,8 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
             "path": "flagsparse_spmm_csr_opt (native accumulation)",
             "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * p_k +
-            shape[0] * N * v}
+            shape[0] * N * v, "prepare_ms": prep_ms,
+            "inputs": {"data": data, "indices": idx, "indptr": ptr, "B": B}}
 
     def cpu(seconds):
         from oracle import oracle
@@ -309,7 +345,8 @@ def _spmm_coo_workload(dev, dtype_name, N, torch, fs, synthetic):
     nbytes = nnz * (v + 4) + (shape[0] + 1) * 4 + shape[1] * N * v + shape[0] * N * v
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
             "path": "flagsparse_spmm_coo (row-run route, fp64 accumulation for fp32)",
-            "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * N * v + shape[0] * N * v}
+            "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * N * v + shape[0] * N * v,
+            "inputs": {"data": data, "row": row, "col": col, "B": B}}
 
     def cpu(seconds):
         from oracle import oracle
@@ -348,7 +385,8 @@ def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
     _, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
     x = synthetic.dense_uniform(shape[0], K, dtype=vdt, seed=1, device=dev)
     y = synthetic.dense_uniform(shape[1], K, dtype=vdt, seed=2, device=dev)
-    prepared = fs.prepare_sddmm_csr(idx, ptr, shape, k_hint=K)
+    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_sddmm_csr(idx, ptr, shape, k_hint=K),
+                                       torch)
     out = torch.empty(prepared.nnz, dtype=vdt, device=dev)
     v = x.element_size()
     nnz = prepared.nnz
@@ -356,7 +394,8 @@ def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
     nbytes = nnz * (4 + 4 + v) + shape[0] * K * v + shape[1] * K * v
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "K": K,
             "path": "flagsparse_sddmm_csr (baseline variant)",
-            "bytes_gather_inclusive": nnz * (4 + 4 + v + 2 * K * v)}
+            "bytes_gather_inclusive": nnz * (4 + 4 + v + 2 * K * v), "prepare_ms": prep_ms,
+            "inputs": {"indices": idx, "indptr": ptr, "x": x, "y": y}}
 
     def cpu(seconds):
         from oracle import oracle
@@ -418,7 +457,14 @@ def _build(name, args, dev, torch):
     return _copy_workload(dev, torch)
 
 
-def _measure(w, steps, warmup, torch):
+KERNEL_TRIALS = 5
+
+
+def _measure(w, steps, warmup, torch, trials=KERNEL_TRIALS):
+    """(ms per step, host wall ms per step, median kernel ms, [kernel ms of each trial],
+    first-call ms).  The first step after prepare is timed on its own, cold; then W warm-up
+    steps, the K timed steps, and ``trials`` runs of K back-to-back kernel launches."""
+    first_ms = _event_loop(w["step"], 1, torch)
     for _ in range(warmup):
         w["step"]()
     t0 = time.perf_counter()
@@ -426,8 +472,9 @@ def _measure(w, steps, warmup, torch):
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
     for _ in range(max(1, warmup // 2)):
         w["launch"]()
-    ms_kernel = _event_loop(w["launch"], steps, torch)
-    return ms_step, wall_ms, ms_kernel
+    runs = [_event_loop(w["launch"], steps, torch) for _ in range(max(1, trials))]
+    ms_kernel = sorted(runs)[len(runs) // 2]
+    return ms_step, wall_ms, ms_kernel, runs, first_ms
 
 
 def _target(name, args, dev, torch, steps):
@@ -437,7 +484,7 @@ def _target(name, args, dev, torch, steps):
     a = A()
     a.opt, a.dtype, a.n = False, "f32", 64
     w = _build(name, a, dev, torch)
-    _, _, ms_kernel = _measure(w, steps, 5, torch)
+    _, _, ms_kernel, _, _ = _measure(w, steps, 5, torch, trials=1)
     achieved = w["nbytes"] / (ms_kernel * 1e-3) / 1e9
     out = {"workload": name if name != "cfg5" else "cfg5 (f32, N=64)", "kernel": w["kernel"],
            "kernel_ms": round(ms_kernel, 6), "achieved_GBs": round(achieved, 2),
@@ -461,13 +508,15 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     w = _build(args.workload, args, dev, torch)
-    ms_step, wall_ms, ms_kernel = _measure(w, args.steps, args.warmup, torch)
+    ms_step, wall_ms, ms_kernel, kernel_runs, first_ms = _measure(w, args.steps, args.warmup,
+                                                                  torch)
     nbytes, flops = w["nbytes"], w["flops"]
     value = nbytes / (ms_step * 1e-3) / 1e9
     achieved = nbytes / (ms_kernel * 1e-3) / 1e9
     cpu = cpu_lib = None
     if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
         cpu = w["cpu"](args.cpu_seconds)
+        cpu["host"] = _host_info(torch)
         if w.get("cpu_lib") is not None:
             cpu_lib = w["cpu_lib"](args.cpu_seconds / 2)
     workload = f"{args.workload}: {WORKLOADS[args.workload]}"
@@ -476,6 +525,13 @@ def main():
     if args.workload == "sddmm":
         workload = f"sddmm ({w['dtype']}, K={args.n}): {WORKLOADS['sddmm']}"
     info, dtype, kernel, tag = dict(w["info"]), w["dtype"], w["kernel"], w["tag"]
+    inputs = info.pop("inputs", None)
+    if inputs:
+        from flagsparse_amd import synthetic
+
+        info["inputs_sha256"] = _digests(inputs, synthetic)
+    del inputs
+    info["first_call_ms"] = round(first_ms, 6)
     del w
     torch.cuda.empty_cache()
     targets = None
@@ -501,7 +557,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": _traffic_from_profile(tag), "kernel": kernel,
-                     "kernel_ms": round(ms_kernel, 6), "profile_tag": tag},
+                     "kernel_ms": round(ms_kernel, 6),
+                     "kernel_ms_trials": [round(t, 6) for t in kernel_runs],
+                     "profile_tag": tag},
         "cpu_baseline": cpu,
         "cpu_reference_path": cpu_lib,
         "targets": targets,

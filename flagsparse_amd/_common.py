@@ -18,6 +18,10 @@ SUPPORTED_VALUE_DTYPES = (
 SUPPORTED_INDEX_DTYPES = (torch.int32, torch.int64)
 KERNEL_VALUE_DTYPES = (torch.float32, torch.float64)
 _INDEX_LIMIT_INT32 = 2**31 - 1
+# The largest entry count for which the kernels read 32-bit row pointers (above it, 64-bit);
+# read at prepare time, so tests can lower it to run the 64-bit row-pointer kernels on small
+# matrices.
+ROWPTR32_MAX_NNZ = _INDEX_LIMIT_INT32
 
 
 def _is_complex_dtype(value_dtype):

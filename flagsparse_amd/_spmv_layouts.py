@@ -33,6 +33,7 @@ import numpy as np
 import torch
 
 from . import _abi
+from . import _common
 from ._common import _INDEX_LIMIT_INT32, _aligned
 from ._plan import build_row_block_plan_windows
 
@@ -90,7 +91,7 @@ class RowBlockLayout:
         self.data = _aligned(data)
         self.cols = _aligned(cols)
         nnz = int(data.numel())
-        if rowptr.dtype == torch.int32 or nnz <= _INDEX_LIMIT_INT32:
+        if nnz <= _common.ROWPTR32_MAX_NNZ:
             self.rowptr, self.rowptr_bits = rowptr.to(torch.int32).contiguous(), 32
         else:
             self.rowptr, self.rowptr_bits = rowptr.to(torch.int64).contiguous(), 64

@@ -17,8 +17,8 @@ import time
 
 import torch
 
-from . import _abi
-from ._common import _INDEX_LIMIT_INT32, _aligned, _benchmark_cuda_op, _tolerance_for_dtype
+from . import _abi, _common
+from ._common import _aligned, _benchmark_cuda_op, _tolerance_for_dtype
 from ._plan import build_row_block_plan_device
 from .synthetic import build_random_csr, build_random_dense
 
@@ -55,8 +55,9 @@ class SDDMMPrepared:
         plan = self._plans.get(lanes)
         if plan is None:
             if self._kernel_ptr is None:
-                self._kernel_ptr = (self.indptr.to(torch.int32) if self.nnz <= _INDEX_LIMIT_INT32
-                                    else self.indptr)
+                self._kernel_ptr = (self.indptr.to(torch.int32)
+                                    if self.nnz <= _common.ROWPTR32_MAX_NNZ
+                                    else self.indptr.to(torch.int64))
             cap = _abi.caps()["spmm_block_nnz"]
             plan = build_row_block_plan_device(self._kernel_ptr, cap, _BLOCK_THREADS // lanes,
                                                min(_SDDMM_ROW_SPLIT_THRESHOLD, cap), cap)

@@ -15,7 +15,7 @@ import time
 
 import torch
 
-from . import _abi
+from . import _abi, _common
 from ._common import (
     SUPPORTED_INDEX_DTYPES,
     SUPPORTED_VALUE_DTYPES,
@@ -299,10 +299,10 @@ class _SpmmKernelCsr:
         self.cols = _aligned(cols)
         self.nnz = int(data.numel())
         self.n_rows = int(indptr64.numel()) - 1
-        if self.nnz <= _INDEX_LIMIT_INT32:
+        if self.nnz <= _common.ROWPTR32_MAX_NNZ:
             self.rowptr, self.rowptr_bits = indptr64.to(torch.int32), 32
         else:
-            self.rowptr, self.rowptr_bits = indptr64, 64
+            self.rowptr, self.rowptr_bits = indptr64.to(torch.int64).contiguous(), 64
         self._plans = {}
         self._args = {}
         self._keep = []

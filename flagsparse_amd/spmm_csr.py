@@ -250,19 +250,6 @@ def _resolve_spmm_alg1_launch_config(n_dense_cols, max_row_nnz, block_n=None, bl
     }
 
 
-def _select_spmm_opt_block_n(n_dense_cols):
-    """spmm_csr.py:405-414."""
-    if n_dense_cols <= 8:
-        return 8
-    if n_dense_cols <= 16:
-        return 16
-    if n_dense_cols <= 32:
-        return 32
-    if n_dense_cols <= 64:
-        return 64
-    return 128
-
-
 def _next_pow2(v):
     p = 1
     while p < v:

@@ -498,9 +498,9 @@ def _target(name, args, dev, torch, steps):
 def main():
     args = _parse()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the "
-              "multi-GPU row-slab design is described in DESIGN.md but not built)",
-              file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (a "
+              "multi-GPU version would shard A by row slabs balanced by entries, with x or B "
+              "replicated on every GPU; it is not built)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -8,11 +8,14 @@ reference's harness does (sparse_operations/benchmarks.py:249-262).  The default
 BASELINE.json configs[1] (CSR SpMV, float64, 5-point Poisson on a 2048 x 2048 grid, the
 reference's default use_opt=False path); --workload selects the others.
 
-value        algorithmic bytes per step / time per step (HIP events around the K steps)
+value        algorithmic bytes per step / time per step (HIP events around the K steps); the
+             untimed warm-up before them runs W steps at a time until at least 50 ms have
+             passed (``warmup_steps_run`` reports how many)
 roofline     the same bytes / the dominant kernel's average duration, timed with HIP events
              around K back-to-back launches on the stream the kernel runs on (the median of 5
-             such trials; all five in ``kernel_ms_trials``), against the 8 TB/s HBM3E peak.  ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the
-             committed rocprofv3 PMC summary (profiles/<kernel tag>_traffic.txt), or null.
+             such trials; all five in ``kernel_ms_trials``), against the 8 TB/s HBM3E peak.
+             ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the committed rocprofv3
+             PMC summary (profiles/<kernel tag>_traffic.txt), or null.
 cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
              (a bounded row sample for SpMM), reported only, never a target
 cpu_reference_path
@@ -460,13 +463,34 @@ def _build(name, args, dev, torch):
 KERNEL_TRIALS = 5
 
 
+# Warm-up runs in chunks of W steps until at least this much time has passed: measured on
+# MI355X, the first ~10 ms of back-to-back work run about 4 % slower (cfg2: 58.9 us per step
+# in the first 200 steps after 20 warm-up steps, 56.6 us after).
+WARM_SECONDS = 0.05
+
+
+def _warm(fn, warmup, torch, seconds=WARM_SECONDS):
+    """Run ``fn`` in chunks of ``warmup`` calls, synchronising after each chunk, until at least
+    ``seconds`` have passed; returns the number of calls (0 when warmup is 0)."""
+    if warmup <= 0:
+        return 0
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for _ in range(warmup):
+            fn()
+        n += warmup
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return n
+
+
 def _measure(w, steps, warmup, torch, trials=KERNEL_TRIALS):
     """(ms per step, host wall ms per step, median kernel ms, [kernel ms of each trial],
-    first-call ms).  The first step after prepare is timed on its own, cold; then W warm-up
-    steps, the K timed steps, and ``trials`` runs of K back-to-back kernel launches."""
+    first-call ms, warm-up steps run).  The first step after prepare is timed on its own, cold;
+    then the warm-up (W steps at a time, untimed), the K timed steps, and ``trials`` runs of K
+    back-to-back kernel launches."""
     first_ms = _event_loop(w["step"], 1, torch)
-    for _ in range(warmup):
-        w["step"]()
+    warm_run = _warm(w["step"], warmup, torch)
     t0 = time.perf_counter()
     ms_step = _event_loop(w["step"], steps, torch)
     wall_ms = (time.perf_counter() - t0) * 1000.0 / steps
@@ -474,7 +498,7 @@ def _measure(w, steps, warmup, torch, trials=KERNEL_TRIALS):
         w["launch"]()
     runs = [_event_loop(w["launch"], steps, torch) for _ in range(max(1, trials))]
     ms_kernel = sorted(runs)[len(runs) // 2]
-    return ms_step, wall_ms, ms_kernel, runs, first_ms
+    return ms_step, wall_ms, ms_kernel, runs, first_ms, warm_run
 
 
 def _target(name, args, dev, torch, steps):
@@ -484,7 +508,7 @@ def _target(name, args, dev, torch, steps):
     a = A()
     a.opt, a.dtype, a.n = False, "f32", 64
     w = _build(name, a, dev, torch)
-    _, _, ms_kernel, _, _ = _measure(w, steps, 5, torch, trials=1)
+    _, _, ms_kernel, _, _, _ = _measure(w, steps, 5, torch, trials=1)
     achieved = w["nbytes"] / (ms_kernel * 1e-3) / 1e9
     out = {"workload": name if name != "cfg5" else "cfg5 (f32, N=64)", "kernel": w["kernel"],
            "kernel_ms": round(ms_kernel, 6), "achieved_GBs": round(achieved, 2),
@@ -508,8 +532,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     w = _build(args.workload, args, dev, torch)
-    ms_step, wall_ms, ms_kernel, kernel_runs, first_ms = _measure(w, args.steps, args.warmup,
-                                                                  torch)
+    ms_step, wall_ms, ms_kernel, kernel_runs, first_ms, warm_run = _measure(
+        w, args.steps, args.warmup, torch)
     nbytes, flops = w["nbytes"], w["flops"]
     value = nbytes / (ms_step * 1e-3) / 1e9
     achieved = nbytes / (ms_kernel * 1e-3) / 1e9
@@ -544,6 +568,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_run,
         "ms_per_step": round(ms_step, 6),
         "higher_is_better": True,
         "scaling": "weak",

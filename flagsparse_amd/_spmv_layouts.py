@@ -3,7 +3,7 @@
 Two layouts, chosen once per matrix at prepare time:
 
 ``RowBlockLayout`` (csrc/spmv.hip, ``spmv_rowblock_kernel``)
-    The CSR arrays as given plus a descriptor table: short-row blocks of <= 2045 entries and
+    The CSR arrays as given plus a descriptor table: short-row blocks of <= 1021 entries and
     <= 1024 rows, and long rows cut into chunks of <= 4093 entries whose sums are added in
     chunk order.  Right when the x entries a block gathers lie close together (banded,
     stencil, locally clustered columns) or x fits in one XCD's L2.

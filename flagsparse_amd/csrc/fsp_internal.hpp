@@ -11,7 +11,7 @@
 namespace fsp {
 
 // Kernel capacities (see the kernels for why each value is what it is).
-constexpr int64_t kSpmvStreamSlots = 2048;               // LDS product slots per short-row block
+constexpr int64_t kSpmvStreamSlots = 1024;               // LDS product slots per short-row block
 constexpr int64_t kSpmvStreamNnzCap = kSpmvStreamSlots - 3;
 constexpr int64_t kSpmvStreamRowsCap = 1024;
 constexpr int64_t kSpmvChunkUnitsPerThread = 4;

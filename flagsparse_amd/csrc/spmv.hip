@@ -8,7 +8,7 @@
 //   spmv_coo.py:111-150   atomic kernel for unsorted COO
 //
 // Work decomposition (MI355X-first, not the reference's bucket launches):
-//   * short-row block  {r0, r1, 0, 0}: the block's contiguous nnz range (<= 2045 entries) is
+//   * short-row block  {r0, r1, 0, 0}: the block's contiguous nnz range (<= 1021 entries) is
 //     read with 16-byte loads, one quad of entries per thread and step; products go to LDS;
 //     then each row is summed by a group of G lanes (G = 256 / next_pow2(rows), <= 64) with a
 //     butterfly shuffle reduction.

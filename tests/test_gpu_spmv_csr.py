@@ -119,7 +119,8 @@ def test_random_unsorted_duplicates_empty_rows(dev, dtype):
 
 
 @pytest.mark.parametrize("lengths", [
-    [2045, 2046, 1, 4093, 4094, 3, 8186, 8187, 2, 12279],       # stream / chunk boundaries
+    [2045, 2046, 1, 4093, 4094, 3, 8186, 8187, 2, 12279],       # chunk boundaries
+    [1021, 1022, 1, 1020, 3, 1021, 1021, 2, 1023, 4093, 1022],    # short-row block capacity
     [1, 2, 3, 5000, 7, 1, 1, 9000, 2045, 1, 2045],              # misaligned row starts
     [0] * 100 + [200000] + [0] * 100,                           # one very long row, empty rows
     [1] * 5000 + [0] * 3000 + [2] * 2000,                       # block row cap (1024 rows)

@@ -28,6 +28,10 @@ SUPPORTED_SDDMM_DIAGNOSTIC_VARIANTS = ("baseline", "acc64", "acc64_out64", "altr
 _BLOCK_THREADS = 256
 # Rows longer than this are cut into chunks that all lane groups of a workgroup share.
 _SDDMM_ROW_SPLIT_THRESHOLD = 128
+# The row-block plan is built in windows of this many blocks' rows, so that a window end adds
+# at most one short block per 16 (windows of one block's rows add a tiny block whenever the
+# entry cap ends a block before the row cap does).
+SDDMM_PLAN_WINDOW_BLOCKS = 16
 
 
 class SDDMMPrepared:
@@ -59,8 +63,10 @@ class SDDMMPrepared:
                                     if self.nnz <= _common.ROWPTR32_MAX_NNZ
                                     else self.indptr.to(torch.int64))
             cap = _abi.caps()["spmm_block_nnz"]
-            plan = build_row_block_plan_device(self._kernel_ptr, cap, _BLOCK_THREADS // lanes,
-                                               min(_SDDMM_ROW_SPLIT_THRESHOLD, cap), cap)
+            rows_cap = _BLOCK_THREADS // lanes
+            plan = build_row_block_plan_device(self._kernel_ptr, cap, rows_cap,
+                                               min(_SDDMM_ROW_SPLIT_THRESHOLD, cap), cap,
+                                               window_rows=SDDMM_PLAN_WINDOW_BLOCKS * rows_cap)
             self._plans[lanes] = plan
         return plan
 

@@ -28,10 +28,10 @@ SUPPORTED_SDDMM_DIAGNOSTIC_VARIANTS = ("baseline", "acc64", "acc64_out64", "altr
 _BLOCK_THREADS = 256
 # Rows longer than this are cut into chunks that all lane groups of a workgroup share.
 _SDDMM_ROW_SPLIT_THRESHOLD = 128
-# The row-block plan is built in windows of this many blocks' rows, so that a window end adds
-# at most one short block per 16 (windows of one block's rows add a tiny block whenever the
-# entry cap ends a block before the row cap does).
-SDDMM_PLAN_WINDOW_BLOCKS = 16
+# The row-block plan is built in windows of this many blocks' rows (windows of one block's
+# rows add a tiny block whenever the entry cap ends a block before the row cap does; wider
+# windows plan more slowly), as for SpMM.
+SDDMM_PLAN_WINDOW_BLOCKS = 4
 
 
 class SDDMMPrepared:

@@ -34,11 +34,12 @@ SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
 XCD_REMAP = 1
 # The row-block plan is built in windows of SPMM_PLAN_WINDOW_BLOCKS x the block row cap (each
 # window's last block may be short).  Windows of one block's rows cut a block after every
-# row-cap rows even when the entry cap ended the one before, adding a tiny block per window:
-# measured on MI355X, cfg5's matrix (32 entries per row) fp32 N=16 382 -> 324 us and fp64 N=8
-# 430 -> 341 us with windows of 16 blocks' rows; rows of 8 uniform entries fp64 N=8 696 ->
-# 660 us; other shapes equal or 1-3 % faster.
-SPMM_PLAN_WINDOW_BLOCKS = 16
+# row-cap rows even when the entry cap ended the one before, adding a tiny block per window;
+# wider windows make the planner (one thread per window) slower, which the paths that plan
+# on every call pay each time.  Measured on MI355X, cfg5's matrix, fp32 N=16, per call
+# (prepared / COO / base): 380 / 813 / 633 us with windows of 1 block, 329 / 840 / 657 with 4,
+# 327 / 1124 / 957 with 16; N=64: 663 / 1087 / 924, 663 / 1099 / 930, 662 / 1174 / 1006.
+SPMM_PLAN_WINDOW_BLOCKS = 4
 # Rows longer than this go to the part path (several lane groups per row).
 _SPMM_ROW_SPLIT_THRESHOLD = 128
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 
@@ -46,6 +46,8 @@ SIGNATURES = {
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
     "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
                             _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),
+    "fsp_index_stats": (_i32, [_p, _i32, _p, _i32, _i64, _p, _p, _p]),
+    "fsp_index_stats_partial_len": (_i64, []),
     "fsp_spmm_coo_atomic": (_i32, [_i32, _i32, _p, _p, _p, _i64, _p, _i64, _i64, _p, _i64, _i64,
                                    _p]),
     "fsp_plan_windows_count": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p]),

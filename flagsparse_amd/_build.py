@@ -19,7 +19,8 @@ LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libflagsparse_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-SOURCES = ("abi.cpp", "mtx.cpp", "plan.hip", "spmv.hip", "spmv_xcs.hip", "spmm.hip", "sddmm.hip")
+SOURCES = ("abi.cpp", "mtx.cpp", "plan.hip", "spmv.hip", "spmv_xcs.hip", "spmm.hip", "sddmm.hip",
+           "index_stats.hip")
 ARCH = "gfx950"
 
 # Packed-FP32 instructions (v_pk_*_f32) are disabled for all device code.

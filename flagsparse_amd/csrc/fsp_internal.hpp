@@ -18,6 +18,7 @@ constexpr int64_t kSpmvChunkUnitsPerThread = 4;
 constexpr int64_t kSpmvChunkCap = kSpmvChunkUnitsPerThread * 4 * 256 - 3;
 constexpr int64_t kSpmmSlots = 2048;                     // LDS (col, val) slots per SpMM block
 constexpr int64_t kSpmmNnzCap = kSpmmSlots - 3;
+constexpr int64_t kIndexStatsBlocks = 1024;             // first-pass workgroups of fsp_index_stats
 constexpr int64_t kXcsItemCap = 2048;                    // entries of one XCS item
 constexpr int64_t kXcsRowsCap = 8192;                    // rows of one XCS tile
 constexpr int64_t kPanelBytes = 65536;                   // x panel copied to LDS (panel SpMV)

@@ -19,6 +19,7 @@ import time
 import torch
 
 from . import _abi
+from ._index_stats import index_stats
 from ._common import (
     SUPPORTED_INDEX_DTYPES,
     _INDEX_LIMIT_INT32,
@@ -70,11 +71,12 @@ def _prepare_spmm_coo_inputs(data, row, col, B, shape):
     nnz = data.numel()
     if nnz > _INDEX_LIMIT_INT32:
         raise ValueError("nnz exceeds the int32 range supported by the Triton COO kernel")
+    row, col = row.contiguous(), col.contiguous()
+    row_sorted = True
     if nnz > 0:
-        # one device reduction, one host sync for all four bounds
-        bounds = torch.stack([row.min().to(torch.int64), row.max().to(torch.int64),
-                              col.min().to(torch.int64), col.max().to(torch.int64)]).tolist()
-        min_row, max_row, min_col, max_col = bounds
+        # one pass over both arrays and one host sync for the four bounds and the row order
+        min_row, max_row, min_col, max_col, descents = index_stats(row, col)
+        row_sorted = descents == 0
         if min_row < 0 or max_row >= n_rows:
             raise IndexError("row indices out of range for n_rows")
         if min_col < 0 or max_col >= n_cols:
@@ -88,7 +90,7 @@ def _prepare_spmm_coo_inputs(data, row, col, B, shape):
     kernel_row = row.contiguous().to(torch.int32)
     kernel_col = col.contiguous().to(torch.int32)
     B = B.contiguous()
-    return data, kernel_row, kernel_col, B, n_rows, n_cols, int(B.shape[1])
+    return data, kernel_row, kernel_col, B, n_rows, n_cols, int(B.shape[1]), row_sorted
 
 
 def _resolve_spmm_coo_launch_config(n_dense_cols, nnz, block_n=None, block_nnz=256):
@@ -121,9 +123,11 @@ class _CooRowOrder:
 
     __slots__ = ("data", "row", "col", "n_rows", "n_cols", "_kc")
 
-    def __init__(self, data, row, col, n_rows, n_cols):
+    def __init__(self, data, row, col, n_rows, n_cols, row_sorted=None):
         nnz = int(data.numel())
-        if nnz > 1 and not bool((row[1:] >= row[:-1]).all().item()):
+        if row_sorted is None:
+            row_sorted = nnz <= 1 or bool((row[1:] >= row[:-1]).all().item())
+        if not row_sorted:
             # (row, col) order, stable, so equal keys keep their input order
             key = row.to(torch.int64) * max(1, n_cols) + col.to(torch.int64)
             order = torch.sort(key, stable=True).indices
@@ -173,7 +177,7 @@ def _run_spmm_coo_route(data, row, col, B, shape, block_n=None, block_nnz=256, o
         raise ValueError("block_n must be positive when provided")
     if block_nnz is not None and block_nnz <= 0:
         raise ValueError("block_nnz must be positive when provided")
-    data, row, col, B, n_rows, n_cols, n_dense_cols = _prepare_spmm_coo_inputs(
+    data, row, col, B, n_rows, n_cols, n_dense_cols, row_sorted = _prepare_spmm_coo_inputs(
         data, row, col, B, shape)
     launch = _resolve_spmm_coo_launch_config(n_dense_cols, data.numel(), block_n=block_n,
                                              block_nnz=block_nnz)
@@ -197,7 +201,7 @@ def _run_spmm_coo_route(data, row, col, B, shape, block_n=None, block_nnz=256, o
         if route == "atomic":
             C = _spmm_coo_atomic(data, row, col, n_rows, B, n_dense_cols)
         else:
-            coo = _CooRowOrder(data, row, col, n_rows, n_cols)
+            coo = _CooRowOrder(data, row, col, n_rows, n_cols, row_sorted)
             direct = _out_ok_direct(out, (B, data))
             C = out if direct else torch.empty((n_rows, n_dense_cols), dtype=dtype,
                                                device=data.device)

@@ -36,6 +36,8 @@
  *   fsp_spmm_coo_atomic  - spmm_coo.py:464-523 (_triton_spmm_coo_atomic_impl).
  *   fsp_sddmm_csr        - sddmm_csr.py:107-151 (_sddmm_csr_real_kernel) and its launch in
  *                          _run_sddmm_prepared (:271-347).
+ *   fsp_index_stats      - the per-call index checks of spmm_coo.py:312-371 (min/max of row
+ *                          and col) and the row-order test of the row-run route (:394-461).
  *   fsp_mtx_read         - the .mtx parsing of the reference's test loaders
  *                          (tests/test_spmv.py:29-103 and its copies).
  */
@@ -242,6 +244,17 @@ int fsp_spmm_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
 int fsp_spmm_coo_atomic(int dtype, int acc_f64, const void* vals, const int32_t* rows,
                         const int32_t* cols, int64_t nnz, const void* B, int64_t ldb, int64_t N,
                         void* C_acc, int64_t ldc, int64_t n_rows, void* stream);
+
+/*
+ * Index checks in one pass: out[0..5) = {min a, max a, min b, max b, number of i in [1, n) with
+ * a[i] < a[i-1]} over n entries of two index arrays (a_bits / b_bits 32 or 64, int32 / int64).
+ * partial is device scratch of fsp_index_stats_partial_len() int64 values; out is 5 int64 on
+ * the device.  Two launches on the stream, no host synchronisation.  n == 0 gives
+ * {INT64_MAX, INT64_MIN, INT64_MAX, INT64_MIN, 0}.
+ */
+int fsp_index_stats(const void* a, int a_bits, const void* b, int b_bits, int64_t n,
+                    int64_t* partial, int64_t* out, void* stream);
+int64_t fsp_index_stats_partial_len(void);
 
 /*
  * CSR SDDMM: out[p] = alpha * dot(x[row(p), 0..K), y[cols[p], 0..K)) + beta * data_in[p]

@@ -199,6 +199,14 @@ def test_kernel_entry_points_reject_before_any_hip_call():
         return L.fsp_spmv_xcs(0, 0, None, None, 0, col_bits, None, None, None, 0, None, 0, None,
                               None, None, None, n_rows, None)
 
+    # fsp_index_stats(a, a_bits, b, b_bits, n, partial, out, stream)
+    assert L.fsp_index_stats(None, 16, None, 32, 0, None, None, None) == -1
+    assert b"widths" in L.fsp_last_error()
+    assert L.fsp_index_stats(None, 32, None, 32, -1, None, None, None) == -1
+    assert L.fsp_index_stats(None, 32, None, 64, 0, None, None, None) == -1  # null partial
+    assert b"null" in L.fsp_last_error()
+    assert L.fsp_index_stats_partial_len() == 5 * 1024
+
     assert xcs() == 0                             # nothing to run
     assert xcs(col_bits=25) == -1                 # col_bits > 24
     assert xcs(n_rows=4) == -1                    # combine without its arrays

@@ -9,6 +9,11 @@ from . import _abi
 def index_stats(a, b):
     """[min a, max a, min b, max b, number of i with a[i] < a[i-1]] as Python ints, for two
     contiguous 1-D int32/int64 device tensors of the same length (one host synchronisation)."""
+    return index_stats_device(a, b).tolist()
+
+
+def index_stats_device(a, b):
+    """The same five values as an int64 device tensor, without synchronising."""
     L = _abi.lib()
     dev = a.device
     partial = torch.empty(int(L.fsp_index_stats_partial_len()), dtype=torch.int64, device=dev)
@@ -17,4 +22,4 @@ def index_stats(a, b):
                                  32 if b.dtype == torch.int32 else 64, int(a.numel()),
                                  _abi.ptr(partial), _abi.ptr(out), _abi.stream_handle(dev)),
                "fsp_index_stats")
-    return out.tolist()
+    return out

@@ -144,7 +144,7 @@ class _CooRowOrder:
             # is >= r: one binary search per row (no atomics, unlike a bincount)
             bounds = torch.arange(self.n_rows + 1, dtype=self.row.dtype, device=self.row.device)
             indptr = torch.searchsorted(self.row, bounds).to(torch.int64)
-            self._kc = _SpmmKernelCsr(self.data, self.col, indptr)
+            self._kc = _SpmmKernelCsr(self.data, self.col, indptr, window_blocks=1)
         return self._kc
 
 

@@ -26,6 +26,7 @@ from ._common import (
     _require_kernel_dtype,
     _tolerance_for_dtype,
 )
+from ._index_stats import index_stats_device
 from ._plan import build_row_block_plan_device
 from .synthetic import build_random_csr, build_random_dense
 
@@ -38,7 +39,8 @@ XCD_REMAP = 1
 # wider windows make the planner (one thread per window) slower, which the paths that plan
 # on every call pay each time.  Measured on MI355X, cfg5's matrix, fp32 N=16, per call
 # (prepared / COO / base): 380 / 813 / 633 us with windows of 1 block, 329 / 840 / 657 with 4,
-# 327 / 1124 / 957 with 16; N=64: 663 / 1087 / 924, 663 / 1099 / 930, 662 / 1174 / 1006.
+# 327 / 1124 / 957 with 16; N=64: 663 / 1087 / 924, 663 / 1099 / 930, 662 / 1174 / 1006.  So
+# prepared matrices plan with 4 and the per-call paths with 1.
 SPMM_PLAN_WINDOW_BLOCKS = 4
 # Rows longer than this go to the part path (several lane groups per row).
 _SPMM_ROW_SPLIT_THRESHOLD = 128
@@ -164,7 +166,7 @@ def _prepare_spmm_csr_matrix(data, indices, indptr, shape):
         probes.append(torch.any(indptr[1:] < indptr[:-1]).to(torch.int64))
         probes.append(torch.max(indptr[1:] - indptr[:-1]).to(torch.int64))
     if nnz > 0:
-        probes += [indices.min().to(torch.int64), indices.max().to(torch.int64)]
+        probes += list(index_stats_device(indices.contiguous(), indices.contiguous())[:2])
     vals = torch.stack(probes).tolist()
     if vals[0] != 0:
         raise ValueError("indptr[0] must be 0")
@@ -287,9 +289,12 @@ class _SpmmKernelCsr:
     """Kernel-facing CSR arrays (aligned, int32 offsets when they fit) and plans per G."""
 
     __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_plans", "_args",
-                 "_keep")
+                 "_keep", "window_blocks")
 
-    def __init__(self, data, cols, indptr64):
+    def __init__(self, data, cols, indptr64, window_blocks=None):
+        # window_blocks: plan window in blocks' rows (SPMM_PLAN_WINDOW_BLOCKS when None); the
+        # paths that plan on every call use 1, which plans fastest
+        self.window_blocks = window_blocks
         self.data = _aligned(data)
         self.cols = _aligned(cols)
         self.nnz = int(data.numel())
@@ -318,7 +323,8 @@ class _SpmmKernelCsr:
             threshold = min(_SPMM_ROW_SPLIT_THRESHOLD, cap)
             chunk = min(cap, max(threshold, 16 * ngrp))
             p = build_row_block_plan_device(self.rowptr, cap, ngrp, threshold, chunk,
-                                            window_rows=SPMM_PLAN_WINDOW_BLOCKS * ngrp)
+                                            window_rows=(self.window_blocks
+                                                         or SPMM_PLAN_WINDOW_BLOCKS) * ngrp)
             self._plans[lanes] = p
         return p
 
@@ -629,7 +635,7 @@ def flagsparse_spmm_csr(data, indices, indptr, B, shape, block_n=None, block_nnz
         direct = False
     else:
         _require_kernel_dtype(dtype, "flagsparse_spmm_csr")
-        kc = _SpmmKernelCsr(data, kernel_indices, kernel_indptr)
+        kc = _SpmmKernelCsr(data, kernel_indices, kernel_indptr, window_blocks=1)
         direct = _out_ok_direct(out, (B, data))
         C = out if direct else torch.empty((n_rows, n_dense_cols), dtype=dtype,
                                            device=data.device)

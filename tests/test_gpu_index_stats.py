@@ -32,6 +32,8 @@ def test_index_stats(dev, n, dt_a, dt_b):
         b[-1] = -(1 << 35)
     a, b = a.to(dt_a), b.to(dt_b)
     assert index_stats(a, b) == _want(a, b)
+    if n > 1:  # views one element in: not 16-byte aligned, the element-wise path
+        assert index_stats(a[1:], b[1:]) == _want(a[1:], b[1:])
     s = torch.sort(a).values  # in order: no descents
     assert index_stats(s, b) == _want(s, b)
     assert index_stats(s, b)[4] == 0

@@ -36,6 +36,7 @@ class PreparedCoo:
         "use_seg_kernel",
         "_run_rows",
         "_layout",
+        "_one_shot",
     )
 
     def __init__(self, data, row, col, shape, seg_starts=None):
@@ -54,12 +55,14 @@ class PreparedCoo:
             self.use_seg_kernel = self.n_segs > 0
         self._run_rows = None
         self._layout = None
+        self._one_shot = False
 
     def _run_layout(self):
         """Kernel layout over the row runs (flagsparse_amd/_spmv_layouts.py) and the
         run -> row map, omitted when it is the identity."""
         if self._layout is None:
-            self._layout = build_layout(self.data, self.col, self.seg_starts, self.n_cols)
+            self._layout = build_layout(self.data, self.col, self.seg_starts, self.n_cols,
+                                        one_shot=self._one_shot)
             if self.n_segs == self.n_rows:
                 self._run_rows = None  # sorted and every row present: run k is row k
             else:
@@ -143,8 +146,14 @@ def _prepare_coo_tensors(data, row, col, shape, sort_by_row):
 
 def prepare_spmv_coo(data, row, col, shape, sort_by_row=True):
     """Cache sorted COO + row-run ``seg_starts`` when ``sort_by_row`` (spmv_coo.py:220-225)."""
+    return _prepare_spmv_coo(data, row, col, shape, sort_by_row, False)
+
+
+def _prepare_spmv_coo(data, row, col, shape, sort_by_row, one_shot):
+    """prepare_spmv_coo; one_shot: for a single call (the layout that builds fastest)."""
     d, kr, kc, seg = _prepare_coo_tensors(data, row, col, shape, sort_by_row)
     prepared = PreparedCoo(d, kr, kc, shape, seg_starts=seg)
+    prepared._one_shot = bool(one_shot)
     if prepared.use_seg_kernel:
         prepared._run_layout()
     return prepared
@@ -209,7 +218,7 @@ def flagsparse_spmv_coo(
     if prepared is None:
         if any(a is None for a in (data, row, col, x, shape)):
             raise ValueError("data, row, col, x, shape required when prepared is None")
-        prepared = prepare_spmv_coo(data, row, col, shape, sort_by_row=sort_by_row)
+        prepared = _prepare_spmv_coo(data, row, col, shape, sort_by_row, True)
     else:
         if x is None:
             raise TypeError("x is required when prepared is set")

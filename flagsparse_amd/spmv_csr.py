@@ -85,6 +85,7 @@ class PreparedCsrSpmv:
         "_kernels",
         "_baseline_compute_dtype",
         "_baseline_data",
+        "_one_shot",
     )
 
     def __init__(self, data, kernel_indices, kernel_indptr, shape, n_rows, n_cols, block_nnz,
@@ -98,6 +99,7 @@ class PreparedCsrSpmv:
         self.block_nnz = block_nnz
         self.max_segments = max_segments
         self.max_row_nnz = max_row_nnz
+        self._one_shot = False
         self.supports_opt = data.dtype in (torch.float32, torch.float64)
         if data.dtype in (torch.float16, torch.bfloat16):
             self._baseline_compute_dtype = torch.float32
@@ -174,11 +176,11 @@ class PreparedCsrSpmv:
             kc = self._kernels.get("full")
             if kc is None:
                 kc = build_layout(self.data, self.kernel_indices, self.kernel_indptr,
-                                  self.n_cols)
+                                  self.n_cols, one_shot=self._one_shot)
                 self._kernels["full"] = kc
         else:
             d, c, ip = truncate_rows(self.data, self.kernel_indices, self.kernel_indptr, caps)
-            kc = build_layout(d, c, ip, self.n_cols)
+            kc = build_layout(d, c, ip, self.n_cols, one_shot=self._one_shot)
         self._kernels[key] = kc
         return kc
 
@@ -261,6 +263,12 @@ def _validate_spmv_x(x, prepared):
 
 def prepare_spmv_csr(data, indices, indptr, shape, block_nnz=256, max_segments=None):
     """One-time validation, narrowing and planning - spmv_csr.py:455-495."""
+    return _prepare_spmv_csr(data, indices, indptr, shape, block_nnz, max_segments, False)
+
+
+def _prepare_spmv_csr(data, indices, indptr, shape, block_nnz, max_segments, one_shot):
+    """prepare_spmv_csr; one_shot marks a prepared object made for a single call (the layout
+    that builds fastest)."""
     (data, kernel_indices, kernel_indptr, n_rows, n_cols, row_lengths,
      max_row_nnz) = _prepare_spmv_csr_matrix(data, indices, indptr, shape)
     block_nnz_use = block_nnz
@@ -274,6 +282,7 @@ def prepare_spmv_csr(data, indices, indptr, shape, block_nnz=256, max_segments=N
     prepared = PreparedCsrSpmv(data, kernel_indices, kernel_indptr, shape, n_rows, n_cols,
                                block_nnz_use, max_segments_use, max_row_nnz, row_lengths,
                                max_segments)
+    prepared._one_shot = bool(one_shot)
     if prepared.supports_opt and n_rows > 0:
         prepared._kernel(False)  # build the descriptor table now, outside the timed calls
     return prepared
@@ -321,8 +330,8 @@ def flagsparse_spmv_csr(
             raise ValueError(
                 "data, indices, indptr, and shape are required when prepared is not provided"
             )
-        prepared = prepare_spmv_csr(data, indices, indptr, shape, block_nnz=block_nnz,
-                                    max_segments=max_segments)
+        prepared = _prepare_spmv_csr(data, indices, indptr, shape, block_nnz, max_segments,
+                                     True)
     x = _validate_spmv_x(x, prepared)
     dtype = prepared.data.dtype
     if out is not None and (tuple(out.shape) != (prepared.n_rows,) or out.dtype != dtype):

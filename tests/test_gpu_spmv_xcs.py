@@ -143,8 +143,16 @@ def test_automatic_choice(dev):
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=5000)  # x: 8 MiB
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
     assert p._kernel(False).kind in ("xcs", "xcs-hybrid")
-    _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), ref, exact_fp32=True)
+    # a call without a prepared object takes the row-block layout (fastest to build)
+    _check(fs.flagsparse_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), x.to(dev), shape), ref,
            exact_fp32=True)
+    rows = torch.repeat_interleave(torch.arange(shape[0]), ptr[1:] - ptr[:-1])
+    _check(fs.flagsparse_spmv_coo(data.to(dev), rows.to(dev), idx.to(dev), x.to(dev), shape),
+           oracle.spmv_coo(rows, idx, data, x, shape[0]))
+    po = fs.prepare_spmv_coo(data.to(dev), rows.to(dev), idx.to(dev), shape)
+    assert po._run_layout().kind in ("xcs", "xcs-hybrid")
     d, i, pp, xx, sh = synthetic.csr_poisson2d(1024)
     p = fs.prepare_spmv_csr(d.to(dev), i.to(dev), pp.to(dev), sh)
     assert p._kernel(False).kind == "rowblock"

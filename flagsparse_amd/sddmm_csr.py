@@ -39,7 +39,7 @@ class SDDMMPrepared:
     one int32 row id per entry, and the reference's launch attributes (block_k, num_warps)."""
 
     __slots__ = ("indices", "indptr", "shape", "n_rows", "n_cols", "nnz", "row_ids", "block_k",
-                 "num_warps", "_plans", "_kernel_ptr")
+                 "num_warps", "_plans", "_kernel_ptr", "_window_blocks")
 
     def __init__(self, indices, indptr, shape, row_ids, block_k, num_warps):
         self.indices = indices
@@ -53,6 +53,7 @@ class SDDMMPrepared:
         self.num_warps = int(num_warps)
         self._plans = {}
         self._kernel_ptr = None
+        self._window_blocks = SDDMM_PLAN_WINDOW_BLOCKS  # 1 for a prepared object of one call
 
     def _row_plan(self, lanes):
         """Row-block plan for ``lanes`` lanes per entry (built on the device, cached)."""
@@ -66,7 +67,7 @@ class SDDMMPrepared:
             rows_cap = _BLOCK_THREADS // lanes
             plan = build_row_block_plan_device(self._kernel_ptr, cap, rows_cap,
                                                min(_SDDMM_ROW_SPLIT_THRESHOLD, cap), cap,
-                                               window_rows=SDDMM_PLAN_WINDOW_BLOCKS * rows_cap)
+                                               window_rows=self._window_blocks * rows_cap)
             self._plans[lanes] = plan
         return plan
 
@@ -297,6 +298,7 @@ def flagsparse_sddmm_csr(data=None, indices=None, indptr=None, x=None, y=None, s
         t0 = time.perf_counter()
         k_hint = int(x.shape[1]) if (x is not None and x.ndim == 2) else 64
         prepared = prepare_sddmm_csr(indices, indptr, shape, k_hint=k_hint)
+        prepared._window_blocks = 1  # planned for this call only: the fastest plan to build
         torch.cuda.synchronize()
         prepare_ms = (time.perf_counter() - t0) * 1000.0
     elif not isinstance(prepared, SDDMMPrepared):

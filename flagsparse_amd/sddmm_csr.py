@@ -209,6 +209,12 @@ def _sddmm_lane_shape(K, x, y):
     lanes = 1
     while lanes < steps and lanes < 64:
         lanes <<= 1
+    # At most 16 lanes while the row-block schedule still holds K (K <= 4 * lanes * vec): wider
+    # groups spend more on the cross-lane sum than their loads gain.  Measured on MI355X, cfg5's
+    # pattern: fp32 K=128 1747 -> 1625 us (32 -> 16 lanes), fp64 K=64 2259 -> 1932 us; fp32
+    # K=64 stays at 16 (8 lanes: 846 vs 807 us).
+    while lanes > 16 and K <= 4 * (lanes // 2) * vec:
+        lanes >>= 1
     return lanes, vec
 
 

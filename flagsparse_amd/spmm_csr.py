@@ -329,23 +329,23 @@ class _SpmmKernelCsr:
         return p
 
 
-# B larger than this is read in column tiles of at most this many bytes (the kernel walks the
-# tiles in launch order, so one tile's rows of B are gathered at a time and stay in the
-# 256 MiB MALL for longer).  Measured on MI355X, cfg5's matrix: fp32 N=256 3.34 -> 2.86 ms
-# (tiles of 128 columns, the rule's choice; 64: 3.01, 32: 2.92), fp64 N=256 6.69 -> 5.82 ms
-# (64, the rule's choice); fp32 N=64 (B of 256 MiB) is fastest untiled; fp64 N=64 (B of
-# exactly 512 MiB, left untiled by the rule) gained 5 % with tiles of 32.
+# A B of more than half this many bytes is read in column tiles: the widest power of two of
+# columns narrower than B whose slice is at most this many bytes (the kernel walks the tiles in
+# launch order, so one tile's rows of B are gathered at a time and stay in the 256 MiB MALL for
+# longer).  Measured on MI355X, cfg5's matrix: fp32 N=256 (B of 1 GiB) 3.34 -> 2.86 ms with
+# tiles of 128 columns (64: 3.01, 32: 2.92); fp64 N=256 6.69 -> 5.82 ms (64); B of 512 MiB:
+# fp64 N=64 1437 -> 1372 us (32; 16: 1466), fp32 N=128 1416 -> 1350 us (64; 32: 1490); B of
+# 256 MiB is fastest untiled (fp32 N=64 662 vs 710 us with 32; fp64 N=32 689 vs 770 with 16).
 SPMM_B_TILE_BYTES = 512 << 20
 
 
 def _auto_tile_cols(B):
-    """Column tile for a large B (None: no tiling): the widest power of two whose slice of B
-    stays within SPMM_B_TILE_BYTES."""
-    rows, n = int(B.shape[0]), int(B.shape[1])
-    if rows * n * B.element_size() < SPMM_B_TILE_BYTES:
+    """Column tile for a large B (None: no tiling), by the rule above."""
+    rows, n, v = int(B.shape[0]), int(B.shape[1]), B.element_size()
+    if 2 * rows * n * v <= SPMM_B_TILE_BYTES:
         return None
     t = _next_pow2(n)
-    while t > 4 and rows * t * B.element_size() > SPMM_B_TILE_BYTES:
+    while t > 4 and (t >= n or rows * t * v > SPMM_B_TILE_BYTES):
         t >>= 1
     return t if t < n else None
 

@@ -49,8 +49,8 @@ def test_banded_random_like_cfg5(dev, dtype, N):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("N", [24, 64, 130])
 def test_large_b_column_tiles(dev, monkeypatch, dtype, N):
-    # the automatic column tiling of a B over SPMM_B_TILE_BYTES, with the threshold lowered so
-    # that a small B takes it (tiles of 16 fp32 / 8 fp64 columns; ragged last tiles for N = 24
+    # the automatic column tiling of a B over half of SPMM_B_TILE_BYTES, with the threshold
+    # lowered so that a small B takes it (tiles of 16 fp32 / 8 fp64 columns; ragged last tiles for N = 24
     # and 130)
     from flagsparse_amd import spmm_csr as mod
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 
@@ -34,15 +34,18 @@ SIGNATURES = {
     "fsp_spmm_block_nnz_cap": (_i64, []),
     "fsp_xcs_item_cap": (_i64, []),
     "fsp_xcs_rows_cap": (_i64, []),
+    "fsp_xcs_window_slots_cap": (_i64, []),
+    "fsp_xcs_window_rows_cap": (_i64, []),
+    "fsp_xcs_item_runs_cap": (_i64, []),
     "fsp_panel_bytes_cap": (_i64, []),
     "fsp_panel_chunk": (_i64, []),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p,
                             _i64, _i64, _p, _p, _p, _p, _i64, _i32, _p]),
     "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64, _p, _p,
-                            _p, _p, _i64, _p]),
+                            _p, _i64, _i64, _p, _p, _p]),
     "fsp_spmv_panels": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i64,
-                               _p, _p, _p, _p, _p, _i64, _p]),
+                               _p, _p, _i64, _p, _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
     "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
                             _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),
@@ -129,6 +132,9 @@ def caps():
         "spmm_block_nnz": int(L.fsp_spmm_block_nnz_cap()),
         "xcs_item": int(L.fsp_xcs_item_cap()),
         "xcs_rows": int(L.fsp_xcs_rows_cap()),
+        "xcs_window_slots": int(L.fsp_xcs_window_slots_cap()),
+        "xcs_window_rows": int(L.fsp_xcs_window_rows_cap()),
+        "xcs_item_runs": int(L.fsp_xcs_item_runs_cap()),
         "panel_bytes": int(L.fsp_panel_bytes_cap()),
         "panel_chunk": int(L.fsp_panel_chunk()),
     }

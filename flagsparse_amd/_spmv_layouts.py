@@ -80,6 +80,13 @@ PANEL_JOB_CHUNKS = 256
 PANEL_RUNS = 8
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
+# Combine windows of the XCS layout: consecutive rows with at most this many partial slots
+# (32 KiB of fp64 sums in LDS) and rows.
+WINDOW_SLOTS = 4096
+WINDOW_ROWS = 2048
+# Stored runs of partial sums (one item's sums in one window) start on a multiple of this many
+# slots: 128 bytes of fp64 sums, a cache line.
+RUN_ALIGN = 16
 
 
 class RowBlockLayout:
@@ -337,43 +344,21 @@ class XcsLayout:
         self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
         del packed, colp, pan, loc_row, pidx, dest
 
-        # 6. Partial slots: one per (item, row run it holds), an item's slots consecutive in
-        #    row order; per row its slots in item order (the combine's summation order).
+        # 6. Partial sums: one per (item, row run it holds); per row they are added in item
+        #    order (the combine's summation order).  Where each is stored: the combine tables.
         er = entry_row[perm]
         del entry_row, perm, key_sorted
         pair_key = torch.unique_consecutive(item_of * max(n_rows, 1) + er)  # sorted entries
         del er, item_of
-        pair_item = pair_key // max(n_rows, 1)
         pair_row = pair_key % max(n_rows, 1)
-        n_pairs = int(pair_key.numel())
-        per_item = torch.bincount(pair_item, minlength=n_items) if n_pairs else \
-            torch.zeros(n_items, dtype=torch.int64, device=dev)
-        item_slot = torch.cumsum(per_item, 0) - per_item
-        by_row = torch.sort(pair_row, stable=True)[1]  # item order kept within a row
-        count = torch.bincount(pair_row, minlength=n_rows) if n_pairs else \
+        pair_item = pair_key // max(n_rows, 1)
+        del pair_key
+        count = torch.bincount(pair_row, minlength=n_rows) if pair_row.numel() else \
             torch.zeros(n_rows, dtype=torch.int64, device=dev)
-        rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
-        torch.cumsum(count, 0, out=rp[1:])
-        # The combine's row table: head[r] = the slot of a row with exactly one slot (most
-        # rows: one load to find it); otherwise -(k + 1), k the row's place in the list of
-        # the other rows, whose slots are slots[split_ptr[k] .. split_ptr[k + 1]) (none: 0).
-        one = count == 1
-        multi = ~one
-        head = torch.empty(n_rows, dtype=torch.int64, device=dev)
-        head[one] = by_row[rp[:-1][one]]
-        head[multi] = -(torch.cumsum(multi.to(torch.int64), 0)[multi])
-        self.head = head.to(torch.int32).contiguous()
-        sp = torch.zeros(int(multi.sum().item()) + 1, dtype=torch.int64, device=dev)
-        torch.cumsum(count[multi], 0, out=sp[1:])
-        self.split_ptr = sp.to(torch.int32).contiguous()
-        keep = multi[torch.sort(pair_row, stable=True)[0]] if n_pairs else \
-            torch.zeros(0, dtype=torch.bool, device=dev)
-        split_slots = by_row[keep]
-        self.slots = split_slots.to(torch.int32).contiguous() if split_slots.numel() else \
-            torch.zeros(1, dtype=torch.int32, device=dev)
-        self.n_partials = n_pairs
         self.n_split_rows = int((count > 1).sum().item()) if n_rows else 0
-        del pair_key, pair_item, pair_row, by_row, rp, count, head, keep, split_slots
+        self.n_runs_total = int(pair_row.numel())
+        self._build_combine_windows(pair_item, pair_row, count, n_items, caps)
+        del pair_row, pair_item, count
 
         # 7. Launch order: XCD x runs the items of panels x, x + 8, x + 16, ... (one panel
         #    after the other, each in tile order); with P < 8 panel p's items are dealt in turn
@@ -402,17 +387,115 @@ class XcsLayout:
         d[:, 10] = -1
         it = order
         t = item_tile[it]
-        pb = item_slot[it]
-        d[slot_of] = torch.stack([item_start[it], item_len[it], item_k[it], torch.zeros_like(t),
-                                  t_r0_d[t],
-                                  t_R_d[t], self.panel_base.to(torch.int64)[item_panel[it]],
-                                  torch.zeros_like(t), pb & 0xFFFFFFFF, pb >> 32, t,
-                                  torch.zeros_like(it)], 1)
+        z = torch.zeros_like(t)
+        d[slot_of] = torch.stack([item_start[it], item_len[it], item_k[it],
+                                  self.item_first_run[it], t_r0_d[t], t_R_d[t],
+                                  self.panel_base.to(torch.int64)[item_panel[it]],
+                                  self.item_n_runs[it], z, z, t, z], 1)
         d = torch.where(d >= (1 << 31), d - (1 << 32), d)
         self.items = d.to(torch.int32).contiguous()
         self.n_items = n_items
         self.max_items_per_panel = q
         self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+
+    def _build_combine_windows(self, pair_item, pair_row, count, n_items, caps):
+        """Where every partial sum is stored, and the tables of the second launch
+        (xcs_window_combine_kernel).  pair_item / pair_row: the item and the row of every
+        partial sum ("pair"), in (item, row) order - the order in which an item produces them.
+
+        Rows are grouped into windows of consecutive rows with at most WINDOW_SLOTS sums and
+        WINDOW_ROWS rows (a row with more sums is a window alone, "big").  The partials buffer
+        holds the windows one after the other, and inside a window one run per item with rows
+        in it (in item order), each run starting on a multiple of RUN_ALIGN slots: an item
+        writes whole lines of its own, and the combine reads a window as one contiguous range.
+        dest gives every stored slot its position in the window's (row, item) order (-1 for
+        the padding), row_start every row its first position."""
+        dev = pair_row.device
+        n_rows, n_pairs = self.n_rows, int(pair_row.numel())
+        win_slots = min(WINDOW_SLOTS, caps["xcs_window_slots"])
+        rows_cap = min(WINDOW_ROWS, caps["xcs_window_rows"])
+        rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(count, 0, out=rp[1:])
+        plan = build_row_block_plan_windows(rp, win_slots, rows_cap, win_slots, 1 << 30,
+                                            PLAN_WINDOW_BLOCKS * rows_cap)
+        wd = plan.desc.to(device=dev, dtype=torch.int64)
+        n_win = int(wd.shape[0])
+        big = wd[:, 2] != 0  # {row, 0, 1, -1}: one row with more sums than a window holds
+        row0 = wd[:, 0]
+        nr = torch.where(big, torch.ones_like(row0), wd[:, 1] - wd[:, 0])
+        win_of_row = torch.repeat_interleave(torch.arange(n_win, device=dev), nr)
+        first_pos = rp[row0]  # a window's first sum in (row, item) order
+        pair_win = win_of_row[pair_row] if n_pairs else torch.zeros(0, dtype=torch.int64,
+                                                                    device=dev)
+        # runs: the sums of one item in one window (consecutive in pair order)
+        brk = torch.ones(n_pairs, dtype=torch.bool, device=dev)
+        if n_pairs > 1:
+            brk[1:] = (pair_item[1:] != pair_item[:-1]) | (pair_win[1:] != pair_win[:-1])
+        run_first = torch.nonzero(brk).flatten()
+        run_len = torch.diff(run_first, append=torch.tensor([n_pairs], device=dev))
+        run_item = pair_item[run_first]
+        run_win = pair_win[run_first]
+        del brk
+        n_runs = int(run_first.numel())
+        # storage: windows in order, runs of a window in item order, starts aligned unless
+        # the padding would cost more than a quarter of the buffer (short runs) or the window
+        # is big (its runs hold one sum each)
+        wkey = torch.sort(run_win * max(n_items, 1) + run_item, stable=True)[1]
+        align = RUN_ALIGN
+        padded = (run_len + align - 1) // align * align
+        if n_runs and int(padded.sum().item()) > 1.25 * n_pairs:
+            align, padded = 1, run_len.clone()
+        padded = torch.where(big[run_win], run_len, padded)
+        plen = padded[wkey]
+        base_sorted = torch.cumsum(plen, 0) - plen
+        run_base = torch.empty_like(base_sorted)
+        run_base[wkey] = base_sorted
+        n_store = int(padded.sum().item()) if n_runs else 0
+        self.run_align = align
+        # windows: {row0, rows (-1: big), first stored slot, stored slots, sums, 0, 0, 0}
+        wlen = torch.bincount(run_win, weights=padded.to(torch.float64), minlength=n_win) \
+            .to(torch.int64) if n_runs else torch.zeros(n_win, dtype=torch.int64, device=dev)
+        wbase = torch.cumsum(wlen, 0) - wlen
+        wsum = torch.bincount(pair_win, minlength=n_win) if n_pairs else \
+            torch.zeros(n_win, dtype=torch.int64, device=dev)
+        z = torch.zeros_like(row0)
+        nr_field = torch.where(big, torch.full_like(nr, -1), nr)
+        self.windows = torch.stack([row0, nr_field, wbase, wlen, wsum, z, z, z], 1) \
+            .to(torch.int32).contiguous()
+        self.n_windows = n_win
+        # every sum's stored slot, and its position in the window's (row, item) order
+        run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), run_len)
+        stored = run_base[run_of] + (torch.arange(n_pairs, device=dev) - run_first[run_of])
+        by_row = torch.sort(pair_row, stable=True)[1]
+        rank = torch.empty_like(by_row)
+        rank[by_row] = torch.arange(n_pairs, device=dev)
+        pos = rank - first_pos[pair_win]
+        pos = torch.where(big[pair_win], torch.zeros_like(pos), pos)
+        dest = torch.full((max(n_store, 1),), -1, dtype=torch.int64, device=dev)
+        dest[stored] = pos
+        self.dest = dest.to(torch.int16).contiguous()
+        row_start = rp[:-1] - first_pos[win_of_row]
+        row_start = torch.where(big[win_of_row], torch.zeros_like(row_start), row_start)
+        self.row_start = row_start.to(torch.int16).contiguous() if n_rows else \
+            torch.zeros(1, dtype=torch.int16, device=dev)
+        del by_row, rank, pos, dest, run_of, stored
+        # per item: its runs (pair order = item order, then window order), each {stored slot
+        # of its first sum, the item's index of that sum, sums, stored length}
+        first_of_item = torch.cumsum(torch.bincount(pair_item, minlength=n_items), 0) - \
+            torch.bincount(pair_item, minlength=n_items) if n_pairs else \
+            torch.zeros(n_items, dtype=torch.int64, device=dev)
+        runs_per_item = torch.bincount(run_item, minlength=n_items) if n_runs else \
+            torch.zeros(n_items, dtype=torch.int64, device=dev)
+        if n_runs and int(runs_per_item.max().item()) > caps["xcs_item_runs"]:
+            raise ValueError("an XCS item spans more combine windows than the kernel holds")
+        self.item_first_run = torch.cumsum(runs_per_item, 0) - runs_per_item
+        self.item_n_runs = runs_per_item
+        ir = torch.stack([run_base, run_first - first_of_item[run_item], run_len, padded], 1) \
+            if n_runs else torch.zeros((1, 4), dtype=torch.int64, device=dev)
+        self.item_runs = ir.to(torch.int32).contiguous()
+        self.n_partials = max(n_store, 1)
+        self.window_rows_cap = rows_cap
+        self.window_slots = win_slots
 
     def kernel_name(self):
         return "spmv_xcs_kernel"
@@ -422,7 +505,8 @@ class XcsLayout:
                 "long_row_tiles": self.n_long_tiles,
                 "items": self.n_items,
                 "slots": self.n_slots, "split_rows": self.n_split_rows,
-                "partials": self.n_partials, "panel_base": self.panel_base_host,
+                "partials": self.n_partials, "combine_windows": self.n_windows,
+                "panel_base": self.panel_base_host,
                 "col_bits": self.col_bits, "padded_entries": self.n_entries}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
@@ -434,14 +518,14 @@ class XcsLayout:
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
-                    self.n_slots, p(self.partials), p(self.head), p(self.split_ptr),
-                    p(self.slots), self.n_rows, None]
+                    self.n_slots, p(self.item_runs), p(self.partials), p(self.windows),
+                    self.n_windows, self.window_slots, p(self.dest), p(self.row_start), None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[7] = x.data_ptr(), y.data_ptr()
         a[8] = None if row_map is None else row_map.data_ptr()
         a[9] = n_out
-        a[17] = _abi.raw_stream(y.device)
+        a[19] = _abi.raw_stream(y.device)
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 
@@ -567,12 +651,13 @@ class PanelLayout:
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
                     p(self.job_panel), self.n_jobs, p(self.chunk_slot), p(self.partials),
-                    p(self.rows), p(self.row_ptr), p(self.slots), self.n_rows, None]
+                    int(self.partials.numel()), p(self.rows), p(self.row_ptr), p(self.slots),
+                    self.n_rows, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
         a[9] = None if row_map is None else row_map.data_ptr()
-        a[19] = _abi.raw_stream(y.device)
+        a[20] = _abi.raw_stream(y.device)
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 

@@ -112,37 +112,58 @@ __global__ __launch_bounds__(kBlock) void sddmm_rowblock_kernel(
     step = 4 * ngrp;
   }
   // The row of x, in registers: lane holds elements lane*VW + c*G*VW (+ j) for c < KC.
+  // Loaded without a per-lane condition (row is a row of the block for every group; a lane
+  // past K reads element 0 and zeroes it), so the KC loads are in flight together.  K == 0
+  // (x and y may then be absent) skips every load; the condition is uniform.
+  const bool any_k = K > 0;
   T xr[KC][VW];
   const T* xp = x + (int64_t)row * ldx;
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     const int k = (lane + c * G) * VW;
-    if (k < K && a < e) {
-      sload<T, VW>(xp + k, xr[c]);
+    if (any_k) {
+      sload<T, VW>(xp + (k < K ? k : 0), xr[c]);
     } else {
 #pragma unroll
       for (int j = 0; j < VW; ++j) xr[c][j] = T(0);
     }
   }
+#pragma unroll
+  for (int c = 0; c < KC; ++c)
+#pragma unroll
+    for (int j = 0; j < VW; ++j)
+      if ((lane + c * G) * VW >= K) xr[c][j] = T(0);
   const A a_alpha = A(alpha), a_beta = A(beta);
   for (int i = a; i < e; i += step) {
-    // four entries i .. i+3 of this group (fewer at the end of the range)
+    // Four entries i .. i+3 of this group (fewer at the end of the range).  All their y loads
+    // are issued before the first is used: a position past the range reads entry i's row and
+    // a lane past K reads element 0, and both are dropped below.  (A load under a per-lane
+    // condition is an exec-masked region of its own; with the products inside it the
+    // compiler waited for each load before issuing the next.)
+    T yv[4][KC][VW];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const T* yp = y + (int64_t)s_col[i + q < e ? i + q : i] * ldy;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int k = (lane + c * G) * VW;
+        if (any_k) {
+          sload<T, VW>(yp + (k < K ? k : 0), yv[q][c]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < VW; ++j) yv[q][c][j] = T(0);
+        }
+      }
+    }
     A acc[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       acc[q] = A(0);
-      if (i + q < e) {
-        const T* yp = y + (int64_t)s_col[i + q] * ldy;
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-          const int k = (lane + c * G) * VW;
-          if (k < K) {
-            T yv[VW];
-            sload<T, VW>(yp + k, yv);
+      for (int c = 0; c < KC; ++c) {
+        const bool use = i + q < e && (lane + c * G) * VW < K;
 #pragma unroll
-            for (int j = 0; j < VW; ++j) acc[q] += A(xr[c][j]) * A(yv[j]);
-          }
-        }
+        for (int j = 0; j < VW; ++j) acc[q] += use ? A(xr[c][j]) * A(yv[q][c][j]) : A(0);
       }
     }
 #pragma unroll
@@ -191,12 +212,16 @@ __global__ __launch_bounds__(kBlock) void sddmm_flat_kernel(
   for (int64_t base = first * span; base < nnz; base += (int64_t)gridDim.x * span) {
     int64_t r[kU], c[kU];
     bool ok[kU];
+    // Loads are issued for every position, past the end too (entry nnz - 1 again), and the
+    // results dropped there, so that all of a lane's loads are in flight together (a load under
+    // a per-lane condition is an exec-masked region that the compiler may wait on by itself).
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int64_t p = base + u * groups + grp;
       ok[u] = p < nnz;
-      r[u] = ok[u] ? row_ids[p] : 0;
-      c[u] = ok[u] ? cols[p] : 0;
+      const int64_t pc = ok[u] ? p : nnz - 1;
+      r[u] = row_ids[pc];
+      c[u] = cols[pc];
     }
     A acc[kU];
 #pragma unroll
@@ -205,18 +230,13 @@ __global__ __launch_bounds__(kBlock) void sddmm_flat_kernel(
       T xv[kU][VW], yv[kU][VW];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        if (ok[u]) {
-          sload<T, VW>(x + r[u] * ldx + k, xv[u]);
-          sload<T, VW>(y + c[u] * ldy + k, yv[u]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < VW; ++j) { xv[u][j] = T(0); yv[u][j] = T(0); }
-        }
+        sload<T, VW>(x + r[u] * ldx + k, xv[u]);
+        sload<T, VW>(y + c[u] * ldy + k, yv[u]);
       }
 #pragma unroll
       for (int u = 0; u < kU; ++u)
 #pragma unroll
-        for (int j = 0; j < VW; ++j) acc[u] += A(xv[u][j]) * A(yv[u][j]);
+        for (int j = 0; j < VW; ++j) acc[u] += ok[u] ? A(xv[u][j]) * A(yv[u][j]) : A(0);
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {

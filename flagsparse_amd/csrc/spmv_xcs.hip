@@ -14,11 +14,14 @@
 //           qp*t + u is at memory quad t + nt*u (coalesced loads, contiguous rows per thread)
 //   pidx    (local row << col_bits) | (column - the panel's first column)
 //   slots   one item descriptor per workgroup in launch order, 12 int32:
-//           {entry start, count, rank k in tile, 0, r0, rows R, panel first column, 0,
-//            first partial slot (2 x int32), tile (-1: empty slot), 0}
-//   rows    every item writes the sum of each row run it holds to a partial slot of its own
-//           (an item's slots are consecutive, in row order); a second launch
-//           (xcs_row_combine_kernel) gives every row the sum of its slots in item order - a
+//           {entry start, count, rank k in tile, first stored run, r0, rows R, panel first
+//            column, stored runs, 0, 0, tile (-1: empty slot), 0}
+//   rows    every item computes the sum of each row run it holds (in row order) and stores
+//           them by combine window: the sums of its rows in window w go to a run of slots of
+//           their own inside w's range (item_runs: {first slot, first sum, sums, stored
+//           length}, a run starting on a line and padded with zeros to whole lines); a second
+//           launch
+//           (xcs_window_combine_kernel) gives every row the sum of its slots in item order - a
 //           fixed order, so the result does not depend on timing - and writes y in row order.
 //           Items never write y themselves: a y line would then be written piecewise by items
 //           on several XCDs, and those partial-line writes cost more than the extra slots
@@ -51,6 +54,8 @@ namespace {
 
 constexpr int kItemCap = (int)kXcsItemCap;
 constexpr int kRowsCap = (int)kXcsRowsCap;
+constexpr int kItemRuns = (int)kXcsItemRunsCap;
+static_assert(kItemRuns <= kBlock, "an item's runs are loaded one per thread");
 
 // Occupancy cap.  The kernel needs at most 16 KiB of LDS (its partial-sum buffer) and 64
 // VGPRs, so up to 8 workgroups would share a CU; measured on MI355X, 5 per CU gathers fastest
@@ -72,7 +77,7 @@ template <typename T, typename A, bool NT>
 __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
     const T* __restrict__ x, const i32x4* __restrict__ items, int n_slots,
-    A* __restrict__ partials) {
+    const i32x4* __restrict__ item_runs, A* __restrict__ partials) {
   constexpr int kPer = kItemCap / kBlock;  // entries per thread at most
   constexpr int kQuads = kPer / 4;
   static_assert(kQuads * 4 == kPer, "whole quads of entries per thread");
@@ -84,6 +89,8 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   // The item's run sums, written out together at the end in whole lines (stored one by one
   // from the threads, partial lines could leave L2 before they filled).
   __shared__ A s_part[kItemCap];
+  // Where the sums go: one stored run per combine window the item's rows reach.
+  __shared__ i32x4 s_runs[kItemRuns];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
@@ -92,10 +99,13 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   const i32x4 d1 = items[3 * slot + 1];
   const i32x4 d2 = items[3 * slot + 2];
   if (d2.z < 0) return;  // empty slot
-  const int e0 = d0.x, len = d0.y;
-  const int R = d1.y, cbase = d1.z;
-  const int64_t sbase = (int64_t)(((uint64_t)(uint32_t)d2.y << 32) | (uint32_t)d2.x);
-  if (R <= 0 || R > kRowsCap || len < 0 || len > kItemCap) return;  // not a planner item
+  const int e0 = d0.x, len = d0.y, run0 = d0.w;
+  const int R = d1.y, cbase = d1.z, n_ir = d1.w;
+  if (R <= 0 || R > kRowsCap || len < 0 || len > kItemCap || n_ir < 0 || n_ir > kItemRuns)
+    return;  // not a planner item
+  // Issued first; stored to LDS once the entry loads are in flight.
+  i32x4 my_run = {0, 0, 0, 0};
+  if (tid < n_ir) my_run = item_runs[run0 + tid];
 
   // Entries [i0, i0 + nm) of this thread (thread-major storage, see the file comment).
   const int q_tot = (len + 3) >> 2;
@@ -126,14 +136,18 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     }
   }
   const uint32_t cmask = (1u << col_bits) - 1u;
+  // Every gather is issued, also for the positions past this thread's entries (which read the
+  // panel's first column, present in any item), and the value is dropped afterwards: a load
+  // under a per-lane condition is an exec-masked region of its own, and with the fp64
+  // conversion inside it the compiler waits for each gather before issuing the next.
   T xv[kPer];
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) xv[q] = q < nm ? x[cbase + (int)(c[q] & cmask)] : T(0);
+  for (int q = 0; q < kPer; ++q) xv[q] = x[cbase + (q < nm ? (int)(c[q] & cmask) : 0)];
   A prod[kPer];
   int row[kPer];
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
-    prod[q] = A(v[q]) * A(xv[q]);
+    prod[q] = q < nm ? A(v[q]) * A(xv[q]) : A(0);
     row[q] = (int)(c[q] >> col_bits);
   }
 
@@ -145,6 +159,7 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
     if (q < nm) my_last = row[q];
   if (lane == 0) s_first_row[wid] = my_first;
   if (lane == kWave - 1) s_last_row[wid] = my_last;
+  if (tid < n_ir) s_runs[tid] = my_run;
   __syncthreads();
   int prev_row = __shfl_up(my_last, 1, kWave);
   if (lane == 0) prev_row = wid > 0 ? s_last_row[wid - 1] : -1;
@@ -207,14 +222,13 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   if (lane == 0) { h_ex = 0; v_ex = A(0); c_ex = 0; }
   __syncthreads();
   A pv = A(0);
-  int pc = 0, n_runs = 0;
+  int pc = 0;
   for (int j = 0; j < kWavesPerBlock; ++j) {
     if (j < wid) {  // waves before this one, in order
       const A wv = s_wv[j];
       if (!s_wh[j]) pv = pv + wv; else pv = wv;
       pc += s_wc[j];
     }
-    n_runs += s_wc[j];
   }
   const A carry = h_ex ? v_ex : pv + v_ex;
 
@@ -235,45 +249,92 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   }
   if (last_ends) *out = (first && cont) ? carry + run : run;
   __syncthreads();
-  for (int i = tid; i < n_runs; i += kBlock) partials[sbase + i] = s_part[i];
+  // Out in whole lines: run j holds the item's sums [r.y, r.y + r.z) at stored slots from r.x,
+  // padded with zeros to r.w slots (a run starts on a line, so no line has two writers).
+  for (int j = 0; j < n_ir; ++j) {
+    const i32x4 r = s_runs[j];
+    for (int l = tid; l < r.w; l += kBlock) partials[r.x + l] = l < r.z ? s_part[r.y + l] : A(0);
+  }
 }
 
-// Second pass: row i gets y = the sum of its slots in item order (a fixed order), 0 without
-// any.  head[i] >= 0 is the slot of a row with exactly one (most rows: one load to find it);
-// head[i] = -(k + 1) points to slots[split_ptr[k] .. split_ptr[k+1]) (on cfg3's short rows,
-// 6 us less than a row pointer and a slot list for every row).  Consecutive threads take
-// consecutive rows, so y is written in whole lines.  A separate launch: the kernel boundary
-// makes the first pass's partials visible on every XCD, so neither pass needs a device-scope
-// fence.
+// Second pass: row r gets y = the sum of its partial sums in item order (a fixed order, so the
+// result does not depend on timing), 0 without any.  Rows are grouped into windows of
+// consecutive rows whose sums fit LDS (<= kXcsWinSlotsCap sums, <= kXcsWinRowsCap rows), and
+// the partials buffer holds the windows one after the other (inside a window one run per item,
+// each starting on a cache line, see spmv_xcs_kernel).  A workgroup per window:
+//   1. streams the window's stored range with every load of a thread issued before the first
+//      is used, and scatters each sum to LDS position dest[slot] - the window's sums in
+//      (row, item) order; padding slots (dest -1) are dropped;
+//   2. gives row r the sum of LDS positions [row_start[r], row_start[r + 1]) (the window's
+//      number of sums for its last row), in order, and writes y in row order.
+// A window of one row with more sums than LDS holds ({row, -1, ...}: a row longer than a
+// tile) is summed by the whole workgroup - thread t takes its slots t, t + 256, ... in order,
+// then the fixed workgroup tree.
+// A separate launch: the kernel boundary makes the first pass's partials visible on every
+// XCD, so neither pass needs a device-scope fence.
+constexpr int kWinPer = 8;  // loads per thread and round of the stream step
+constexpr int kWinRound = kWinPer * kBlock;
+
 template <typename T, typename A>
-__global__ __launch_bounds__(kBlock) void xcs_row_combine_kernel(
-    const int* __restrict__ head, const int* __restrict__ split_ptr,
-    const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
-    const int* __restrict__ row_map, int n_rows) {
-  const int i = blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n_rows) return;
-  const int h = head[i];
-  A acc = A(0);
-  if (h >= 0) {
-    acc += partials[h];
-  } else {
-    const int a = split_ptr[-h - 1], b = split_ptr[-h];
-    // Eight slots per round: all slot indices, then all partials, are requested before the
-    // first is used, so a row costs two memory round trips per eight slots, not two per slot.
-    constexpr int kU = 8;
-    for (int j0 = a; j0 < b; j0 += kU) {
-      int sl[kU];
-      A pv[kU];
+__global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
+    const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
+    const int16_t* __restrict__ row_start, const A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map, int win_cap) {
+  // win_cap sums of LDS (the layout's window size): smaller windows leave room for more
+  // workgroups per CU, whose stream and sum phases then overlap.
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  A* const s_val = reinterpret_cast<A*>(s_dyn);
+  __shared__ A s_red[kWavesPerBlock];
+  const int tid = threadIdx.x;
+  const i32x4 w0 = windows[2 * blockIdx.x];
+  const int total = windows[2 * blockIdx.x + 1].x;
+  const int row0 = w0.x, nr = w0.y, base = w0.z, len = w0.w;
+
+  if (nr < 0) {  // one row with more sums than LDS holds: a workgroup sum in a fixed order
+    A acc = A(0);
+    for (int l = tid; l < len; l += kBlock) acc += partials[base + l];
+    acc = block_sum(acc, s_red);
+    if (tid == 0) y[row_map ? row_map[row0] : row0] = T(acc);
+    return;
+  }
+  if (nr > (int)kXcsWinRowsCap || total > win_cap) return;  // not a layout window (uniform)
+
+  // Row starts of this thread's rows, requested first (they do not depend on LDS).
+  constexpr int kRowsPer = (int)(kXcsWinRowsCap / kBlock);
+  int rs[kRowsPer], re[kRowsPer];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) sl[u] = j0 + u < b ? slots[j0 + u] : -1;
+  for (int m = 0; m < kRowsPer; ++m) {
+    const int i = tid + m * kBlock;
+    rs[m] = i < nr ? (int)row_start[row0 + i] : 0;
+    re[m] = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
+  }
+
+  for (int c0 = 0; c0 < len; c0 += kWinRound) {  // uniform
+    A v[kWinPer];
+    int d[kWinPer];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) pv[u] = sl[u] >= 0 ? partials[sl[u]] : A(0);
+    for (int k = 0; k < kWinPer; ++k) {
+      const int j = c0 + tid + k * kBlock;
+      const int jj = j < len ? j : 0;  // past the end: reload the first slot, dropped below
+      v[k] = partials[base + jj];
+      d[k] = (int)dest[base + jj];
+    }
 #pragma unroll
-      for (int u = 0; u < kU; ++u)
-        if (j0 + u < b) acc += pv[u];
+    for (int k = 0; k < kWinPer; ++k)
+      if (c0 + tid + k * kBlock < len && (unsigned)d[k] < (unsigned)win_cap) s_val[d[k]] = v[k];
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    const int i = tid + m * kBlock;
+    if (i < nr) {
+      A acc = A(0);
+      for (int k = rs[m]; k < re[m]; ++k) acc += s_val[k];
+      const int row = row0 + i;
+      y[row_map ? row_map[row] : row] = T(acc);
     }
   }
-  y[row_map ? row_map[i] : i] = T(acc);
 }
 
 // Panel layout (see the file comment): one workgroup per job, waves independent after the
@@ -281,6 +342,20 @@ __global__ __launch_bounds__(kBlock) void xcs_row_combine_kernel(
 // the runs that end in a lane are emitted by it, the first one with the carry from the lanes
 // before (a segmented wave scan), into consecutive slots from chunk_slot[c] in entry order.
 constexpr int kPanelBlock = 512;
+// Word 3 of a raw buffer resource on gfx9-family GPUs (gfx950): 32-bit data format, no swizzle.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+// A byte offset no buffer here reaches: a store there is dropped by the range check.
+constexpr unsigned kDropOffset = 0xFFFFFFF0u;
+
+template <typename A>
+__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned off, A v) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(A) == 8) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
+  }
+}
 constexpr int kPanelPerLane = (int)kPanelChunk / kWave;
 static_assert(kPanelPerLane == 8, "eight entries per lane");
 
@@ -289,22 +364,26 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
     const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
     const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
-    A* __restrict__ partials) {
+    A* __restrict__ partials, int64_t n_partials) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
+  // The partial sums as a buffer resource of n_partials slots (< 2^32 bytes, checked by the
+  // host): stores beyond it are dropped by the hardware.
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      partials, 0, (int)(n_partials * (int64_t)sizeof(A)), kBufferRsrcWord3);
   T* const sx = reinterpret_cast<T*>(s_dyn);
   const int job = blockIdx.x;
   const int64_t pbase = (int64_t)job_panel[job] << col_bits;
   const int64_t rest = x_len - pbase;
   const int width = rest < ((int64_t)1 << col_bits) ? (int)rest : (1 << col_bits);
-  for (int i = threadIdx.x; i < width; i += kPanelBlock) sx[i] = x[pbase + i];
-  __syncthreads();
-
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const uint32_t cmask = (1u << col_bits) - 1u;
   const int c_hi = jobs[job + 1];
   // The entries are streamed once with non-temporal loads, and the next chunk's loads are
-  // issued before the current chunk is reduced, so a wave keeps two chunks in flight.
-  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], uint32_t (&c)[kPanelPerLane]) {
+  // issued before the current chunk is reduced, so a wave keeps two chunks in flight.  The
+  // chunk's first slot is loaded with its entries: loaded on its own after the next chunk's
+  // loads, waiting for it (loads complete in order) also waited for the whole next chunk.
+  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], uint32_t (&c)[kPanelPerLane],
+                        int& slot0) {
     const int64_t e0 = (int64_t)chunk * kPanelChunk;
 #pragma unroll
     for (int h = 0; h < kPanelPerLane / 4; ++h) {
@@ -321,21 +400,13 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       c[4 * h] = (uint32_t)cc.x; c[4 * h + 1] = (uint32_t)cc.y;
       c[4 * h + 2] = (uint32_t)cc.z; c[4 * h + 3] = (uint32_t)cc.w;
     }
+    slot0 = chunk_slot[chunk];
   };
-  constexpr int kStride = kPanelBlock / kWave;
-  T vn[kPanelPerLane];
-  uint32_t cn[kPanelPerLane];
-  int ch = jobs[job] + wid;
-  if (ch < c_hi) load_chunk(ch, vn, cn);
-  for (; ch < c_hi; ch += kStride) {
-    T v[kPanelPerLane];
-    uint32_t c[kPanelPerLane];
-#pragma unroll
-    for (int q = 0; q < kPanelPerLane; ++q) {
-      v[q] = vn[q];
-      c[q] = cn[q];
-    }
-    if (ch + kStride < c_hi) load_chunk(ch + kStride, vn, cn);
+  // One chunk's reduction: products from the LDS panel, then the runs (rows) that end in each
+  // lane are emitted, the first one with the carry from the lanes before (a segmented wave
+  // scan), into consecutive slots from the chunk's first.
+  auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const uint32_t (&c)[kPanelPerLane],
+                          int slot0) {
     A prod[kPanelPerLane];
     int row[kPanelPerLane];
 #pragma unroll
@@ -379,41 +450,97 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     A carry = __shfl_up(v_in, 1, kWave);
     int slot = __shfl_up(c_in, 1, kWave);
     if (lane == 0) { carry = A(0); slot = 0; }
-    A* out = partials + chunk_slot[ch] + slot;
+    // Emission: eight stores per lane, always issued - a lane without a run ending at q
+    // stores past the end of the buffer, which the buffer range check drops.  Under per-lane
+    // conditions the number of stores varied, and the compiler then waited for every
+    // outstanding memory operation (the prefetched chunks included) before each chunk.
+    unsigned k = (unsigned)(slot0 + slot);
     bool first = true;
     A run = A(0);
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
-      if (q > 0 && row[q] != row[q - 1]) {
-        *out++ = (first && cont) ? carry + run : run;
+      run += prod[q];
+      const bool ends = q < kLast ? row[q] != row[q + 1] : row[kLast] != next_row;
+      store_partial(out_rsrc, ends ? k * (unsigned)sizeof(A) : kDropOffset,
+                    (first && cont) ? carry + run : run);
+      if (ends) {
+        ++k;
         first = false;
         run = A(0);
       }
-      run += prod[q];
     }
-    if (row[kLast] != next_row) *out = (first && cont) ? carry + run : run;
+  };
+
+  // Three chunk buffers per wave: while one chunk is reduced, the next two are in flight (with
+  // two, the next chunk was requested only one reduction before it was needed, and the waves
+  // waited on memory: 5.2 TB/s on cfg3's long rows).
+  constexpr int kStride = kPanelBlock / kWave;
+  T va[kPanelPerLane], vb[kPanelPerLane], vc[kPanelPerLane];
+  uint32_t ca[kPanelPerLane], cb[kPanelPerLane], cc[kPanelPerLane];
+  int sa = 0, sb = 0, sc = 0;
+  int ch = jobs[job] + wid;
+  // The first chunks' entries are requested before the panel copy, so the two overlap.
+  if (ch < c_hi) load_chunk(ch, va, ca, sa);
+  if (ch + kStride < c_hi) load_chunk(ch + kStride, vb, cb, sb);
+
+  // Panel copy: every thread issues all its 16-byte loads before its first LDS store (one
+  // memory round trip; as a load-store loop the copy waited for each load in turn).  A panel
+  // starts at a multiple of 2^col_bits values; the vector part needs x 16-byte aligned there.
+  {
+    constexpr int kVec = 16 / (int)sizeof(T);
+    constexpr int kCopy = (int)(kPanelBytes / 16 / kPanelBlock);  // vectors per thread, at most
+    const T* src = x + pbase;
+    const bool vec_ok = (reinterpret_cast<uintptr_t>(src) & 15u) == 0;
+    const int n_vec = vec_ok ? width / kVec : 0;
+    i32x4 buf[kCopy];
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) {
+      const int i = (int)threadIdx.x + k * kPanelBlock;
+      if (i < n_vec) buf[k] = *reinterpret_cast<const i32x4*>(src + (int64_t)i * kVec);
+    }
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) {
+      const int i = (int)threadIdx.x + k * kPanelBlock;
+      if (i < n_vec) *reinterpret_cast<i32x4*>(sx + i * kVec) = buf[k];
+    }
+    for (int i = n_vec * kVec + (int)threadIdx.x; i < width; i += kPanelBlock) sx[i] = src[i];
+  }
+  __syncthreads();
+
+  for (; ch < c_hi; ch += 3 * kStride) {
+    if (ch + 2 * kStride < c_hi) load_chunk(ch + 2 * kStride, vc, cc, sc);
+    reduce_chunk(va, ca, sa);
+    if (ch + kStride >= c_hi) break;
+    if (ch + 3 * kStride < c_hi) load_chunk(ch + 3 * kStride, va, ca, sa);
+    reduce_chunk(vb, cb, sb);
+    if (ch + 2 * kStride >= c_hi) break;
+    if (ch + 4 * kStride < c_hi) load_chunk(ch + 4 * kStride, vb, cb, sb);
+    reduce_chunk(vc, cc, sc);
   }
 }
 
 template <typename T, typename A>
 int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
-               const int32_t* row_map, const int32_t* items, int64_t n_slots, void* partials,
-               const int32_t* head, const int32_t* split_ptr, const int32_t* slots,
-               int64_t n_rows, hipStream_t st) {
+               const int32_t* row_map, const int32_t* items, int64_t n_slots,
+               const int32_t* item_runs, void* partials, const int32_t* windows,
+               int64_t n_windows, int64_t window_slots, const int16_t* dest,
+               const int16_t* row_start, hipStream_t st) {
   if (n_slots > 0) {
     hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
                        xcs_lds_reserve<A>(), st, static_cast<const T*>(vals), pidx, col_bits,
                        static_cast<const T*>(x), reinterpret_cast<const i32x4*>(items),
-                       (int)n_slots, static_cast<A*>(partials));
+                       (int)n_slots, reinterpret_cast<const i32x4*>(item_runs),
+                       static_cast<A*>(partials));
     int rc = check_hip(hipGetLastError(), "spmv_xcs_kernel launch");
     if (rc) return rc;
   }
-  if (n_rows == 0) return FSP_OK;
-  const int64_t blocks = (n_rows + kBlock - 1) / kBlock;
-  hipLaunchKernelGGL((xcs_row_combine_kernel<T, A>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                     head, split_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
-                     row_map, (int)n_rows);
-  return check_hip(hipGetLastError(), "xcs_row_combine_kernel launch");
+  if (n_windows == 0) return FSP_OK;
+  hipLaunchKernelGGL((xcs_window_combine_kernel<T, A>), dim3((unsigned)n_windows), dim3(kBlock),
+                     (size_t)window_slots * sizeof(A), st,
+                     reinterpret_cast<const i32x4*>(windows), dest, row_start,
+                     static_cast<const A*>(partials), static_cast<T*>(y), row_map,
+                     (int)window_slots);
+  return check_hip(hipGetLastError(), "xcs_window_combine_kernel launch");
 }
 
 // Second pass of the panel layout: its rows have hundreds of slots each, so one wave adds a
@@ -450,13 +577,14 @@ template <typename T, typename A>
 int launch_panels(const void* vals, const uint32_t* pidx, int col_bits, const void* x,
                   int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
                   const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_slot,
-                  void* partials, const int32_t* rows, const int32_t* row_ptr,
-                  const int32_t* slots, int64_t n_rows, hipStream_t st) {
+                  void* partials, int64_t n_partials, const int32_t* rows,
+                  const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                  hipStream_t st) {
   if (n_jobs > 0) {
     hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
                        ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
                        pidx, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
-                       chunk_slot, static_cast<A*>(partials));
+                       chunk_slot, static_cast<A*>(partials), n_partials);
     int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
     if (rc) return rc;
   }
@@ -478,52 +606,59 @@ using namespace fsp;
 extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                             int64_t n_entries, int col_bits, const void* x, void* y,
                             const int32_t* row_map, int64_t n_out, const int32_t* items,
-                            int64_t n_slots, void* partials, const int32_t* head,
-                            const int32_t* split_ptr, const int32_t* slots, int64_t n_rows,
-                            void* stream) {
+                            int64_t n_slots, const int32_t* item_runs, void* partials,
+                            const int32_t* windows, int64_t n_windows, int64_t window_slots,
+                            const int16_t* dest, const int16_t* row_start, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
-  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_rows < 0)
+  if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_windows < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: negative size");
   if (n_entries > 0x7fffffffLL - kXcsItemCap || n_slots > 0x3fffffffLL ||
-      n_rows > 0x7fffffffLL - kBlock)
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or rows");
+      n_windows > 0x3fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or windows");
   if (col_bits < 1 || col_bits > 24)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: col_bits outside [1, 24]");
-  if (n_slots > 0 && (!vals || !pidx || !x || !items || !partials))
+  if (n_windows > 0 && (window_slots < 1 || window_slots > kXcsWinSlotsCap))
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: window_slots outside [1, " +
+                                     std::to_string(kXcsWinSlotsCap) + "]");
+  if (n_slots > 0 && (!vals || !pidx || !x || !items || !item_runs || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null pointer");
-  if (n_rows > 0 && (!y || !head || !split_ptr || !slots || !partials))
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: null row pointer");
-  if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items))
-    return set_error(FSP_EINVAL, "fsp_spmv_xcs: vals, pidx and items must be 16-byte aligned");
+  if (n_windows > 0 && (!y || !windows || !dest || !row_start || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: null combine-table pointer");
+  if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items) || !aligned16(item_runs) ||
+      !aligned16(windows))
+    return set_error(FSP_EINVAL,
+                     "fsp_spmv_xcs: vals, pidx, items, item_runs and windows must be 16-byte "
+                     "aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (row_map && n_out > 0) {
     int rc = (dtype == FSP_F32) ? fill_zero<float>(static_cast<float*>(y), n_out, st)
                                 : fill_zero<double>(static_cast<double*>(y), n_out, st);
     if (rc) return rc;
   }
+#define FSP_XCS_ARGS vals, pidx, col_bits, x, y, row_map, items, n_slots, item_runs, partials, \
+                     windows, n_windows, window_slots, dest, row_start, st
   if (dtype == FSP_F32) {
-    if (acc_f64)
-      return launch_xcs<float, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                       partials, head, split_ptr, slots, n_rows, st);
-    return launch_xcs<float, float>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                    partials, head, split_ptr, slots, n_rows, st);
+    if (acc_f64) return launch_xcs<float, double>(FSP_XCS_ARGS);
+    return launch_xcs<float, float>(FSP_XCS_ARGS);
   }
-  return launch_xcs<double, double>(vals, pidx, col_bits, x, y, row_map, items, n_slots,
-                                    partials, head, split_ptr, slots, n_rows, st);
+  return launch_xcs<double, double>(FSP_XCS_ARGS);
+#undef FSP_XCS_ARGS
 }
 
 extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                                int64_t n_entries, int col_bits, const void* x, int64_t x_len,
                                void* y, const int32_t* row_map, const int32_t* jobs,
                                const int32_t* job_panel, int64_t n_jobs,
-                               const int32_t* chunk_slot, void* partials, const int32_t* rows,
-                               const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
-                               void* stream) {
+                               const int32_t* chunk_slot, void* partials, int64_t n_partials,
+                               const int32_t* rows, const int32_t* row_ptr,
+                               const int32_t* slots, int64_t n_rows, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
     return set_error(FSP_ENOTSUP, "fsp_spmv_panels: dtype");
   const int64_t vsize = dtype == FSP_F32 ? 4 : 8;
-  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0)
+  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0 || n_partials < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: negative size");
+  if (n_partials * 8 > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: more partial slots than 2^31 bytes hold");
   if (n_entries % kPanelChunk != 0 || n_entries / kPanelChunk > 0x7fffffffLL ||
       n_jobs > 0x7fffffffLL || n_rows > 0x7fffffffLL - kBlock)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: n_entries must be a multiple of " +
@@ -542,13 +677,13 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
   if (dtype == FSP_F32) {
     if (acc_f64)
       return launch_panels<float, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
-                                          job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
-                                          slots, n_rows, st);
+                                          job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                          row_ptr, slots, n_rows, st);
     return launch_panels<float, float>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
-                                       slots, n_rows, st);
+                                       job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                       row_ptr, slots, n_rows, st);
   }
   return launch_panels<double, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_slot, partials, rows, row_ptr,
-                                       slots, n_rows, st);
+                                       job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                       row_ptr, slots, n_rows, st);
 }

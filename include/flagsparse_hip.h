@@ -74,6 +74,9 @@ int64_t fsp_spmv_chunk_nnz_cap(void);    /* max nnz of one long-row chunk       
 int64_t fsp_spmm_block_nnz_cap(void);    /* max nnz of one SpMM row block / row part  */
 int64_t fsp_xcs_item_cap(void);          /* max entries of one XCS item               */
 int64_t fsp_xcs_rows_cap(void);          /* max rows of one XCS tile                  */
+int64_t fsp_xcs_window_slots_cap(void);  /* max partial slots of one XCS combine window */
+int64_t fsp_xcs_window_rows_cap(void);   /* max rows of one XCS combine window        */
+int64_t fsp_xcs_item_runs_cap(void);     /* max stored runs (windows) of one XCS item */
 int64_t fsp_panel_bytes_cap(void);       /* max bytes of one x panel (panel SpMV)     */
 int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)            */
 
@@ -159,22 +162,32 @@ int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
  *   col_bits     in [1, 24]
  *   row_map      NULL: layout row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
  *   items        n_slots slots of 12 int32 in launch order (slot j runs on XCD j / (n_slots/8)
- *                when n_slots is a multiple of 8): {entry start, count, rank k in tile, 0, r0,
- *                rows, panel first column, 0, first partial slot as two int32 (low, high),
- *                tile (-1 marks an empty slot), 0}
- *   partials     one slot of 8 bytes per (item, row run it holds); an item's slots are
- *                consecutive in row order
- *   head, split_ptr, slots
- *                n_rows rows, each given y (a second launch on the same stream, y written in
- *                row order): head[i] >= 0 - the row's only slot, partials[head[i]]; head[i] =
- *                -(k + 1) - the sum of partials[slots[j]], j in [split_ptr[k], split_ptr[k+1])
- *                increasing, 0 for an empty range.  Calls sharing partials must not overlap.
+ *                when n_slots is a multiple of 8): {entry start, count, rank k in tile, first
+ *                stored run, r0, rows, panel first column, stored runs (<=
+ *                fsp_xcs_item_runs_cap()), 0, 0, tile (-1 marks an empty slot), 0}
+ *   item_runs    int32 quadruples {first slot, first sum, sums, stored length}: an item's row
+ *                run sums (in row order) [first sum, first sum + sums) go to partials[first
+ *                slot ...], followed by zeros up to the stored length
+ *   partials     8 bytes per stored slot
+ *   windows, dest, row_start
+ *                the second launch (y written in row order), one workgroup per window:
+ *                windows[w] = 8 int32 {row0, rows, first slot, stored length, sums, 0, 0, 0}:
+ *                rows [row0, row0 + rows) (<= fsp_xcs_window_rows_cap()) take their sums from
+ *                partials[first slot .. + stored length): slot s goes to position dest[s] of the
+ *                window (its rank in (row, item) order; -1: padding, dropped; at most
+ *                window_slots <= fsp_xcs_window_slots_cap() sums, the LDS each workgroup
+ *                takes) and row r gets the sum, in that order, of
+ *                positions [row_start[r], row_start[r + 1]) (the window's number of sums for its
+ *                last row; int16, relative to the window).  rows = -1: one row given the sum of
+ *                all the window's slots (more than fit one window).  Calls sharing partials
+ *                must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  int64_t n_entries, int col_bits, const void* x, void* y,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
-                 void* partials, const int32_t* head, const int32_t* split_ptr,
-                 const int32_t* slots, int64_t n_rows, void* stream);
+                 const int32_t* item_runs, void* partials, const int32_t* windows,
+                 int64_t n_windows, int64_t window_slots, const int16_t* dest,
+                 const int16_t* row_start, void* stream);
 
 /*
  * y[rows[i]] (y[row_map[rows[i]]] when row_map != NULL) = row i of A @ x for the long rows of
@@ -191,6 +204,8 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])
  *   chunk_slot   per chunk the first partial slot (8 bytes each); a chunk writes one slot per
  *                row it holds, in entry order
+ *   n_partials   slots in partials (n_partials * 8 < 2^31: the kernel stores through a buffer
+ *                resource of that size)
  *   rows, row_ptr, slots
  *                n_rows long rows; rows[i] gets the sum of partials[slots[k]], k in
  *                [row_ptr[i], row_ptr[i+1]) (a second launch, one wave per row: lane l adds
@@ -201,8 +216,8 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pi
                     int64_t n_entries, int col_bits, const void* x, int64_t x_len, void* y,
                     const int32_t* row_map, const int32_t* jobs, const int32_t* job_panel,
                     int64_t n_jobs, const int32_t* chunk_slot, void* partials,
-                    const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
-                    int64_t n_rows, void* stream);
+                    int64_t n_partials, const int32_t* rows, const int32_t* row_ptr,
+                    const int32_t* slots, int64_t n_rows, void* stream);
 
 /*
  * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)

@@ -195,9 +195,9 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert b"split-row" in L.fsp_last_error()
     assert spmm(lanes=3) == -1                    # lanes_per_row not a power of two
     assert spmm(dtype=1, lanes=4, vec=4) == -1    # 4-wide vectors are fp32 only
-    def xcs(col_bits=10, n_rows=0):
+    def xcs(col_bits=10, n_windows=0):
         return L.fsp_spmv_xcs(0, 0, None, None, 0, col_bits, None, None, None, 0, None, 0, None,
-                              None, None, None, n_rows, None)
+                              None, None, n_windows, 1024, None, None, None)
 
     # fsp_index_stats(a, a_bits, b, b_bits, n, partial, out, stream)
     assert L.fsp_index_stats(None, 16, None, 32, 0, None, None, None) == -1
@@ -209,18 +209,21 @@ def test_kernel_entry_points_reject_before_any_hip_call():
 
     assert xcs() == 0                             # nothing to run
     assert xcs(col_bits=25) == -1                 # col_bits > 24
-    assert xcs(n_rows=4) == -1                    # combine without its arrays
+    assert xcs(n_windows=4) == -1                 # combine without its tables
     assert b"null" in L.fsp_last_error()
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1
 
-    def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0):
+    def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0, n_partials=0):
         return L.fsp_spmv_panels(dtype, 0, None, None, n_entries, col_bits, None, 1, None, None,
-                                 None, None, n_jobs, None, None, None, None, None, n_rows, None)
+                                 None, None, n_jobs, None, None, n_partials, None, None, None,
+                                 n_rows, None)
 
     assert panels() == 0                          # nothing to run
     assert panels(dtype=5) == -3
     assert panels(n_entries=100) == -1            # not a whole number of chunks
     assert b"multiple" in L.fsp_last_error()
+    assert panels(n_partials=1 << 28) == -1       # partials beyond the buffer resource range
+    assert b"partial" in L.fsp_last_error()
     assert panels(col_bits=15) == -1              # 2^15 fp32 > 64 KiB of LDS
     assert panels(dtype=1, col_bits=14) == -1     # 2^14 fp64 > 64 KiB
     assert b"LDS" in L.fsp_last_error()

@@ -31,56 +31,100 @@ def _item_positions(e0, ln):
 
 
 def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
-    """numpy restatement of spmv_xcs_kernel + xcs_row_combine_kernel over the layout: every
-    item writes each row run it holds to its next slot (in row order); row r then gets the sum
-    of its slots in the listed (item) order, 0 without any, at y[row_map[r]] when a row map is
-    given."""
+    """numpy restatement of spmv_xcs_kernel + xcs_window_combine_kernel over the layout: every
+    item sums each row run it holds (in row order) and stores the sums through its runs
+    (item_runs: {first slot, first sum, sums, stored length}, zeros after the sums); each combine
+    window then places its stored slots at their dest positions (-1: padding) and row r gets
+    the sum of positions [row_start[r], row_start[r + 1]) in order - its sums in item order -,
+    0 without any, at y[row_map[r]] when a row map is given.  A big window (rows -1) is one row
+    given the sum of all its slots."""
+    caps = _spmv_layouts._abi.caps()
     items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
+    item_runs = layout.item_runs.numpy().astype(np.int64)
     vals = layout.vals.numpy().astype(acc)
     pidx = layout.pidx.numpy().view(np.uint32)
     cbits = layout.col_bits
     out = (lambda r: r) if row_map is None else (lambda r: int(row_map[r]))  # noqa: E731
     y = np.full(layout.n_rows, np.nan) if y is None else y
-    partials = np.full(max(layout.n_partials, 1), np.nan)
-    written = np.zeros(max(layout.n_partials, 1), dtype=bool)
-    for e0, ln, k, _, r0, R, cbase, _, plo, phi, tile, _ in items:
+    n_store = layout.n_partials
+    partials = np.full(n_store, np.nan)
+    slot_row = np.full(n_store, -1, dtype=np.int64)  # -2: padding
+    slot_item = np.full(n_store, -1, dtype=np.int64)
+    for e0, ln, k, run0, r0, R, cbase, n_ir, _, _, tile, _ in items:
         if tile < 0:
             continue
-        slot = (plo & 0xFFFFFFFF) | (phi << 32)
+        assert 0 <= n_ir <= caps["xcs_item_runs"]
         pos = _item_positions(e0, ln)
         p = pidx[pos]
         lrow = (p >> cbits).astype(np.int64)
         col = cbase + (p & ((1 << cbits) - 1)).astype(np.int64)
         prod = vals[pos] * x[col].astype(acc)
         assert np.all(np.diff(lrow) >= 0) and np.all(lrow < R)
+        sums, rows = [], []
         for r in np.unique(lrow):  # runs in row order
             s = acc(0)
             for v in prod[lrow == r]:
                 s = acc(s + v)
-            assert not written[slot]
-            partials[slot] = s
-            written[slot] = True
-            slot += 1
-    assert written[:layout.n_partials].all()
-    # the combine's row table: head >= 0 is a row's only slot, else -(k + 1) points to the
-    # k-th slot list; every slot is used by exactly one row
-    head = layout.head.numpy().astype(np.int64)
-    sp = layout.split_ptr.numpy()
-    slots = layout.slots.numpy()
-    used = np.zeros(max(layout.n_partials, 1), dtype=np.int64)
-    for r in range(layout.n_rows):
-        s = acc(0)
-        if head[r] >= 0:
-            s = acc(s + partials[head[r]])
-            used[head[r]] += 1
-        else:
-            k = -head[r] - 1
-            assert sp[k + 1] - sp[k] != 1  # one-slot rows use head
-            for j in range(sp[k], sp[k + 1]):
-                s = acc(s + partials[slots[j]])
-                used[slots[j]] += 1
-        y[out(r)] = s
-    assert np.all(used[:layout.n_partials] == 1)
+            sums.append(s)
+            rows.append(r0 + r)
+        nxt = 0
+        for first, s0, cnt, stored in item_runs[run0:run0 + n_ir]:
+            assert s0 == nxt and stored >= cnt  # the runs take the sums in order
+            for j in range(stored):
+                assert slot_row[first + j] == -1  # one writer per slot
+                if j < cnt:
+                    partials[first + j] = sums[s0 + j]
+                    slot_row[first + j] = rows[s0 + j]
+                    slot_item[first + j] = run0  # increases with the item number
+                else:
+                    partials[first + j] = 0.0
+                    slot_row[first + j] = -2
+            nxt = s0 + cnt
+        assert nxt == len(sums)
+    # the combine windows: consecutive rows and consecutive stored ranges, every slot once
+    windows = layout.windows.numpy().reshape(-1, 8).astype(np.int64)
+    dest = layout.dest.numpy().astype(np.int64)
+    row_start = layout.row_start.numpy().astype(np.int64)
+    next_row, next_slot = 0, 0
+    for row0, nr, base, ln, total, _, _, _ in windows:
+        assert row0 == next_row and base == next_slot
+        sl = np.arange(base, base + ln)
+        next_slot = base + ln
+        real = sl[slot_row[sl] >= 0] if ln else sl
+        assert real.size == total
+        if nr < 0:  # one row with more sums than a window holds
+            assert total > layout.window_slots and ln == total
+            assert np.all(slot_row[sl] == row0)
+            s = acc(0)
+            for v in partials[sl]:
+                s = acc(s + v)
+            y[out(row0)] = s
+            next_row = row0 + 1
+            continue
+        assert total <= layout.window_slots <= caps["xcs_window_slots"]
+        assert 1 <= nr <= caps["xcs_window_rows"]
+        assert np.all(dest[sl][slot_row[sl] == -2] == -1)  # padding dropped
+        d = dest[real]
+        assert sorted(d.tolist()) == list(range(total))  # a permutation of the positions
+        lds = np.full(total, np.nan)
+        lds[d] = partials[real]
+        lds_slot = np.full(total, -1, dtype=np.int64)
+        lds_slot[d] = real
+        for i in range(nr):
+            a = row_start[row0 + i]
+            b = row_start[row0 + i + 1] if i + 1 < nr else total
+            mine = lds_slot[a:b]
+            # the row's own sums, all of them, in item order
+            assert np.all(slot_row[mine] == row0 + i)
+            assert np.all(np.diff(slot_item[mine]) > 0)
+            assert mine.size == int(np.sum(slot_row[sl] == row0 + i))
+            s = acc(0)
+            for v in lds[a:b]:
+                s = acc(s + v)
+            y[out(row0 + i)] = s
+        next_row = row0 + nr
+    assert next_row == layout.n_rows and next_slot == max(n_store, 1) or n_store == 1
+    assert np.all(slot_row != -1) or n_store == 1
     return y
 
 
@@ -262,6 +306,46 @@ def test_xcs_skewed_columns_and_empty_matrix():
     ip0 = torch.zeros(5001, dtype=torch.int64)
     lay = XcsLayout(torch.empty(0), torch.empty(0, dtype=torch.int32), ip0, 100)
     assert np.all(_emulate(lay, np.ones(100)) == 0.0)
+
+
+@pytest.mark.parametrize("win_slots,win_rows", [(8, 2048), (64, 16), (4096, 3)])
+def test_xcs_combine_windows(win_slots, win_rows, monkeypatch):
+    # small combine windows: rows with more slots than a window holds become one-row windows
+    # (summed whole), tiles cut into several windows, windows of a few rows
+    monkeypatch.setattr(_spmv_layouts, "WINDOW_SLOTS", win_slots)
+    monkeypatch.setattr(_spmv_layouts, "WINDOW_ROWS", win_rows)
+    # tiny windows make an item reach more of them than the kernel's run table holds; the
+    # emulation checks the layout logic, so the cap is lifted here
+    real = _abi.caps()
+    monkeypatch.setattr(_spmv_layouts._abi, "caps", lambda: dict(real, xcs_item_runs=1 << 20))
+    lengths = [3, 0, 40000, 1, 1, 2] + [0] * 900 + [17000, 5, 0, 2048 * 3, 7] + [9] * 3000
+    vals, cols, ip, x = _case(lengths, 300000, 5, unsorted=True)
+    lay = XcsLayout(vals, cols, ip, 300000, panels_per_xcd=2)
+    _check_structure(lay, vals, cols, ip)
+    w = lay.windows.numpy().reshape(-1, 8)
+    assert (w[:, 1] < 0).any() == (win_slots == 8)  # one-row windows only when rows exceed 8
+    assert lay.n_windows > lay.n_tiles
+    y = _emulate(lay, x.numpy())
+    np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
+
+
+def test_xcs_item_run_cap(monkeypatch):
+    # an item stores its sums through at most the kernel's number of runs (one per combine
+    # window its rows reach); a layout that needs more is refused, and build_layout then falls
+    # back to row blocks
+    real = _abi.caps()
+    rng = np.random.default_rng(3)
+    lengths = rng.zipf(2.0, 20000).clip(max=200)
+    vals, cols, ip, x = _case(lengths, 60000, 3)
+    lay = XcsLayout(vals, cols, ip, 60000, panels_per_xcd=1)
+    most = int(lay.item_n_runs.max())
+    assert 2 <= most <= real["xcs_item_runs"]
+    monkeypatch.setattr(_spmv_layouts._abi, "caps", lambda: dict(real, xcs_item_runs=most - 1))
+    with pytest.raises(ValueError):
+        XcsLayout(vals, cols, ip, 60000, panels_per_xcd=1)
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-l2")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANELS_PER_XCD", 1)
+    assert _spmv_layouts.build_layout(vals, cols, ip, 60000).kind == "rowblock"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])

@@ -42,6 +42,9 @@ SIGNATURES = {
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p,
                             _i64, _i64, _p, _p, _p, _p, _i64, _i32, _p]),
+    "fsp_spmv_scratch_slots": (_i64, []),
+    "fsp_spmv_csr_static": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p,
+                                   _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p]),
     "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64, _p, _p,
                             _p, _i64, _i64, _p, _p, _p]),
     "fsp_spmv_panels": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i64,

@@ -158,12 +158,13 @@ __device__ __forceinline__ int xcd_logical_block(int i, int n) {
 // group_base[g] and are laid out [n][S].  It runs as a separate launch on the same stream: the
 // kernel boundary makes the first pass's partials visible on every XCD, so neither pass needs
 // a device-scope fence.  With reset != 0 every slot read is set back to 0, for first passes
-// that write only the slots of rows they hold.
+// that write only the slots of rows they hold.  Slots at or beyond partials_cap (the
+// workspace's size) are neither read nor written.
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
     const i32x4* __restrict__ groups, const int64_t* __restrict__ group_base,
-    const int* __restrict__ split_rows, A* __restrict__ partials, T* __restrict__ y,
-    const int* __restrict__ row_map, int reset) {
+    const int* __restrict__ split_rows, A* __restrict__ partials, int64_t partials_cap,
+    T* __restrict__ y, const int* __restrict__ row_map, int reset) {
   __shared__ A red[kWavesPerBlock];
   const i32x4 g = groups[blockIdx.x];
   const int first = g.x, S = g.y, n = g.z;
@@ -174,6 +175,7 @@ __global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
     // single thread.
     A acc = A(0);
     for (int j = threadIdx.x; j < n; j += kBlock) {
+      if (base + j >= partials_cap) break;  // a plan larger than the workspace
       A* p = &partials[base + j];
       acc += *p;
       if (reset) *p = A(0);
@@ -188,6 +190,7 @@ __global__ __launch_bounds__(kBlock) void split_row_combine_kernel(
   for (int s = threadIdx.x; s < S; s += kBlock) {
     A acc = A(0);
     for (int j = 0; j < n; ++j) {
+      if (base + (int64_t)j * S + s >= partials_cap) break;  // a plan larger than the workspace
       A* p = &partials[base + (int64_t)j * S + s];
       acc += *p;
       if (reset) *p = A(0);

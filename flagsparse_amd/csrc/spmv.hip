@@ -16,6 +16,10 @@
 //     registers, reduce across the workgroup; with nch > 1 the chunk sum goes to
 //     partials[part + k] and a second launch (split_row_combine_kernel) adds
 //     partials[part .. part+nch) in index order, so the result does not depend on timing.
+#include <atomic>
+#include <mutex>
+#include <string>
+
 #include "fsp_device.hpp"
 #include "fsp_internal.hpp"
 
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
     const T* __restrict__ vals, const int* __restrict__ cols, const P* __restrict__ rowptr,
     P nnz_total, const T* __restrict__ x, T* __restrict__ y, const int* __restrict__ row_map,
     const i32x4* __restrict__ desc, const int64_t* __restrict__ ranges, int n_desc, P chunk,
-    A* __restrict__ partials, int xcd_remap) {
+    A* __restrict__ partials, int64_t partials_cap, int xcd_remap) {
   __shared__ A s_prod[kStreamSlots];
   __shared__ P s_ptr[kStreamRows + 1];
   __shared__ A s_red[kWavesPerBlock];
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void spmv_rowblock_kernel(
   const A total = block_sum(acc, s_red);
   if (tid == 0) {
     if (nch == 1) y[row_map ? row_map[row] : row] = T(total);
-    else partials[part + k] = total;
+    else if ((int64_t)part + k < partials_cap) partials[part + k] = total;
   }
 }
 
@@ -198,8 +202,9 @@ template <typename T, typename A, typename P>
 int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64_t nnz,
                 const void* x, void* y, const int32_t* row_map, int64_t n_out,
                 const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
-                void* partials, const int32_t* groups, const int64_t* group_base,
-                const int32_t* split_rows, int64_t n_groups, int xcd_remap, hipStream_t st) {
+                void* partials, int64_t partials_cap, const int32_t* groups,
+                const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
+                int xcd_remap, hipStream_t st) {
   if (row_map) {
     int rc = fill_zero<T>(static_cast<T*>(y), n_out, st);
     if (rc) return rc;
@@ -212,12 +217,12 @@ int launch_spmv(const void* vals, const int32_t* cols, const void* rowptr, int64
                      0, st, static_cast<const T*>(vals), cols, static_cast<const P*>(rowptr),
                      (P)nnz, static_cast<const T*>(x), static_cast<T*>(y), row_map,
                      reinterpret_cast<const i32x4*>(desc), ranges, (int)n_desc, (P)chunk,
-                     static_cast<A*>(partials), xcd_remap);
+                     static_cast<A*>(partials), partials_cap, xcd_remap);
   int rc = check_hip(hipGetLastError(), "spmv_rowblock_kernel launch");
   if (rc || n_groups == 0) return rc;
   hipLaunchKernelGGL((split_row_combine_kernel<T, A>), dim3((unsigned)n_groups), dim3(kBlock), 0,
                      st, reinterpret_cast<const i32x4*>(groups), group_base, split_rows,
-                     static_cast<A*>(partials), static_cast<T*>(y), row_map, 0);
+                     static_cast<A*>(partials), partials_cap, static_cast<T*>(y), row_map, 0);
   return check_hip(hipGetLastError(), "split_row_combine_kernel launch");
 }
 
@@ -225,15 +230,16 @@ template <typename T, typename A>
 int dispatch_ptr(int rowptr_bits, const void* vals, const int32_t* cols, const void* rowptr,
                  int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
                  const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
-                 void* partials, const int32_t* groups, const int64_t* group_base,
-                 const int32_t* split_rows, int64_t n_groups, int xcd_remap, hipStream_t st) {
+                 void* partials, int64_t partials_cap, const int32_t* groups,
+                 const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
+                 int xcd_remap, hipStream_t st) {
   if (rowptr_bits == 32)
     return launch_spmv<T, A, int>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, ranges,
-                                  n_desc, chunk, partials, groups, group_base, split_rows,
-                                  n_groups, xcd_remap, st);
+                                  n_desc, chunk, partials, partials_cap, groups, group_base,
+                                  split_rows, n_groups, xcd_remap, st);
   return launch_spmv<T, A, int64_t>(vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, ranges,
-                                    n_desc, chunk, partials, groups, group_base, split_rows,
-                                    n_groups, xcd_remap, st);
+                                    n_desc, chunk, partials, partials_cap, groups, group_base,
+                                    split_rows, n_groups, xcd_remap, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -262,6 +268,84 @@ int fill_zero_f64(double* y, int64_t n, hipStream_t st) { return launch_fill<dou
 
 using namespace fsp;
 
+namespace {
+
+// The checks and launches of fsp_spmv_csr; partials holds partials_cap slots (INT64_MAX when
+// the caller sized it; the kernels then never compare).
+int spmv_csr_checked(const char* who, int dtype, int acc_f64, const void* vals,
+                     const int32_t* cols, const void* rowptr, int rowptr_bits, int64_t n_rows,
+                     int64_t nnz, const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                     const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                     void* partials, int64_t partials_cap, const int32_t* groups,
+                     const int64_t* group_base, const int32_t* split_rows, int64_t n_groups,
+                     int xcd_remap, void* stream) {
+  const std::string w(who);
+  if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, w + ": dtype");
+  if (rowptr_bits != 32 && rowptr_bits != 64)
+    return set_error(FSP_EINVAL, w + ": rowptr_bits must be 32 or 64");
+  if (n_rows < 0 || nnz < 0 || n_desc < 0 || n_out < 0 || n_groups < 0)
+    return set_error(FSP_EINVAL, w + ": negative size");
+  if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL || n_groups > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, w + ": more than 2^31-1 rows, descriptors or groups");
+  if (rowptr_bits == 32 && nnz > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, w + ": nnz exceeds int32 rowptr range");
+  if (chunk < 1 || chunk > kSpmvChunkCap)
+    return set_error(FSP_EINVAL, w + ": chunk outside [1, fsp_spmv_chunk_nnz_cap()]");
+  if (n_desc > 0 && (!rowptr || !y || !desc || !ranges))
+    return set_error(FSP_EINVAL, w + ": null pointer");
+  if (nnz > 0 && (!vals || !cols || !x)) return set_error(FSP_EINVAL, w + ": null pointer");
+  if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
+    return set_error(FSP_EINVAL, w + ": null split-row pointer");
+  if (!aligned16(vals) || !aligned16(cols) || !aligned16(desc) || !aligned16(groups))
+    return set_error(FSP_EINVAL, w + ": vals, cols, desc and groups must be 16-byte aligned");
+  if (row_map && !y) return set_error(FSP_EINVAL, w + ": null y");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define FSP_SPMV_ARGS rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out, desc, ranges, \
+                      n_desc, chunk, partials, partials_cap, groups, group_base, split_rows, \
+                      n_groups, xcd_remap, st
+  if (dtype == FSP_F32) {
+    if (acc_f64) return dispatch_ptr<float, double>(FSP_SPMV_ARGS);
+    return dispatch_ptr<float, float>(FSP_SPMV_ARGS);
+  }
+  return dispatch_ptr<double, double>(FSP_SPMV_ARGS);
+#undef FSP_SPMV_ARGS
+}
+
+// The partial-sum workspace of fsp_spmv_csr_static: one array per GPU for the life of the
+// process.  Its name is a host-side handle only; kernels get the device address that
+// hipGetSymbolAddress returns for the current device, resolved once per device.
+constexpr int64_t kSpmvScratchSlots = 1 << 17;  // 8-byte slots: 1 MiB per GPU
+__device__ __align__(256) double scratch[kSpmvScratchSlots];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  int rc = check_hip(hipGetDevice(&dev), "fsp_spmv_csr_static: hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr_static: device index beyond " +
+                                     std::to_string(kMaxDevices));
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                     "fsp_spmv_csr_static: hipGetSymbolAddress");
+      if (rc) return rc;
+      if (!p) return set_error(FSP_EHIP, "fsp_spmv_csr_static: null scratch address");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FSP_OK;
+}
+
+}  // namespace
+
 extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                             const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
                             const void* x, void* y, const int32_t* row_map, int64_t n_out,
@@ -269,38 +353,34 @@ extern "C" int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int3
                             int64_t chunk, void* partials, const int32_t* groups,
                             const int64_t* group_base, const int32_t* split_rows,
                             int64_t n_groups, int xcd_remap, void* stream) {
-  if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_csr: dtype");
-  if (rowptr_bits != 32 && rowptr_bits != 64)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: rowptr_bits must be 32 or 64");
-  if (n_rows < 0 || nnz < 0 || n_desc < 0 || n_out < 0 || n_groups < 0)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: negative size");
-  if (n_desc > 0x7fffffffLL || n_rows > 0x7fffffffLL || n_groups > 0x7fffffffLL)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: more than 2^31-1 rows, descriptors or groups");
-  if (rowptr_bits == 32 && nnz > 0x7fffffffLL)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: nnz exceeds int32 rowptr range");
-  if (chunk < 1 || chunk > kSpmvChunkCap)
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: chunk outside [1, fsp_spmv_chunk_nnz_cap()]");
-  if (n_desc > 0 && (!rowptr || !y || !desc || !ranges))
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
-  if (nnz > 0 && (!vals || !cols || !x)) return set_error(FSP_EINVAL, "fsp_spmv_csr: null pointer");
-  if (n_groups > 0 && (!groups || !group_base || !split_rows || !partials))
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: null split-row pointer");
-  if (!aligned16(vals) || !aligned16(cols) || !aligned16(desc) || !aligned16(groups))
-    return set_error(FSP_EINVAL, "fsp_spmv_csr: vals, cols, desc and groups must be 16-byte aligned");
-  if (row_map && !y) return set_error(FSP_EINVAL, "fsp_spmv_csr: null y");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == FSP_F32) {
-    if (acc_f64)
-      return dispatch_ptr<float, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                         desc, ranges, n_desc, chunk, partials, groups,
-                                         group_base, split_rows, n_groups, xcd_remap, st);
-    return dispatch_ptr<float, float>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, ranges, n_desc, chunk, partials, groups,
-                                      group_base, split_rows, n_groups, xcd_remap, st);
-  }
-  return dispatch_ptr<double, double>(rowptr_bits, vals, cols, rowptr, nnz, x, y, row_map, n_out,
-                                      desc, ranges, n_desc, chunk, partials, groups,
-                                      group_base, split_rows, n_groups, xcd_remap, st);
+  return spmv_csr_checked("fsp_spmv_csr", dtype, acc_f64, vals, cols, rowptr, rowptr_bits, n_rows,
+                          nnz, x, y, row_map, n_out, desc, ranges, n_desc, chunk, partials,
+                          INT64_MAX, groups, group_base, split_rows, n_groups, xcd_remap,
+                          stream);
+}
+
+extern "C" int64_t fsp_spmv_scratch_slots(void) { return kSpmvScratchSlots; }
+
+extern "C" int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals,
+                                   const int32_t* cols, const void* rowptr, int rowptr_bits,
+                                   int64_t n_rows, int64_t nnz, const void* x, void* y,
+                                   const int32_t* row_map, int64_t n_out, const int32_t* desc,
+                                   const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                                   int64_t n_parts, const int32_t* groups,
+                                   const int64_t* group_base, const int32_t* split_rows,
+                                   int64_t n_groups, int xcd_remap, void* stream) {
+  if (n_parts < 0 || n_parts > kSpmvScratchSlots)
+    return set_error(FSP_EINVAL, "fsp_spmv_csr_static: the plan needs " + std::to_string(n_parts) +
+                                     " partial slots; the static workspace holds " +
+                                     std::to_string(kSpmvScratchSlots) +
+                                     " (use fsp_spmv_csr with a workspace of that size)");
+  void* ptr = nullptr;
+  int rc = scratch_for_current_device(&ptr);
+  if (rc) return rc;
+  return spmv_csr_checked("fsp_spmv_csr_static", dtype, acc_f64, vals, cols, rowptr, rowptr_bits,
+                          n_rows, nnz, x, y, row_map, n_out, desc, ranges, n_desc, chunk, ptr,
+                          kSpmvScratchSlots, groups, group_base, split_rows, n_groups, xcd_remap,
+                          stream);
 }
 
 extern "C" int fsp_spmv_coo_atomic(int dtype, const void* vals, const int32_t* rows,

@@ -156,6 +156,29 @@ int fsp_spmv_csr(int dtype, int acc_f64, const void* vals, const int32_t* cols,
                  const int32_t* split_rows, int64_t n_groups, int xcd_remap, void* stream);
 
 /*
+ * fsp_spmv_csr without a caller workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It has
+ * no counterpart in the reference: it is fsp_spmv_csr with `partials` replaced by a static
+ * device array of fsp_spmv_scratch_slots() 8-byte slots (1 MiB) that every GPU holds for the
+ * life of the process.
+ *   n_parts   the plan's partial slots (fsp_plan_row_blocks' n_parts, or the device planner's
+ *             total); a plan needing more than fsp_spmv_scratch_slots() is rejected with
+ *             FSP_EINVAL (use fsp_spmv_csr with a workspace of that size instead)
+ * Nothing is allocated: the array's device address is resolved once per device
+ * (hipGetSymbolAddress) on the first call made with that device current.  Every call on one
+ * GPU shares the array: calls that overlap on one GPU (two streams, two threads) race and give
+ * wrong sums.  The array keeps the last call's contents; a call writes every slot it reads
+ * first, so nothing needs clearing.
+ */
+int64_t fsp_spmv_scratch_slots(void);
+int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals, const int32_t* cols,
+                        const void* rowptr, int rowptr_bits, int64_t n_rows, int64_t nnz,
+                        const void* x, void* y, const int32_t* row_map, int64_t n_out,
+                        const int32_t* desc, const int64_t* ranges, int64_t n_desc, int64_t chunk,
+                        int64_t n_parts, const int32_t* groups, const int64_t* group_base,
+                        const int32_t* split_rows, int64_t n_groups, int xcd_remap, void* stream);
+
+/*
  * y = A @ x in the XCD column-split layout (fp32/fp64 values, fp64 or native accumulation).
  *   vals, pidx   n_entries padded entries (16-byte aligned): pidx = (local row << col_bits) |
  *                (column - the panel's first column); every item starts on a multiple of 4

@@ -193,6 +193,13 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert spmv(chunk=10**9) == -1                # chunk beyond the compiled capacity
     assert spmv(n_groups=3) == -1                 # split-row groups without their arrays
     assert b"split-row" in L.fsp_last_error()
+    # the allocation-free variant refuses a plan larger than its static workspace before it
+    # resolves the workspace (no HIP call)
+    cap = L.fsp_spmv_scratch_slots()
+    assert cap == 1 << 17
+    assert L.fsp_spmv_csr_static(0, 0, None, None, None, 32, 0, 0, None, None, None, 0, None,
+                                 None, 0, 1, cap + 1, None, None, None, 0, 0, None) == -1
+    assert b"static workspace" in L.fsp_last_error()
     assert spmm(lanes=3) == -1                    # lanes_per_row not a power of two
     assert spmm(dtype=1, lanes=4, vec=4) == -1    # 4-wide vectors are fp32 only
     def xcs(col_bits=10, n_windows=0):

@@ -40,7 +40,8 @@ class RowBlockPlan:
 
     def workspace(self, width=1):
         """Partial-sum buffer for ``width`` values per row part, kept on the plan and reused by
-        every call.  Calls that share a plan must not run concurrently on different streams."""
+        every call; the layouts that launch with it order calls from different streams
+        (StreamOrder)."""
         ws = self._workspaces.get(int(width))
         if ws is None:
             n = max(self.n_parts, 1)
@@ -66,6 +67,42 @@ class RowBlockPlan:
             self._groups = (torch.from_numpy(groups).to(device), torch.from_numpy(base).to(device),
                             torch.from_numpy(rows).to(device))
         return self._groups
+
+
+class StreamOrder:
+    """Orders the calls that share one workspace (partial sums) across streams.
+
+    Calls made on one stream are ordered by the stream itself.  When a call comes from a
+    different stream than the previous one (or than the one the object was built on), the new
+    stream first waits for everything already queued on the previous stream - an event recorded
+    there at that moment - so two streams never interleave their use of the workspace.  The
+    reference allocates its workspace per call (spmm_csr.py:979-983) and has no such hazard;
+    here the steady state on one stream costs one comparison and allocates nothing.  The
+    tensors passed are also marked as used on the new stream, so the caching allocator does
+    not reuse their memory while that stream may still read them."""
+
+    __slots__ = ("_last",)
+
+    def __init__(self, device=None):
+        self._last = _abi.raw_stream(device) if device is not None and \
+            torch.device(device).type == "cuda" else None
+
+    def stream(self, device, tensors=()):
+        """The raw handle of torch's current stream on ``device``, ordered after the previous
+        user's work when it differs."""
+        s = _abi.raw_stream(device)
+        last = self._last
+        if last is not None and s != last:
+            old = torch.cuda.ExternalStream(last, device=device)
+            new = torch.cuda.ExternalStream(s, device=device)
+            ev = torch.cuda.Event()
+            ev.record(old)
+            new.wait_event(ev)
+            for t in tensors:
+                if t is not None and t.is_cuda:
+                    t.record_stream(new)
+        self._last = s
+        return s
 
 
 def rowptr_to_host(rowptr):

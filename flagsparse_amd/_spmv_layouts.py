@@ -35,7 +35,7 @@ import torch
 from . import _abi
 from . import _common
 from ._common import _INDEX_LIMIT_INT32, _aligned
-from ._plan import build_row_block_plan_windows
+from ._plan import StreamOrder, build_row_block_plan_windows
 
 XCD_COUNT = 8
 L2_BYTES = 4 << 20
@@ -120,6 +120,7 @@ class RowBlockLayout:
                 self.band_offset = off
         self._args = {}
         self._keep = None
+        self._order = StreamOrder(self.data.device)
 
     def kernel_name(self):
         return "spmv_rowblock_kernel"
@@ -136,7 +137,8 @@ class RowBlockLayout:
         if args is None:
             plan = self.plan
             groups, group_base, split_rows = plan.split_groups()
-            keep = (plan.workspace(), groups, group_base, split_rows)
+            keep = (plan.workspace(), groups, group_base, split_rows, plan.desc, plan.ranges,
+                    self.data, self.cols, self.rowptr)
             args = [_abi.dtype_code(self.data.dtype), int(acc_f64), self.data.data_ptr(),
                     self.cols.data_ptr(), self.rowptr.data_ptr(), self.rowptr_bits,
                     self.n_rows, self.nnz, None, None, None, 0, plan.desc.data_ptr(),
@@ -152,7 +154,7 @@ class RowBlockLayout:
         a[10] = None if row_map is None else row_map.data_ptr()
         a[11] = n_out
         a[21] = XCD_REMAP_ROWBLOCK
-        a[22] = _abi.raw_stream(y.device)
+        a[22] = self._order.stream(y.device, self._keep)
         _abi.check(_abi.lib().fsp_spmv_csr(*a), "fsp_spmv_csr")
         return y
 
@@ -397,6 +399,7 @@ class XcsLayout:
         self.n_items = n_items
         self.max_items_per_panel = q
         self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+        self._order = StreamOrder(dev)
 
     def _build_combine_windows(self, pair_item, pair_row, count, n_items, caps):
         """Where every partial sum is stored, and the tables of the second launch
@@ -525,7 +528,9 @@ class XcsLayout:
         a[6], a[7] = x.data_ptr(), y.data_ptr()
         a[8] = None if row_map is None else row_map.data_ptr()
         a[9] = n_out
-        a[19] = _abi.raw_stream(y.device)
+        a[19] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.items,
+                                              self.item_runs, self.windows, self.dest,
+                                              self.row_start))
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 
@@ -634,6 +639,7 @@ class PanelLayout:
         self.n_panels = n_panels
         self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
         self._args = {}
+        self._order = StreamOrder(dev)
 
     def kernel_name(self):
         return "spmv_panel_kernel"
@@ -657,7 +663,9 @@ class PanelLayout:
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
         a[9] = None if row_map is None else row_map.data_ptr()
-        a[20] = _abi.raw_stream(y.device)
+        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.jobs,
+                                              self.job_panel, self.chunk_slot, self.rows,
+                                              self.row_ptr, self.slots))
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 

@@ -27,7 +27,7 @@ from ._common import (
     _tolerance_for_dtype,
 )
 from ._index_stats import index_stats_device
-from ._plan import build_row_block_plan_device
+from ._plan import StreamOrder, build_row_block_plan_device
 from .synthetic import build_random_csr, build_random_dense
 
 SUPPORTED_SPMM_VALUE_DTYPES = SUPPORTED_VALUE_DTYPES
@@ -289,7 +289,7 @@ class _SpmmKernelCsr:
     """Kernel-facing CSR arrays (aligned, int32 offsets when they fit) and plans per G."""
 
     __slots__ = ("data", "cols", "rowptr", "rowptr_bits", "nnz", "n_rows", "_plans", "_args",
-                 "_keep", "window_blocks")
+                 "_keep", "window_blocks", "_order")
 
     def __init__(self, data, cols, indptr64, window_blocks=None):
         # window_blocks: plan window in blocks' rows (SPMM_PLAN_WINDOW_BLOCKS when None); the
@@ -305,7 +305,8 @@ class _SpmmKernelCsr:
             self.rowptr, self.rowptr_bits = indptr64.to(torch.int64).contiguous(), 64
         self._plans = {}
         self._args = {}
-        self._keep = []
+        self._keep = [self.data, self.cols, self.rowptr]  # what a launch reads or writes
+        self._order = StreamOrder(self.data.device)
 
     def kernel_name(self):
         return "spmm_rowblock_kernel"
@@ -372,11 +373,11 @@ def _run_spmm(kc, B, C, acc_f64, tile_cols=None):
                 p(plan.desc), plan.n_desc, plan.chunk, lanes, vec, p(partials), p(groups),
                 p(group_base), p(split_rows), int(groups.shape[0]), 0, None]
         kc._args[key] = args
-        kc._keep.append(partials)
+        kc._keep.extend((partials, plan.desc, groups, group_base, split_rows))
     a = list(args)
     a[8], a[9], a[11], a[12] = B.data_ptr(), B.stride(0), C.data_ptr(), C.stride(0)
     a[23] = XCD_REMAP
-    a[24] = _abi.raw_stream(C.device)
+    a[24] = kc._order.stream(C.device, kc._keep)
     _abi.check(_abi.lib().fsp_spmm_csr(*a), "fsp_spmm_csr")
     return C
 

@@ -1,33 +1,50 @@
 """Benchmark of the flagsparse_amd hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2] [--no-targets]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3] [--no-targets]
 
 Prints ONE JSON line.  A step is one call of the public API over the workload's matrix with
 the inputs already resident in HBM and the prepare step outside the timed region, as the
 reference's harness does (sparse_operations/benchmarks.py:249-262).  The default workload is
-BASELINE.json configs[1] (CSR SpMV, float64, 5-point Poisson on a 2048 x 2048 grid, the
-reference's default use_opt=False path); --workload selects the others.
+cfg3 (CSR SpMV, float32, the 8M-row power-law matrix, the
+reference's default use_opt=False path), the configuration north_star's SpMV target is quoted
+on; --workload selects the others, and the two probe workloads.
 
 value        algorithmic bytes per step / time per step (HIP events around the K steps); the
              untimed warm-up before them runs W steps at a time until at least 50 ms have
              passed (``warmup_steps_run`` reports how many)
-roofline     the same bytes / the dominant kernel's average duration, timed with HIP events
-             around K back-to-back launches on the stream the kernel runs on (the median of 5
-             such trials; all five in ``kernel_ms_trials``), against the 8 TB/s HBM3E peak.
-             ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch from the committed rocprofv3
-             PMC summary (profiles/<kernel tag>_traffic.txt), or null.
+roofline     the same bytes / the path's kernel time (all the kernels of one launch), timed
+             with HIP events around K back-to-back launches on the stream the kernels run on
+             (the median of 5 such trials; all five in ``kernel_ms_trials``), against the
+             8 TB/s HBM3E peak.  From the committed rocprofv3 summaries
+             (profiles/<tag>_traffic.txt): ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch,
+             ``l2_hit_rate`` and ``occupancy_percent`` per kernel.  ``bytes_gather_inclusive``
+             counts x (SpMV) or B (SpMM) once per entry instead of once, and
+             ``frac_gather_inclusive`` is that count over the same time against the peak.
+             ``gather_bound`` (cfg3, cfg5): the probe kernels timed in the same run on the
+             workload's own gather count and pattern - the rate the gathers alone reach
 cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
              (a bounded row sample for SpMM), reported only, never a target
 cpu_reference_path
              the reference's own CPU path - scipy.sparse (one core) and torch's CPU sparse
              product (torch's thread count) - on the same matrix, a few seconds each, with
              the same byte and flop counts; reported only
-config       also ``prepare_ms`` (the prepare call, synchronised), ``first_call_ms`` (the first
+config       also ``lib_load_ms`` (loading the HIP library, once per process), ``prepare_ms``
+             (the prepare call and the first layout build, synchronised; ``prepare_call_ms``
+             and ``layout_build_ms`` separately), ``plan.layout_bytes`` (device memory the
+             prepared layout holds beyond the caller's arrays), ``first_call_ms`` (the first
              step after prepare, cold) and ``inputs_sha256`` (SHA-256 of every generated input
              array, so that runs on different machines provably use the same data)
-targets      north_star's two targets measured in the same run (kernel time only): CSR SpMV
-             fp32 on the 8M power-law matrix (>= 70% of HBM peak) and CSR SpMM fp32 N=64
-             (>= 60%); omitted with --no-targets
+targets      north_star's two targets measured in the same run, each with the same roofline
+             block: CSR SpMV fp32 on the 8M power-law matrix (>= 70% of HBM peak; the headline
+             itself when the workload is cfg3) and CSR SpMM fp32 N=64 (>= 60%), the latter with
+             its own bounded CPU baseline; omitted with --no-targets
+
+Probe workloads (measurement only; the access patterns the kernels are bound by, alone):
+  probe-gather  random 4-byte gathers (fsp_probe_gather) from an fp32 x of --probe-bytes
+                (default 33.5 MB, cfg3's x), 16 per thread in flight; --probe-xcd restricts
+                the gathers of XCD k to the k-th eighth of x (the XCS layout's placement)
+  probe-rows    random 256-byte row gathers (fsp_probe_rows) from an fp32 B[rows, 64] of
+                --probe-bytes (default 268 MB, cfg5 N=64's B): 16.8M gathers, cfg5's random half
 
 Algorithmic bytes count each array once at the width the kernel reads:
   SpMV  nnz*(v + i) + (n_rows + 1)*p + n_cols*v + n_rows*v
@@ -63,6 +80,8 @@ WORKLOADS = {
     "sddmm": "CSR SDDMM on cfg5's pattern (1M x 1M, 32 nnz/row), x [1M, K] and y [1M, K] "
              "row-major ~U(-1,1), alpha 1, beta 0, fp32 accumulation (the reference's baseline)",
     "copy": "plain device copy of 1 GiB (PMC calibration kernel)",
+    "probe-gather": "random 4-byte gathers from an fp32 x (fsp_probe_gather), 16 per thread",
+    "probe-rows": "random 256-byte row gathers from an fp32 B[rows, 64] (fsp_probe_rows)",
 }
 
 
@@ -71,7 +90,7 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="cfg2", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="cfg3", choices=sorted(WORKLOADS))
     ap.add_argument("--dtype", default=None, choices=("f32", "f64"),
                     help="value type for cfg5 / coo5 / sddmm (default f32)")
     ap.add_argument("--n", type=int, default=64,
@@ -83,17 +102,32 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-targets", action="store_true",
                     help="skip the north_star target measurements")
+    ap.add_argument("--probe-bytes", type=int, default=None,
+                    help="probe workloads: bytes of x (probe-gather) or B (probe-rows)")
+    ap.add_argument("--probe-n", type=int, default=None,
+                    help="probe workloads: number of gathers")
+    ap.add_argument("--probe-xcd", action="store_true",
+                    help="probe-gather: XCD k gathers only from the k-th eighth of x")
     return ap.parse_args()
 
 
-def _traffic_from_profile(tag):
-    """HBM bytes per launch from profiles/<tag>_traffic.txt ("traffic_bytes_per_launch: N")."""
+def _profile(tag):
+    """What the committed profiles/<tag>_traffic.txt records: ``traffic_bytes_per_launch`` and
+    the per-kernel ``l2_hit_rate[...]`` / ``occupancy_percent[...]`` lines ({} if absent)."""
     path = os.path.join(ROOT, "profiles", f"{tag}_traffic.txt")
     if not os.path.exists(path):
-        return None
+        return {}
     with open(path) as fh:
-        m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", fh.read(), re.M)
-    return float(m.group(1)) if m else None
+        text = fh.read()
+    out = {}
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, re.M)
+    if m:
+        out["traffic"] = float(m.group(1))
+    for key in ("l2_hit_rate", "occupancy_percent"):
+        vals = {k: float(v) for k, v in re.findall(rf"^{key}\[([^\]]+)\]:\s*([0-9.]+)", text, re.M)}
+        if vals:
+            out[key] = vals
+    return out
 
 
 def _event_loop(fn, count, torch):
@@ -208,25 +242,45 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         data, idx, ptr, x, shape = synthetic.csr_powerlaw(device=dev)
     from flagsparse_amd import spmv_csr as mod
 
-    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmv_csr(data, idx, ptr, shape), torch)
+    prepared, prep_call_ms = _timed_prepare(lambda: fs.prepare_spmv_csr(data, idx, ptr, shape),
+                                            torch)
     use_opt = bool(opt and prepared.supports_opt)
     # the layout and launch arguments are built on first use; count them as prepare work
-    _, kernel_ms0 = _timed_prepare(lambda: prepared._kernel(use_opt), torch)
-    prep_ms = round(prep_ms + kernel_ms0, 3)
+    _, layout_ms = _timed_prepare(lambda: prepared._kernel(use_opt), torch)
     y = torch.empty(shape[0], dtype=data.dtype, device=dev)
     kc = prepared._kernel(use_opt)
     v = data.element_size()
     p_k = prepared.kernel_indptr.element_size()
     nnz = int(data.numel())
     nbytes = nnz * (v + 4) + (shape[0] + 1) * p_k + shape[1] * v + shape[0] * v
+    from flagsparse_amd._spmv_layouts import tensor_bytes
+
+    caller = (data, idx, ptr)
+    narrowed = [t for t in (prepared.kernel_indices, prepared.kernel_indptr)
+                if all(t.untyped_storage().data_ptr() != c.untyped_storage().data_ptr()
+                       for c in caller)]
+    plan = dict(kc.describe(), layout_bytes=int(kc.held_bytes(caller)),
+                narrowed_index_bytes=int(tensor_bytes(*narrowed)))
+    # the first prepare of a process also pays one-time set-up (the first use of each torch
+    # operation it runs); a second prepare of the same matrix shows the steady cost
+    _, prep_again_ms = _timed_prepare(
+        lambda: fs.prepare_spmv_csr(data, idx, ptr, shape)._kernel(use_opt), torch)
+    torch.cuda.empty_cache()
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz,
             "index_supplied": str(idx.dtype).replace("torch.", ""), "index_kernel": "int32",
             "rowptr_kernel": f"int{8 * p_k}",
             "path": "use_opt=True" if use_opt else "default (use_opt=False)",
             "bytes_as_supplied": nnz * (v + idx.element_size()) +
             (shape[0] + 1) * ptr.element_size() + shape[1] * v + shape[0] * v,
-            "plan": kc.describe(), "prepare_ms": prep_ms,
+            "plan": plan, "prepare_ms": round(prep_call_ms + layout_ms, 3),
+            "prepare_call_ms": prep_call_ms, "layout_build_ms": layout_ms,
+            "prepare_ms_repeat": prep_again_ms,
             "inputs": {"data": data, "indices": idx, "indptr": ptr, "x": x}}
+    acc_f64 = (not use_opt) or data.dtype == torch.float64
+    parts = None
+    if kc.kind == "xcs-hybrid":  # the two parts of the launch, each timed alone
+        parts = {"xcs_part": lambda: kc.short.launch(x, y, acc_f64),
+                 "panel_part": lambda: kc.long.launch(x, y, acc_f64)}
 
     def cpu(seconds):
         from oracle import oracle
@@ -238,9 +292,21 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
                           f"the same matrix in {secs:.1f} s",
                 "gflops": round(2 * nnz * passes / secs / 1e9, 3)}
 
+    gather_bound = None
+    if name == "cfg3" and kc.kind == "xcs-hybrid":
+        # the XCS part's gathers: its entries, from per-XCD panels of x (P panels, P / 8 per
+        # XCD in turn: an x of 8 / P of the whole, each XCD gathering from its eighth)
+        n_g = kc.short.nnz // 4 * 4
+        x_len = max(8, shape[1] * 8 // kc.short.n_panels)
+        gather_bound = lambda: _gather_bound(x_len, n_g, True, dev, torch,  # noqa: E731
+                                             f"{n_g} random 4-byte gathers (the XCS part's "
+                                             f"entries), XCD k from the k-th eighth of an x of "
+                                             f"{x_len * 4} bytes (one of the XCS panels per XCD)")
     return {
         "step": lambda: fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y),
         "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
+        "parts": parts, "gather_bound": gather_bound,
+        "bytes_gather_inclusive": nnz * (v + 4 + v) + (shape[0] + 1) * p_k + shape[0] * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
         "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), x, shape,
                                                        seconds, nbytes, 2 * nnz, torch),
@@ -253,17 +319,22 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
     from flagsparse_amd import spmv_coo as mod
 
     data, row, col, x, shape = synthetic.coo_uniform(device=dev)
-    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmv_coo(data, row, col, shape), torch)
+    prepared, prep_call_ms = _timed_prepare(
+        lambda: fs.prepare_spmv_coo(data, row, col, shape), torch)
     y = torch.empty(shape[0], dtype=data.dtype, device=dev)
     v = data.element_size()
     nnz = int(data.numel())
     runs = prepared.n_segs
+    layout, layout_ms = _timed_prepare(prepared._run_layout, torch)  # built on first use
     nbytes = nnz * (v + 4) + (runs + 1) * 4 + shape[1] * v + shape[0] * v
-    if prepared._run_rows is not None:
+    if prepared._run_rows is not None:  # the run -> row map, and y zeroed first
         nbytes += runs * 4 + shape[0] * v
+    plan = dict(prepared._kernel_plan_description(),
+                layout_bytes=int(layout.held_bytes((data, row, col))))
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "row_runs": runs,
             "bytes_literal_row_col_val": nnz * (v + 8) + shape[1] * v + shape[0] * v,
-            "plan": prepared._kernel_plan_description(), "prepare_ms": prep_ms,
+            "plan": plan, "prepare_ms": round(prep_call_ms + layout_ms, 3),
+            "prepare_call_ms": prep_call_ms, "layout_build_ms": layout_ms,
             "inputs": {"data": data, "row": row, "col": col, "x": x}}
 
     def cpu(seconds):
@@ -278,6 +349,7 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
     return {
         "step": lambda: fs.flagsparse_spmv_coo(x=x, prepared=prepared, out=y),
         "launch": lambda: mod._run_spmv_coo(prepared, x, y, 256),
+        "bytes_gather_inclusive": nbytes - shape[1] * v + nnz * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu, "dtype": "f32",
         "cpu_lib": lambda seconds: _cpu_reference_path("coo", (row, col, data), x, shape,
                                                        seconds, nbytes, 2 * nnz, torch),
@@ -291,19 +363,33 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
     vdt = torch.float64 if dtype_name == "f64" else torch.float32
     data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
     B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
-    prepared, prep_ms = _timed_prepare(lambda: fs.prepare_spmm_csr_opt(data, idx, ptr, shape), torch)
+    prepared, prep_call_ms = _timed_prepare(
+        lambda: fs.prepare_spmm_csr_opt(data, idx, ptr, shape), torch)
     C = torch.empty((shape[0], N), dtype=vdt, device=dev)
-    kc, kernel_ms0 = _timed_prepare(prepared._kernel_csr, torch)
-    prep_ms = round(prep_ms + kernel_ms0, 3)
+    kc, layout_ms = _timed_prepare(prepared._kernel_csr, torch)
     v = data.element_size()
     nnz = int(data.numel())
     p_k = 4 if kc.rowptr_bits == 32 else 8
     nbytes = nnz * (v + 4) + (shape[0] + 1) * p_k + shape[1] * N * v + shape[0] * N * v
+    launch = lambda: mod._run_spmm(kc, B, C, acc_f64=vdt == torch.float64)  # noqa: E731
+    launch()  # the plan for this N and its workspace are built on the first launch
+    torch.cuda.synchronize()
+    from flagsparse_amd._spmv_layouts import tensor_bytes
+
+    theirs = {t.untyped_storage().data_ptr() for t in (data, idx, ptr)}
+    held = tensor_bytes(*[t for t in kc._keep if t.untyped_storage().data_ptr() not in theirs])
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "N": N,
             "path": "flagsparse_spmm_csr_opt (native accumulation)",
-            "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * p_k +
-            shape[0] * N * v, "prepare_ms": prep_ms,
+            "plan": dict(kc.describe(), layout_bytes=int(held)),
+            "prepare_ms": round(prep_call_ms + layout_ms, 3), "prepare_call_ms": prep_call_ms,
+            "layout_build_ms": layout_ms,
             "inputs": {"data": data, "indices": idx, "indptr": ptr, "B": B}}
+    gather_bound = None
+    if N == 64 and vdt == torch.float32:
+        n_rand = nnz // 2  # cfg5: 16 of the 32 entries of every row at uniform random columns
+        gather_bound = lambda: _rows_bound(shape[1], n_rand, dev, torch,  # noqa: E731
+                                           f"{n_rand} random 256-byte row gathers (cfg5's "
+                                           f"random half) from a B of {shape[1] * 256} bytes")
 
     def cpu(seconds):
         from oracle import oracle
@@ -320,7 +406,9 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
 
     return {
         "step": lambda: fs.flagsparse_spmm_csr_opt(B=B, prepared=prepared, out=C),
-        "launch": lambda: mod._run_spmm(kc, B, C, acc_f64=vdt == torch.float64),
+        "launch": launch, "gather_bound": gather_bound,
+        "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * p_k +
+        shape[0] * N * v,
         "nbytes": nbytes, "flops": 2 * nnz * N, "info": info, "cpu": cpu,
         "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), B, shape,
                                                        seconds, nbytes, 2 * nnz * N, torch),
@@ -396,8 +484,7 @@ def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
     # per entry: column, row id, result; x and y rows once each
     nbytes = nnz * (4 + 4 + v) + shape[0] * K * v + shape[1] * K * v
     info = {"n_rows": shape[0], "n_cols": shape[1], "nnz": nnz, "K": K,
-            "path": "flagsparse_sddmm_csr (baseline variant)",
-            "bytes_gather_inclusive": nnz * (4 + 4 + v + 2 * K * v), "prepare_ms": prep_ms,
+            "path": "flagsparse_sddmm_csr (baseline variant)", "prepare_ms": prep_ms,
             "inputs": {"indices": idx, "indptr": ptr, "x": x, "y": y}}
 
     def cpu(seconds):
@@ -424,10 +511,96 @@ def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
     return {
         "step": lambda: fs.flagsparse_sddmm_csr(x=x, y=y, prepared=prepared, out=out),
         "launch": lambda: mod._launch_sddmm(prepared, x, y, None, 1.0, 0.0, out, False),
+        "bytes_gather_inclusive": nnz * (4 + 4 + v + 2 * K * v),
         "nbytes": nbytes, "flops": 2 * nnz * K, "info": info, "cpu": cpu,
         "dtype": dtype_name, "kernel": "sddmm_csr_kernel",
         "tag": f"sddmm_csr_kernel_{dtype_name}_k{K}",
     }
+
+
+def _probe_indices(n, hi, xcd, dev, torch, per_block):
+    """n int32 indices uniform in [0, hi) (seed fixed); with xcd, the indices of workgroup b
+    (per_block consecutive ones) lie in the (b mod 8)-th eighth of [0, hi) - workgroup b runs
+    on XCD b mod 8."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(20260)
+    if not xcd:
+        return torch.randint(0, hi, (n,), generator=g, device=dev, dtype=torch.int32)
+    w = max(1, hi // 8)
+    blk = torch.arange(n, device=dev, dtype=torch.int64) // per_block
+    r = torch.randint(0, w, (n,), generator=g, device=dev, dtype=torch.int64)
+    return ((blk % 8) * w + r).to(torch.int32)
+
+
+def _probe_gather_call(x_len, n, xcd, dev, torch):
+    from flagsparse_amd import _abi
+
+    L = _abi.lib()
+    x = torch.ones(x_len, dtype=torch.float32, device=dev)
+    idx = _probe_indices(n, x_len, xcd, dev, torch, 256 * 16)
+    out = torch.empty(max(1, int(L.fsp_probe_gather_blocks(n))), dtype=torch.float32, device=dev)
+    args = (x.data_ptr(), x_len, idx.data_ptr(), n, out.data_ptr())
+
+    def call():
+        _abi.check(L.fsp_probe_gather(*args, _abi.raw_stream(dev)), "fsp_probe_gather")
+
+    call.keep = (x, idx, out)
+    return call
+
+
+def _probe_rows_call(n_rows, n, dev, torch):
+    from flagsparse_amd import _abi
+
+    L = _abi.lib()
+    B = torch.ones((n_rows, 64), dtype=torch.float32, device=dev)
+    rows = _probe_indices(n, n_rows, False, dev, torch, 64)
+    out = torch.empty(max(1, int(L.fsp_probe_rows_blocks(n))), dtype=torch.float32, device=dev)
+    args = (B.data_ptr(), n_rows, 64, rows.data_ptr(), n, out.data_ptr())
+
+    def call():
+        _abi.check(L.fsp_probe_rows(*args, _abi.raw_stream(dev)), "fsp_probe_rows")
+
+    call.keep = (B, rows, out)
+    return call
+
+
+def _bound(call, n, what, torch):
+    """The probe's time (median of 5 runs of 20 back-to-back launches) as a gather bound."""
+    for _ in range(3):
+        call()
+    ms = sorted(_event_loop(call, 20, torch) for _ in range(5))[2]
+    return {"pattern": what, "gathers": int(n), "ms": round(ms, 6),
+            "G_per_s": round(n / (ms * 1e-3) / 1e9, 2)}
+
+
+def _gather_bound(x_len, n, xcd, dev, torch, what):
+    return _bound(_probe_gather_call(x_len, n, xcd, dev, torch), n, what, torch)
+
+
+def _rows_bound(n_rows, n, dev, torch, what):
+    return _bound(_probe_rows_call(n_rows, n, dev, torch), n, what, torch)
+
+
+def _probe_workload(name, args, dev, torch):
+    if name == "probe-gather":
+        x_len = (args.probe_bytes or 8 * (1 << 20) * 4) // 4
+        n = (args.probe_n or 100 * (1 << 20)) // 4 * 4
+        call = _probe_gather_call(x_len, n, args.probe_xcd, dev, torch)
+        nbytes = n * 8  # an index and a gathered value per gather
+        info = {"x_bytes": x_len * 4, "gathers": n, "xcd_panels": bool(args.probe_xcd),
+                "bytes_counted": "4-byte index + 4-byte value per gather"}
+        tag = f"probe_gather_{x_len * 4}{'_xcd' if args.probe_xcd else ''}"
+    else:
+        n_rows = (args.probe_bytes or (1 << 20) * 256) // 256
+        n = args.probe_n or 16 * (1 << 20)
+        call = _probe_rows_call(n_rows, n, dev, torch)
+        nbytes = n * (256 + 4)
+        info = {"b_bytes": n_rows * 256, "row_gathers": n,
+                "bytes_counted": "256-byte row + 4-byte index per gather"}
+        tag = f"probe_rows_{n_rows * 256}"
+    return {"step": call, "launch": call, "nbytes": nbytes, "flops": 0, "info": info,
+            "cpu": None, "dtype": "f32", "kernel": f"{name.replace('-', '_')}_kernel",
+            "tag": tag, "gathers": n}
 
 
 def _copy_workload(dev, torch):
@@ -457,6 +630,8 @@ def _build(name, args, dev, torch):
         return _spmm_coo_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
     if name == "sddmm":
         return _sddmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
+    if name.startswith("probe-"):
+        return _probe_workload(name, args, dev, torch)
     return _copy_workload(dev, torch)
 
 
@@ -501,22 +676,67 @@ def _measure(w, steps, warmup, torch, trials=KERNEL_TRIALS):
     return ms_step, wall_ms, ms_kernel, runs, first_ms, warm_run
 
 
-def _target(name, args, dev, torch, steps):
+def _roofline(w, ms_kernel, kernel_runs, torch):
+    """The roofline block of a workload measured at ms_kernel per launch (see the module
+    docstring), with what the committed profile records and the gather bound measured now."""
+    nbytes = w["nbytes"]
+    achieved = nbytes / (ms_kernel * 1e-3) / 1e9
+    prof = _profile(w["tag"])
+    out = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+           "traffic": prof.get("traffic"), "kernel": w["kernel"],
+           "kernel_ms": round(ms_kernel, 6),
+           "kernel_ms_trials": [round(t, 6) for t in kernel_runs],
+           "profile_tag": w["tag"]}
+    if prof.get("traffic"):
+        out["traffic_over_algorithmic"] = round(prof["traffic"] / nbytes, 3)
+    for key in ("l2_hit_rate", "occupancy_percent"):
+        if key in prof:
+            out[key] = prof[key]
+    gi = w.get("bytes_gather_inclusive")
+    if gi:
+        out["bytes_gather_inclusive"] = int(gi)
+        out["frac_gather_inclusive"] = round(gi / (ms_kernel * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if w.get("parts"):
+        out["parts_ms"] = {k: round(sorted(_event_loop(fn, 20, torch) for _ in range(3))[1], 6)
+                           for k, fn in w["parts"].items()}
+    if w.get("gather_bound"):
+        gb = w["gather_bound"]()
+        gb["kernel_ms_over_bound"] = round(ms_kernel / gb["ms"], 3)
+        out["gather_bound"] = gb
+    return out
+
+
+def _target(name, args, dev, torch, steps, cpu_seconds):
     class A:
         pass
 
     a = A()
     a.opt, a.dtype, a.n = False, "f32", 64
     w = _build(name, a, dev, torch)
-    _, _, ms_kernel, _, _, _ = _measure(w, steps, 5, torch, trials=1)
-    achieved = w["nbytes"] / (ms_kernel * 1e-3) / 1e9
-    out = {"workload": name if name != "cfg5" else "cfg5 (f32, N=64)", "kernel": w["kernel"],
-           "kernel_ms": round(ms_kernel, 6), "achieved_GBs": round(achieved, 2),
-           "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_launch": int(w["nbytes"]),
-           "gflops": round(w["flops"] / (ms_kernel * 1e-3) / 1e9, 2)}
+    _, _, ms_kernel, runs, _, _ = _measure(w, steps, 5, torch, trials=3)
+    out = {"workload": name if name != "cfg5" else "cfg5 (f32, N=64)",
+           "bytes_per_launch": int(w["nbytes"]),
+           "gflops": round(w["flops"] / (ms_kernel * 1e-3) / 1e9, 2),
+           "roofline": _roofline(w, ms_kernel, runs, torch),
+           "prepare_ms": w["info"].get("prepare_ms"), "plan": w["info"].get("plan")}
+    if cpu_seconds > 0 and w["cpu"] is not None:
+        out["cpu_baseline"] = w["cpu"](cpu_seconds)
+        if w.get("cpu_lib") is not None:
+            out["cpu_reference_path"] = w["cpu_lib"](cpu_seconds / 2)
     del w
     torch.cuda.empty_cache()
     return out
+
+
+def _lib_load_ms(torch):
+    """Loading the HIP library and reading its capacities (once per process)."""
+    from flagsparse_amd import _abi
+
+    t0 = time.perf_counter()
+    _abi.lib()
+    _abi.caps()
+    return round((time.perf_counter() - t0) * 1000.0, 3)
 
 
 def main():
@@ -531,12 +751,13 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    lib_ms = _lib_load_ms(torch)
     w = _build(args.workload, args, dev, torch)
     ms_step, wall_ms, ms_kernel, kernel_runs, first_ms, warm_run = _measure(
         w, args.steps, args.warmup, torch)
     nbytes, flops = w["nbytes"], w["flops"]
     value = nbytes / (ms_step * 1e-3) / 1e9
-    achieved = nbytes / (ms_kernel * 1e-3) / 1e9
+    roofline = _roofline(w, ms_kernel, kernel_runs, torch)
     cpu = cpu_lib = None
     if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
         cpu = w["cpu"](args.cpu_seconds)
@@ -548,7 +769,7 @@ def main():
         workload = f"{args.workload} ({w['dtype']}, N={args.n}): {WORKLOADS[args.workload]}"
     if args.workload == "sddmm":
         workload = f"sddmm ({w['dtype']}, K={args.n}): {WORKLOADS['sddmm']}"
-    info, dtype, kernel, tag = dict(w["info"]), w["dtype"], w["kernel"], w["tag"]
+    info, dtype = dict(w["info"]), w["dtype"]
     inputs = info.pop("inputs", None)
     if inputs:
         from flagsparse_amd import synthetic
@@ -556,15 +777,26 @@ def main():
         info["inputs_sha256"] = _digests(inputs, synthetic)
     del inputs
     info["first_call_ms"] = round(first_ms, 6)
+    info["lib_load_ms"] = lib_ms
+    metric, unit = METRIC, "GB/s"
+    if args.workload.startswith("probe-"):
+        metric, unit = "random gather rate (measurement probe)", "G gathers/s"
+        value = w["gathers"] / (ms_step * 1e-3) / 1e9
     del w
     torch.cuda.empty_cache()
     targets = None
     if not args.no_targets:
-        targets = [_target("cfg3", args, dev, torch, 20), _target("cfg5", args, dev, torch, 20)]
+        cpu_s = 0.0 if args.no_cpu else args.cpu_seconds / 2
+        targets = []
+        if args.workload == "cfg3" and not args.opt:
+            targets.append({"workload": "cfg3", "roofline": "the headline line"})
+        else:
+            targets.append(_target("cfg3", args, dev, torch, 20, cpu_s))
+        targets.append(_target("cfg5", args, dev, torch, 20, cpu_s))
     out = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(value, 2),
-        "unit": "GB/s",
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -579,12 +811,7 @@ def main():
                        flops_per_step=int(flops),
                        gflops=round(flops / (ms_step * 1e-3) / 1e9, 2),
                        host_wall_ms_per_step=round(wall_ms, 6)),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _traffic_from_profile(tag), "kernel": kernel,
-                     "kernel_ms": round(ms_kernel, 6),
-                     "kernel_ms_trials": [round(t, 6) for t in kernel_runs],
-                     "profile_tag": tag},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "cpu_reference_path": cpu_lib,
         "targets": targets,

@@ -62,6 +62,10 @@ SIGNATURES = {
     "fsp_mtx_read": (_i32, [ctypes.c_char_p, _p, _p, _p, _p, _i64]),
     "fsp_sddmm_csr": (_i32, [_i32, _i32, _i32, _p, _p, _p, _i32, _i64, _p, _i64, _p, _i64, _i64,
                              _p, _f64, _f64, _p, _p, _p, _i64, _i32, _i32, _p]),
+    "fsp_probe_gather_blocks": (_i64, [_i64]),
+    "fsp_probe_gather": (_i32, [_p, _i64, _p, _i64, _p, _p]),
+    "fsp_probe_rows_blocks": (_i64, [_i64]),
+    "fsp_probe_rows": (_i32, [_p, _i64, _i64, _p, _i64, _p, _p]),
 }
 
 

@@ -20,7 +20,7 @@ LIB_NAME = "libflagsparse_hip.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
 SOURCES = ("abi.cpp", "mtx.cpp", "plan.hip", "spmv.hip", "spmv_xcs.hip", "spmm.hip", "sddmm.hip",
-           "index_stats.hip")
+           "index_stats.hip", "probe.hip")
 ARCH = "gfx950"
 
 # Packed-FP32 instructions (v_pk_*_f32) are disabled for all device code.

@@ -125,6 +125,14 @@ class RowBlockLayout:
     def kernel_name(self):
         return "spmv_rowblock_kernel"
 
+    def held_bytes(self, caller=()):
+        """Device bytes this layout holds beyond the caller's arrays ``caller``."""
+        plan = self.plan
+        mine = [plan.desc, plan.ranges, plan.workspace(), *plan.split_groups(), self.data,
+                self.cols, self.rowptr]
+        theirs = {t.untyped_storage().data_ptr() for t in caller if isinstance(t, torch.Tensor)}
+        return tensor_bytes(*[t for t in mine if t.untyped_storage().data_ptr() not in theirs])
+
     def describe(self):
         return {"layout": self.kind, "descriptors": self.plan.n_desc,
                 "split_rows": self.plan.n_split_rows, "partials": self.plan.n_parts,
@@ -197,6 +205,20 @@ def band_launch_order(n_desc, off, device):
     rank = torch.empty_like(b)
     rank[by_xcd] = b - first[xcd[by_xcd]]
     return torch.sort(rank * XCD_COUNT + xcd)[1]
+
+
+def tensor_bytes(*tensors):
+    """Device bytes held by the given tensors (each storage counted once; None skipped)."""
+    seen, total = set(), 0
+    for t in tensors:
+        if t is None or not isinstance(t, torch.Tensor):
+            continue
+        st = t.untyped_storage()
+        key = st.data_ptr()
+        if key not in seen:
+            seen.add(key)
+            total += st.nbytes()
+    return total
 
 
 def _ceil_log2(v):
@@ -503,6 +525,11 @@ class XcsLayout:
     def kernel_name(self):
         return "spmv_xcs_kernel"
 
+    def held_bytes(self, caller=()):
+        """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
+        return tensor_bytes(self.vals, self.pidx, self.items, self.item_runs, self.windows,
+                            self.dest, self.row_start, self.partials, self.panel_base)
+
     def describe(self):
         return {"layout": self.kind, "panels": self.n_panels, "tiles": self.n_tiles,
                 "long_row_tiles": self.n_long_tiles,
@@ -644,6 +671,11 @@ class PanelLayout:
     def kernel_name(self):
         return "spmv_panel_kernel"
 
+    def held_bytes(self, caller=()):
+        """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
+        return tensor_bytes(self.vals, self.pidx, self.rows, self.chunk_slot, self.slots,
+                            self.row_ptr, self.jobs, self.job_panel, self.partials)
+
     def describe(self):
         return {"layout": self.kind, "rows": self.n_rows, "panels": self.n_panels,
                 "col_bits": self.col_bits, "jobs": self.n_jobs,
@@ -696,6 +728,9 @@ class XcsHybridLayout:
 
     def kernel_name(self):
         return "spmv_xcs_kernel+spmv_panel_kernel"
+
+    def held_bytes(self, caller=()):
+        return self.short.held_bytes(caller) + self.long.held_bytes(caller)
 
     def describe(self):
         return {"layout": self.kind, "long_rows": self.long.n_rows,

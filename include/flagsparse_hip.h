@@ -332,6 +332,23 @@ int fsp_sddmm_csr(int dtype, int acc_f64, int out_f64, const int32_t* cols,
 int fsp_mtx_read(const char* path, int64_t* info, int64_t* rows, int64_t* cols, double* vals,
                  int64_t capacity);
 
+/*
+ * Measurement probes (bench.py): no counterpart in the reference and not on the product path.
+ * They time, alone, the access patterns the kernels above are bound by.  Each workgroup writes
+ * the sum of what it loaded to out[workgroup] (fsp_probe_*_blocks(n) values).
+ *   fsp_probe_gather  n (a multiple of 4) random 4-byte gathers x[idx[i]] from fp32 x[x_len],
+ *                     16 per thread in flight (idx int32, 16-byte aligned; clamped into x)
+ *   fsp_probe_rows    n random gathers of whole 256-byte rows b[rows[i]][0..64) from a
+ *                     row-major fp32 b[n_rows][64], 16 lanes per row, 4 rows per lane in
+ *                     flight (row indices clamped into b)
+ */
+int64_t fsp_probe_gather_blocks(int64_t n);
+int fsp_probe_gather(const float* x, int64_t x_len, const int32_t* idx, int64_t n, float* out,
+                     void* stream);
+int64_t fsp_probe_rows_blocks(int64_t n);
+int fsp_probe_rows(const float* b, int64_t n_rows, int64_t row_floats, const int32_t* rows,
+                   int64_t n, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

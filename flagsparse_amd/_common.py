@@ -24,6 +24,26 @@ _INDEX_LIMIT_INT32 = 2**31 - 1
 ROWPTR32_MAX_NNZ = _INDEX_LIMIT_INT32
 
 
+# CuPy / cuSPARSE: the reference compares against them when they import (_common.py:14-19),
+# and its scripts skip those comparisons when ``cp`` is None.  This build has no CuPy: the
+# module handles exist for those scripts, and the converters say so.
+cp = None
+cpx_sparse = None
+
+
+def _require_cupy():
+    raise RuntimeError("CuPy is not available in the flagsparse_amd build (the cuSPARSE "
+                       "comparison is skipped when cp is None)")
+
+
+def _cupy_from_torch(tensor):
+    _require_cupy()
+
+
+def _torch_from_cupy(array):
+    _require_cupy()
+
+
 def _is_complex_dtype(value_dtype):
     return value_dtype in (torch.complex64, torch.complex128)
 

@@ -99,7 +99,6 @@ extern "C" int fsp_mtx_read(const char* path, int64_t* info, int64_t* rows, int6
   bool have_size = false;
   int64_t n_rows = 0, n_cols = 0, nnz = 0, n_read = 0, n_missing = 0;
   while (c.p < c.end) {
-    const char* line = c.p;
     skip_blanks(c);
     if (at_eol(c)) {  // blank line
       next_line(c);
@@ -107,7 +106,7 @@ extern "C" int fsp_mtx_read(const char* path, int64_t* info, int64_t* rows, int6
     }
     if (*c.p == '%') {
       // "%%MatrixMarket matrix coordinate <field> <symmetry>" (case-insensitive)
-      if (c.end - line >= 14 && std::strncmp(c.p, "%%MatrixMarket", 14) == 0) {
+      if (c.end - c.p >= 14 && std::strncmp(c.p, "%%MatrixMarket", 14) == 0) {
         const char *b, *e;
         std::vector<std::string> t;
         while (token(c, &b, &e)) t.push_back(lower(b, e));

@@ -18,7 +18,14 @@ import time
 import torch
 
 from . import _abi, _common
-from ._common import _aligned, _benchmark_cuda_op, _tolerance_for_dtype
+from ._common import (  # noqa: F401  (cp and the converters: the reference scripts' names)
+    _aligned,
+    _benchmark_cuda_op,
+    _cupy_from_torch,
+    _tolerance_for_dtype,
+    _torch_from_cupy,
+    cp,
+)
 from ._plan import build_row_block_plan_device
 from .synthetic import build_random_csr, build_random_dense
 

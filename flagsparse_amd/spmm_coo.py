@@ -39,8 +39,9 @@ from .spmm_csr import (
 from .synthetic import build_random_coo, build_random_dense
 
 
-def _prepare_spmm_coo_inputs(data, row, col, B, shape):
-    """Validation and narrowing of spmm_coo.py:312-371 (same checks, messages and types)."""
+def _prepare_spmm_coo_inputs_checked(data, row, col, B, shape):
+    """Validation and narrowing of spmm_coo.py:312-371 (same checks, messages and types), plus
+    whether the rows are already in order (from the same pass over the indices)."""
     if len(shape) != 2:
         raise ValueError("shape must be a 2-tuple: (n_rows, n_cols)")
     if data.ndim != 1 or row.ndim != 1 or col.ndim != 1:
@@ -91,6 +92,13 @@ def _prepare_spmm_coo_inputs(data, row, col, B, shape):
     kernel_col = col.contiguous().to(torch.int32)
     B = B.contiguous()
     return data, kernel_row, kernel_col, B, n_rows, n_cols, int(B.shape[1]), row_sorted
+
+
+def _prepare_spmm_coo_inputs(data, row, col, B, shape):
+    """spmm_coo.py:312-371: the validated, narrowed inputs (data, row int32, col int32, B,
+    n_rows, n_cols, n_dense_cols) - the seven values the reference's scripts unpack
+    (tests/test_spmm_coo.py:290)."""
+    return _prepare_spmm_coo_inputs_checked(data, row, col, B, shape)[:7]
 
 
 def _resolve_spmm_coo_launch_config(n_dense_cols, nnz, block_n=None, block_nnz=256):
@@ -177,8 +185,8 @@ def _run_spmm_coo_route(data, row, col, B, shape, block_n=None, block_nnz=256, o
         raise ValueError("block_n must be positive when provided")
     if block_nnz is not None and block_nnz <= 0:
         raise ValueError("block_nnz must be positive when provided")
-    data, row, col, B, n_rows, n_cols, n_dense_cols, row_sorted = _prepare_spmm_coo_inputs(
-        data, row, col, B, shape)
+    data, row, col, B, n_rows, n_cols, n_dense_cols, row_sorted = \
+        _prepare_spmm_coo_inputs_checked(data, row, col, B, shape)
     launch = _resolve_spmm_coo_launch_config(n_dense_cols, data.numel(), block_n=block_n,
                                              block_nnz=block_nnz)
     dtype = data.dtype
@@ -230,6 +238,117 @@ def flagsparse_spmm_coo(data, row, col, B, shape, block_n=None, block_nnz=256, o
     """
     return _run_spmm_coo_route(data, row, col, B, shape, block_n=block_n, block_nnz=block_nnz,
                                out=out, return_time=return_time, route="rowrun")
+
+
+# ------------------------------------------------------------------------------------------
+# The canonical route of the reference's benchmark scripts (spmm_coo.py:11-18, 54-119,
+# 572-624, 697-713, 754-790): duplicates summed, entries in (row, col) order, float32 data and
+# B widened to float64 before the product, the result rounded back.  The helpers keep the
+# reference's argument lists and return tuples, which tests/test_spmm_coo.py:288-375 unpacks.
+# ------------------------------------------------------------------------------------------
+
+
+def _spmm_coo_compute_dtype(value_dtype):
+    """spmm_coo.py:11-18: float32 is computed in float64; fp16/bf16 in float32."""
+    if value_dtype in (torch.complex64, torch.complex128):
+        return torch.complex128 if value_dtype == torch.complex64 else value_dtype
+    if value_dtype in (torch.float16, torch.bfloat16):
+        return torch.float32
+    if value_dtype == torch.float32:
+        return torch.float64
+    return value_dtype
+
+
+def _build_torch_sparse_coo(data, row, col, shape):
+    """A coalesced torch COO tensor (int64 indices) for torch.sparse.mm (spmm_coo.py:54-75)."""
+    n_rows, n_cols = int(shape[0]), int(shape[1])
+    idx = torch.stack([row.to(torch.int64), col.to(torch.int64)]) if data.numel() else \
+        torch.empty((2, 0), dtype=torch.int64, device=data.device)
+    t = torch.sparse_coo_tensor(idx, data, size=(n_rows, n_cols), device=data.device,
+                                dtype=data.dtype)
+    return t.coalesce() if data.numel() else t
+
+
+def _prepare_spmm_coo_canonical_prepared(data, row, col, B, n_rows, n_cols, n_dense_cols):
+    """(data, row int64, col int64, B, n_rows, n_cols, n_dense_cols, output dtype, compute
+    dtype): the entries in the compute dtype with duplicate (row, col) pairs summed, in
+    (row, col) order; B in the compute dtype (spmm_coo.py:78-105)."""
+    output_dtype = data.dtype
+    compute_dtype = _spmm_coo_compute_dtype(output_dtype)
+    d = data if compute_dtype == output_dtype else data.to(compute_dtype)
+    Bc = B if compute_dtype == output_dtype else B.to(compute_dtype)
+    if d.numel() == 0:
+        z = torch.empty(0, dtype=torch.int64, device=data.device)
+        return (d.contiguous(), z, z.clone(), Bc, n_rows, n_cols, n_dense_cols, output_dtype,
+                compute_dtype)
+    coo = _build_torch_sparse_coo(d, row, col, (n_rows, n_cols))  # sums duplicates, sorts
+    idx = coo.indices()
+    return (coo.values().contiguous(), idx[0].contiguous(), idx[1].contiguous(), Bc, n_rows,
+            n_cols, n_dense_cols, output_dtype, compute_dtype)
+
+
+def _prepare_spmm_coo_canonical_inputs(data, row, col, B, shape):
+    """Validation, then the canonical entries (spmm_coo.py:108-118)."""
+    return _prepare_spmm_coo_canonical_prepared(*_prepare_spmm_coo_inputs(data, row, col, B,
+                                                                           shape))
+
+
+def _run_spmm_coo_canonical_route(canonical_data, canonical_row, canonical_col, canonical_B,
+                                  n_rows, n_dense_cols, output_dtype, block_n=None,
+                                  block_nnz=256, out=None, return_time=False, route="rowrun"):
+    """The product over canonical entries, in their dtype, rounded to ``output_dtype``, with
+    the reference's out checks and host timing (spmm_coo.py:572-624)."""
+    route = _normalize_spmm_coo_route(route)
+    n_cols = int(canonical_B.shape[0])
+    if out is not None:
+        if not out.is_cuda:
+            raise ValueError("out must be a CUDA tensor")
+        if out.device != canonical_data.device:
+            raise ValueError("out must be on the same CUDA device as the inputs")
+        if out.shape != (n_rows, n_dense_cols) or out.dtype != output_dtype:
+            raise ValueError("out shape/dtype must match result")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    C = _run_spmm_coo_route(canonical_data, canonical_row, canonical_col, canonical_B,
+                            (n_rows, n_cols), block_n=block_n, block_nnz=block_nnz, route=route)
+    if C.dtype != output_dtype:
+        C = C.to(output_dtype)
+    torch.cuda.synchronize()
+    elapsed_ms = (time.perf_counter() - t0) * 1000.0
+    if out is not None:
+        out.copy_(C)
+        C = out
+    return (C, elapsed_ms) if return_time else C
+
+
+def _build_spmm_coo_pytorch_reference_from_canonical(canonical_data, canonical_row,
+                                                     canonical_col, canonical_B, shape,
+                                                     output_dtype):
+    """torch.sparse.mm over the canonical entries, rounded to ``output_dtype``
+    (spmm_coo.py:697-713) - the scripts' correctness reference."""
+    coo = _build_torch_sparse_coo(canonical_data, canonical_row, canonical_col, shape)
+    expected = torch.sparse.mm(coo, canonical_B)
+    return expected if expected.dtype == output_dtype else expected.to(output_dtype)
+
+
+def _benchmark_spmm_coo_canonical_route(canonical_data, canonical_row, canonical_col,
+                                        canonical_B, n_rows, n_dense_cols, output_dtype, warmup,
+                                        iters, block_n, block_nnz, route):
+    """(values, steady ms, first-call ms) of the canonical route (spmm_coo.py:754-790)."""
+    route = _normalize_spmm_coo_route(route)
+
+    def op():
+        return _run_spmm_coo_canonical_route(canonical_data, canonical_row, canonical_col,
+                                             canonical_B, n_rows, n_dense_cols, output_dtype,
+                                             block_n=block_n, block_nnz=block_nnz, route=route)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    op()
+    torch.cuda.synchronize()
+    first_call_ms = (time.perf_counter() - t0) * 1000.0
+    values, steady_ms = _benchmark_cuda_op(op, warmup=warmup, iters=iters)
+    return values, steady_ms, first_call_ms
 
 
 # ------------------------------------------------------------------------------------------

@@ -271,7 +271,9 @@ def _spmm_lane_shape(n_dense_cols, dtype, B, C, tile_cols=None):
     """(lanes per B row G, elements per lane vec) for the gfx950 kernel.
 
     vec: 16-byte loads (4 fp32 / 2 fp64) when N and both base pointers allow it, else 2 or 1.
-    G: enough lanes to cover min(N, tile_cols) columns, a power of two <= 64.
+    G: enough lanes to cover min(N, tile_cols) columns, a power of two <= 64.  The kernel's
+    column tile is G * vec, so with narrower lanes (odd N, unaligned B or C) a tile of more
+    than 64 * vec columns is launched as tiles of 64 * vec.
     """
     vmax = 4 if dtype == torch.float32 else 2
     aligned = B.data_ptr() % 16 == 0 and C.data_ptr() % 16 == 0

@@ -8,7 +8,10 @@ size-independent properties that hold exactly:
         float32(fp64 oracle) on the default path; two calls bit-identical
   cfg4  COO 2M, 41.9M entries: oracle bars; A * 0 = 0
   cfg5  SpMM N=64 fp32 (opt) and N=16 fp64 (base): oracle bars; column j of A B = A B[:, j]
-        (the SpMV of the same matrix), bit for bit where both sum the same products in fp64
+        (the SpMV of the same matrix), bit for bit where both sum the same products in fp64;
+        the column-tiled launches (fp32 N=256, fp64 N=64 and N=256: B of 512 MiB - 2 GiB): a
+        strided sample of C's rows against the oracle over the same rows, columns of C in
+        different tiles against the SpMV of those columns
   sddmm cfg5's pattern, K = 64 fp32: oracle bars
 
 Bars as everywhere: relative L2 error <= 1e-5 (fp32) / 1e-12 (fp64) and the reference scripts'
@@ -101,6 +104,46 @@ def test_cfg5_full(dev, dtype, N):
     j = N // 3
     col = fs.flagsparse_spmv_csr(data, idx, ptr, B[:, j].contiguous(), shape)
     _bars(col, ref[:, j], dtype)
+
+
+def _sampled_rows(ptr, idx, data, rows):
+    """The CSR arrays of the listed rows only (host numpy), for an oracle over a row sample."""
+    ip = ptr.cpu().numpy().astype(np.int64)
+    starts, lengths = ip[rows], ip[rows + 1] - ip[rows]
+    sub_ptr = np.zeros(rows.size + 1, dtype=np.int64)
+    np.cumsum(lengths, out=sub_ptr[1:])
+    pos = np.arange(sub_ptr[-1]) - np.repeat(sub_ptr[:-1], lengths) + np.repeat(starts, lengths)
+    return sub_ptr, idx.cpu().numpy()[pos], data.cpu().numpy()[pos]
+
+
+@pytest.mark.parametrize("dtype,N,opt", [(torch.float32, 256, True), (torch.float64, 64, False),
+                                         (torch.float64, 256, True)])
+def test_cfg5_full_column_tiled(dev, dtype, N, opt):
+    # B of 512 MiB - 2 GiB: the launch reads B in column tiles (spmm_csr.SPMM_B_TILE_BYTES);
+    # a strided sample of C's rows against the oracle over the same rows, and a column of C
+    # against the SpMV of that column of B
+    from flagsparse_amd import spmm_csr
+
+    print(f"full size cfg5 column-tiled {dtype} N={N} opt={opt}", flush=True)
+    data, idx, ptr, shape = synthetic.csr_banded_random(dtype=dtype, device=dev)
+    B = synthetic.dense_uniform(shape[1], N, dtype=dtype, device=dev)
+    assert spmm_csr._auto_tile_cols(B) is not None
+    if opt:
+        C = fs.flagsparse_spmm_csr_opt(B=B, prepared=fs.prepare_spmm_csr_opt(data, idx, ptr,
+                                                                               shape))
+    else:
+        C = fs.flagsparse_spmm_csr(data, idx, ptr, B, shape)
+    rows = np.unique(np.concatenate([np.arange(0, shape[0], 61), [shape[0] - 1]]))
+    sp, si, sd = _sampled_rows(ptr, idx, data, rows)
+    ref = oracle.spmm_csr(sp, si, sd, B.cpu())
+    got = C[torch.from_numpy(rows).to(dev)]
+    _bars(got, ref, dtype)
+    for j in (0, N // 2 + 1, N - 1):  # first, middle (another tile) and last column
+        col = fs.flagsparse_spmv_csr(data, idx, ptr, B[:, j].contiguous(), shape)
+        name = "float64" if dtype == torch.float64 else "float32"
+        assert oracle.rel_l2(C[:, j], col) <= oracle.REL_L2_BOUND[name]
+    del C, B
+    torch.cuda.empty_cache()
 
 
 def test_sddmm_full(dev):

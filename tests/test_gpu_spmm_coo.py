@@ -196,3 +196,34 @@ def test_benchmark_spmm_coo_case(dev):
     r = spmm_coo.comprehensive_spmm_coo_test(n_rows=128, n_cols=96, nnz=1000, n_dense_cols=5,
                                              dtype=torch.float64, warmup=1, iters=2)
     assert r["parameters"]["route"] == "rowrun" and r["verification"]["triton_match_reference"]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("route", ["rowrun", "atomic"])
+def test_canonical_route_as_the_reference_scripts_drive_it(dev, dtype, route):
+    # tests/test_spmm_coo.py:288-375: validate, canonicalise (duplicates summed, entries in
+    # (row, col) order, float32 widened to float64), time the canonical route and compare it
+    # with torch.sparse.mm over the same canonical entries
+    import flagsparse.sparse_operations.spmm_coo as ast_ops
+
+    n_rows, n_cols, N = 600, 450, 24
+    data, row, col = _random_coo(dev, n_rows, n_cols, 7000, dtype, torch.int64, seed=21,
+                                 dups=400)
+    B = synthetic.dense_uniform(n_cols, N, dtype, seed=22, device=dev)
+    shape = (n_rows, n_cols)
+    print(f"canonical route {dtype} {route}", flush=True)
+    nd, nr, nc, nB, n_r, n_c, n_d = ast_ops._prepare_spmm_coo_inputs(data, row, col, B, shape)
+    cd, cr, cc, cB, _, _, _, out_dtype, compute_dtype = \
+        ast_ops._prepare_spmm_coo_canonical_prepared(nd, nr, nc, nB, n_r, n_c, n_d)
+    assert out_dtype == dtype and compute_dtype == torch.float64
+    assert cd.numel() < nd.numel()  # duplicates merged
+    key = cr * n_cols + cc
+    assert bool((key[1:] > key[:-1]).all())  # strictly increasing: sorted, no duplicates
+    values, steady_ms, first_ms = ast_ops._benchmark_spmm_coo_canonical_route(
+        cd, cr, cc, cB, n_r, n_d, out_dtype, 2, 5, None, 256, route)
+    assert values.dtype == dtype and steady_ms > 0 and first_ms > 0
+    expected = ast_ops._build_spmm_coo_pytorch_reference_from_canonical(cd, cr, cc, cB, shape,
+                                                                        out_dtype)
+    metrics = ast_ops._spmm_validation_metrics(values, expected)
+    assert metrics["max_relative_error"] <= (1e-6 if dtype == torch.float32 else 1e-13)
+    _check(values, row, col, data, B, n_rows)

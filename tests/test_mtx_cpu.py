@@ -162,3 +162,11 @@ def test_errors(tmp_path):
     v, r, c, _ = mtx.load_mtx_to_coo_torch(path, dtype=torch.float64, device="cpu",
                                            coalesce=False)
     assert v.tolist() == [0.0, 3.0]  # a missing value reads as 0 in this loader
+
+
+@pytest.mark.parametrize("text", ["   %%Matrix", "\t%%MatrixMarke", "  %", "%%MatrixMarket"])
+def test_truncated_header_at_end_of_file(tmp_path, text):
+    # a header cut short after leading blanks at the very end of the file (no newline): the
+    # reader compares only the bytes that exist, and reports a missing header
+    with pytest.raises(ValueError, match="header"):
+        mtx.read_mtx_entries(_write(tmp_path, "t.mtx", text))

@@ -17,7 +17,9 @@ roofline     the same bytes / the path's kernel time (all the kernels of one lau
              (the median of 5 such trials; all five in ``kernel_ms_trials``), against the
              8 TB/s HBM3E peak.  From the committed rocprofv3 summaries
              (profiles/<tag>_traffic.txt): ``traffic`` = FETCH_SIZE + WRITE_SIZE per launch,
-             ``l2_hit_rate`` and ``occupancy_percent`` per kernel.  ``bytes_gather_inclusive``
+             ``l2_hit_rate`` and ``occupancy_percent`` per kernel; ``traffic_gbs`` and
+             ``frac_traffic``: that traffic over the kernel time measured now (the rate at
+             which the kernel moves the bytes it does move).  ``bytes_gather_inclusive``
              counts x (SpMV) or B (SpMM) once per entry instead of once, and
              ``frac_gather_inclusive`` is that count over the same time against the peak.
              ``gather_bound`` (cfg3, cfg5): the probe kernels timed in the same run on the
@@ -45,6 +47,8 @@ Probe workloads (measurement only; the access patterns the kernels are bound by,
                 the gathers of XCD k to the k-th eighth of x (the XCS layout's placement)
   probe-rows    random 256-byte row gathers (fsp_probe_rows) from an fp32 B[rows, 64] of
                 --probe-bytes (default 268 MB, cfg5 N=64's B): 16.8M gathers, cfg5's random half
+  --cfg5-part band|random   cfg5 with only its banded or only its random half (16 entries per
+                row), to price each half of the matrix separately
 
 Algorithmic bytes count each array once at the width the kernel reads:
   SpMV  nnz*(v + i) + (n_rows + 1)*p + n_cols*v + n_rows*v
@@ -95,6 +99,9 @@ def _parse():
                     help="value type for cfg5 / coo5 / sddmm (default f32)")
     ap.add_argument("--n", type=int, default=64,
                     help="dense columns N for cfg5 / coo5, K for sddmm")
+    ap.add_argument("--cfg5-part", default="all", choices=("all", "band", "random"),
+                    help="cfg5: the whole matrix, or only its banded or only its random half "
+                         "(16 entries per row each) - the cost of each half")
     ap.add_argument("--opt", action="store_true",
                     help="SpMV: use_opt=True (native accumulation) instead of the default path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -357,11 +364,12 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
     }
 
 
-def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
+def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic, part="all"):
     from flagsparse_amd import spmm_csr as mod
 
     vdt = torch.float64 if dtype_name == "f64" else torch.float32
-    data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev)
+    halves = {"all": {}, "band": {"rand_nnz": 0}, "random": {"band_nnz": 0}}[part]
+    data, idx, ptr, shape = synthetic.csr_banded_random(dtype=vdt, device=dev, **halves)
     B = synthetic.dense_uniform(shape[1], N, dtype=vdt, device=dev)
     prepared, prep_call_ms = _timed_prepare(
         lambda: fs.prepare_spmm_csr_opt(data, idx, ptr, shape), torch)
@@ -384,9 +392,12 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
             "prepare_ms": round(prep_call_ms + layout_ms, 3), "prepare_call_ms": prep_call_ms,
             "layout_build_ms": layout_ms,
             "inputs": {"data": data, "indices": idx, "indptr": ptr, "B": B}}
+    if part != "all":
+        info["path"] += f"; only the {part} half of cfg5's rows (16 entries per row)"
     gather_bound = None
-    if N == 64 and vdt == torch.float32:
-        n_rand = nnz // 2  # cfg5: 16 of the 32 entries of every row at uniform random columns
+    if N == 64 and vdt == torch.float32 and part != "band":
+        # cfg5: 16 of the 32 entries of every row at uniform random columns
+        n_rand = nnz if part == "random" else nnz // 2
         gather_bound = lambda: _rows_bound(shape[1], n_rand, dev, torch,  # noqa: E731
                                            f"{n_rand} random 256-byte row gathers (cfg5's "
                                            f"random half) from a B of {shape[1] * 256} bytes")
@@ -413,7 +424,8 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic):
         "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), B, shape,
                                                        seconds, nbytes, 2 * nnz * N, torch),
         "dtype": dtype_name, "kernel": kc.kernel_name(),
-        "tag": f"{kc.kernel_name()}_cfg5_{dtype_name}_n{N}",
+        "tag": f"{kc.kernel_name()}_cfg5_{dtype_name}_n{N}" + ("" if part == "all" else
+                                                                f"_{part}_half"),
     }
 
 
@@ -625,7 +637,8 @@ def _build(name, args, dev, torch):
     if name == "cfg4":
         return _spmv_coo_workload(dev, torch, fs, synthetic)
     if name == "cfg5":
-        return _spmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
+        return _spmm_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic,
+                              getattr(args, "cfg5_part", "all"))
     if name == "coo5":
         return _spmm_coo_workload(dev, args.dtype or "f32", int(args.n), torch, fs, synthetic)
     if name == "sddmm":
@@ -690,6 +703,10 @@ def _roofline(w, ms_kernel, kernel_runs, torch):
            "profile_tag": w["tag"]}
     if prof.get("traffic"):
         out["traffic_over_algorithmic"] = round(prof["traffic"] / nbytes, 3)
+        # the rate the kernel moves what it does move: the profiled bytes over the time now
+        rate = prof["traffic"] / (ms_kernel * 1e-3) / 1e9
+        out["traffic_gbs"] = round(rate, 2)
+        out["frac_traffic"] = round(rate / HBM_PEAK_GBS, 4)
     for key in ("l2_hit_rate", "occupancy_percent"):
         if key in prof:
             out[key] = prof[key]

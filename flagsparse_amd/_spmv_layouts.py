@@ -87,6 +87,8 @@ WINDOW_ROWS = 2048
 # Stored runs of partial sums (one item's sums in one window) start on a multiple of this many
 # slots: 128 bytes of fp64 sums, a cache line.
 RUN_ALIGN = 16
+# Every combine window's stored range starts on a multiple of this many slots (a line).
+WINDOW_ALIGN = 16
 
 
 class RowBlockLayout:
@@ -471,16 +473,22 @@ class XcsLayout:
         if n_runs and int(padded.sum().item()) > 1.25 * n_pairs:
             align, padded = 1, run_len.clone()
         padded = torch.where(big[run_win], run_len, padded)
-        plen = padded[wkey]
-        base_sorted = torch.cumsum(plen, 0) - plen
-        run_base = torch.empty_like(base_sorted)
-        run_base[wkey] = base_sorted
-        n_store = int(padded.sum().item()) if n_runs else 0
         self.run_align = align
-        # windows: {row0, rows (-1: big), first stored slot, stored slots, sums, 0, 0, 0}
+        # windows: {row0, rows (-1: big), first stored slot, stored slots, sums, 0, 0, 0};
+        # every window starts on a line (WINDOW_ALIGN slots) whatever the run alignment; the
+        # slots between windows stay dest -1
         wlen = torch.bincount(run_win, weights=padded.to(torch.float64), minlength=n_win) \
             .to(torch.int64) if n_runs else torch.zeros(n_win, dtype=torch.int64, device=dev)
-        wbase = torch.cumsum(wlen, 0) - wlen
+        wspan = (wlen + WINDOW_ALIGN - 1) // WINDOW_ALIGN * WINDOW_ALIGN
+        wbase = torch.cumsum(wspan, 0) - wspan
+        n_store = int(wspan.sum().item()) if n_win else 0
+        plen = padded[wkey]
+        win_sorted = run_win[wkey]
+        in_win = torch.cumsum(plen, 0) - plen  # exclusive, over all windows
+        wfirst = torch.cumsum(wlen, 0) - wlen  # the same, at each window's first run
+        run_base = torch.empty_like(in_win)
+        run_base[wkey] = wbase[win_sorted] + in_win - wfirst[win_sorted]
+        del plen, win_sorted, in_win, wfirst
         wsum = torch.bincount(pair_win, minlength=n_win) if n_pairs else \
             torch.zeros(n_win, dtype=torch.int64, device=dev)
         z = torch.zeros_like(row0)
@@ -566,7 +574,7 @@ def _panel_col_bits(n_cols, value_bytes):
     """Bits of a column inside its panel: 2^bits values fit the LDS copy (and no more than x
     needs)."""
     fit = (_abi.caps()["panel_bytes"] // value_bytes).bit_length() - 1
-    return max(1, min(fit, _ceil_log2(max(int(n_cols), 2))))
+    return max(1, min(fit, 15, _ceil_log2(max(int(n_cols), 2))))  # 15: the 16-bit entries
 
 
 def panel_row_min(n_cols, value_bytes):
@@ -598,8 +606,8 @@ class PanelLayout:
         self.n_cols, self.nnz = int(n_cols), int(data.numel())
         n_rows = int(rowptr.numel()) - 1
         cb = _panel_col_bits(n_cols, data.element_size())
-        if n_rows >= (1 << (32 - cb)):
-            raise ValueError("too many rows for the panel packing")
+        if n_rows >= (1 << (63 - cb)):
+            raise ValueError("too many rows for the panel layout")
         self.col_bits = cb
         self.rows = rows.to(torch.int32).contiguous()
         rp = rowptr.to(torch.int64)
@@ -642,14 +650,17 @@ class PanelLayout:
         torch.cumsum(torch.bincount(slot_row, minlength=n_rows), 0, out=row_ptr[1:])
         self.row_ptr = row_ptr.to(torch.int32).contiguous()
         self.n_rows = n_rows
-        # storage order inside a chunk: logical quad 2L + h at quad 64h + L
+        # values: inside a chunk, logical quad 2L + h at quad 64h + L; 16-bit entries in logical
+        # order, the column in the panel | 0x8000 at a run start (the kernel needs only where
+        # runs start: a chunk's runs take consecutive slots)
         mem = panel_storage_positions(n_entries, chunk, dev)
         self.vals = torch.zeros_like(vals)
         self.vals[mem] = vals[:n_entries]
-        packed = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
-        self.pidx = torch.zeros(max(n_entries, 4), dtype=torch.int32, device=dev)
-        self.pidx[mem] = packed
-        del pidx, rowpos, starts, slot_row, vals, packed, mem
+        pcol = (pidx & ((1 << cb) - 1)) | (starts.to(torch.int64) << 15)
+        self.pcol = torch.zeros(max(n_entries, 8), dtype=torch.int16, device=dev)
+        self.pcol[:n_entries] = torch.where(pcol >= (1 << 15), pcol - (1 << 16), pcol) \
+            .to(torch.int16)
+        del pidx, rowpos, starts, slot_row, vals, pcol, mem
         # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
         # sizes keep the rounds of workgroups even)
         per_panel = padded // chunk
@@ -673,7 +684,7 @@ class PanelLayout:
 
     def held_bytes(self, caller=()):
         """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
-        return tensor_bytes(self.vals, self.pidx, self.rows, self.chunk_slot, self.slots,
+        return tensor_bytes(self.vals, self.pcol, self.rows, self.chunk_slot, self.slots,
                             self.row_ptr, self.jobs, self.job_panel, self.partials)
 
     def describe(self):
@@ -686,7 +697,7 @@ class PanelLayout:
         args = self._args.get(bool(acc_f64))
         if args is None:  # static arguments converted once per accumulation mode
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
-            args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
+            args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pcol),
                     self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
                     p(self.job_panel), self.n_jobs, p(self.chunk_slot), p(self.partials),
                     int(self.partials.numel()), p(self.rows), p(self.row_ptr), p(self.slots),
@@ -695,7 +706,7 @@ class PanelLayout:
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
         a[9] = None if row_map is None else row_map.data_ptr()
-        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.jobs,
+        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pcol, self.jobs,
                                               self.job_panel, self.chunk_slot, self.rows,
                                               self.row_ptr, self.slots))
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")

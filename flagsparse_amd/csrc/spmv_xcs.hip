@@ -33,10 +33,13 @@
 // x is cut into panels of 2^col_bits columns, at most 64 KiB each, and a row with many entries
 // per panel gets them gathered from an LDS copy of the panel instead of from L2:
 //   entries  the long rows' entries ordered by (panel, row), each panel's run padded with
-//            zero entries of its last row to a multiple of kPanelChunk (pidx as above, the row
-//            being the index in the list of long rows); inside a chunk, logical quad 2L + h
-//            (lane L's h-th quad) is stored at quad h * 64 + L, so each 16-byte load of a
-//            wave reads one contiguous kilobyte
+//            zero entries of its last row to a multiple of kPanelChunk.  An entry is its value
+//            and 16 bits, pcol = column in the panel | 0x8000 when it starts a run (its row
+//            differs from the previous entry's, or it opens a chunk): the kernel needs row
+//            changes only, never row numbers, since a chunk's runs take consecutive slots.
+//            Values: inside a chunk, logical quad 2L + h (lane L's h-th quad) is stored at
+//            quad h * 64 + L, so each 16-byte load of a wave reads one contiguous kilobyte;
+//            pcol in logical order (lane L's 8 entries are the 16 bytes at 16 L)
 //   chunks   kPanelChunk consecutive entries, one wave's unit of work; chunk_slot[c] is the
 //            first partial slot of chunk c, which has one slot per run (row) it holds
 //   jobs     workgroup j copies panel job_panel[j] into LDS and its waves take the chunks
@@ -309,6 +312,9 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
     re[m] = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
   }
 
+  // Every load of a thread is issued before the first is used.  (Measured on MI355X, cfg3:
+  // 50.6 us as written, 52.1 / 53.0 us reading 4 slots per load - 16-byte sums, 8-byte dest
+  // words - in 2 / 4 groups per thread: more registers, fewer workgroups per CU.)
   for (int c0 = 0; c0 < len; c0 += kWinRound) {  // uniform
     A v[kWinPer];
     int d[kWinPer];
@@ -359,9 +365,11 @@ __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned
 constexpr int kPanelPerLane = (int)kPanelChunk / kWave;
 static_assert(kPanelPerLane == 8, "eight entries per lane");
 
+constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
+
 template <typename T, typename A>
 __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
-    const T* __restrict__ vals, const uint32_t* __restrict__ pidx, int col_bits,
+    const T* __restrict__ vals, const uint16_t* __restrict__ pcol, int col_bits,
     const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
     const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
     A* __restrict__ partials, int64_t n_partials) {
@@ -382,8 +390,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   // issued before the current chunk is reduced, so a wave keeps two chunks in flight.  The
   // chunk's first slot is loaded with its entries: loaded on its own after the next chunk's
   // loads, waiting for it (loads complete in order) also waited for the whole next chunk.
-  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], uint32_t (&c)[kPanelPerLane],
-                        int& slot0) {
+  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], i32x4& c, int& slot0) {
     const int64_t e0 = (int64_t)chunk * kPanelChunk;
 #pragma unroll
     for (int h = 0; h < kPanelPerLane / 4; ++h) {
@@ -396,36 +403,34 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
         const f64x2 b = ld_stream<true>(reinterpret_cast<const f64x2*>(vals + m + 2));
         v[4 * h] = a.x; v[4 * h + 1] = a.y; v[4 * h + 2] = b.x; v[4 * h + 3] = b.y;
       }
-      const i32x4 cc = ld_stream<true>(reinterpret_cast<const i32x4*>(pidx + m));
-      c[4 * h] = (uint32_t)cc.x; c[4 * h + 1] = (uint32_t)cc.y;
-      c[4 * h + 2] = (uint32_t)cc.z; c[4 * h + 3] = (uint32_t)cc.w;
     }
+    c = ld_stream<true>(reinterpret_cast<const i32x4*>(pcol + e0) + lane);
     slot0 = chunk_slot[chunk];
   };
   // One chunk's reduction: products from the LDS panel, then the runs (rows) that end in each
   // lane are emitted, the first one with the carry from the lanes before (a segmented wave
   // scan), into consecutive slots from the chunk's first.
-  auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const uint32_t (&c)[kPanelPerLane],
-                          int slot0) {
+  auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const i32x4& cq, int slot0) {
     A prod[kPanelPerLane];
-    int row[kPanelPerLane];
+    bool start[kPanelPerLane];
+    const uint32_t cw[4] = {(uint32_t)cq.x, (uint32_t)cq.y, (uint32_t)cq.z, (uint32_t)cq.w};
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
-      prod[q] = A(v[q]) * A(sx[c[q] & cmask]);
-      row[q] = (int)(c[q] >> col_bits);
+      const uint32_t e = (q & 1) ? cw[q >> 1] >> 16 : cw[q >> 1] & 0xffffu;
+      prod[q] = A(v[q]) * A(sx[e & cmask]);
+      start[q] = (e & kRunStart) != 0;
     }
     constexpr int kLast = kPanelPerLane - 1;
-    int prev_row = __shfl_up(row[kLast], 1, kWave);
-    if (lane == 0) prev_row = -1;  // a chunk starts a run
-    int next_row = __shfl_down(row[0], 1, kWave);
-    if (lane == kWave - 1) next_row = -1;  // and ends one
-    const bool cont = row[0] == prev_row;
+    // a chunk starts a run whatever its first entry says, and ends one
+    const bool cont = lane > 0 && !start[0];
+    const int next_start = __shfl_down((int)start[0], 1, kWave);
+    const bool end_last = lane == kWave - 1 || next_start != 0;
     int has_head = cont ? 0 : 1;
-    int n_end = row[kLast] != next_row ? 1 : 0;
+    int n_end = end_last ? 1 : 0;
     A piece = A(0);
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
-      if (q > 0 && row[q] != row[q - 1]) {
+      if (q > 0 && start[q]) {
         has_head = 1;
         ++n_end;
         piece = A(0);
@@ -460,7 +465,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
       run += prod[q];
-      const bool ends = q < kLast ? row[q] != row[q + 1] : row[kLast] != next_row;
+      const bool ends = q < kLast ? start[q + 1] : end_last;
       store_partial(out_rsrc, ends ? k * (unsigned)sizeof(A) : kDropOffset,
                     (first && cont) ? carry + run : run);
       if (ends) {
@@ -476,7 +481,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   // waited on memory: 5.2 TB/s on cfg3's long rows).
   constexpr int kStride = kPanelBlock / kWave;
   T va[kPanelPerLane], vb[kPanelPerLane], vc[kPanelPerLane];
-  uint32_t ca[kPanelPerLane], cb[kPanelPerLane], cc[kPanelPerLane];
+  i32x4 ca = {0, 0, 0, 0}, cb = {0, 0, 0, 0}, cc = {0, 0, 0, 0};
   int sa = 0, sb = 0, sc = 0;
   int ch = jobs[job] + wid;
   // The first chunks' entries are requested before the panel copy, so the two overlap.
@@ -574,7 +579,7 @@ __global__ __launch_bounds__(kBlock) void panel_combine_kernel(
 }
 
 template <typename T, typename A>
-int launch_panels(const void* vals, const uint32_t* pidx, int col_bits, const void* x,
+int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const void* x,
                   int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
                   const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_slot,
                   void* partials, int64_t n_partials, const int32_t* rows,
@@ -583,7 +588,7 @@ int launch_panels(const void* vals, const uint32_t* pidx, int col_bits, const vo
   if (n_jobs > 0) {
     hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
                        ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
-                       pidx, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
+                       pcol, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
                        chunk_slot, static_cast<A*>(partials), n_partials);
     int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
     if (rc) return rc;
@@ -645,7 +650,7 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
 #undef FSP_XCS_ARGS
 }
 
-extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
+extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pcol,
                                int64_t n_entries, int col_bits, const void* x, int64_t x_len,
                                void* y, const int32_t* row_map, const int32_t* jobs,
                                const int32_t* job_panel, int64_t n_jobs,
@@ -663,27 +668,28 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
       n_jobs > 0x7fffffffLL || n_rows > 0x7fffffffLL - kBlock)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: n_entries must be a multiple of " +
                                      std::to_string(kPanelChunk) + " and sizes within int32");
-  if (col_bits < 1 || (vsize << col_bits) > kPanelBytes)
-    return set_error(FSP_EINVAL, "fsp_spmv_panels: a panel of 2^col_bits values must fit " +
+  if (col_bits < 1 || col_bits > 15 || (vsize << col_bits) > kPanelBytes)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: col_bits must be <= 15 and a panel of "
+                                 "2^col_bits values must fit " +
                                      std::to_string(kPanelBytes) + " bytes of LDS");
-  if (n_jobs > 0 && (!vals || !pidx || !x || !jobs || !job_panel || !chunk_slot || !partials))
+  if (n_jobs > 0 && (!vals || !pcol || !x || !jobs || !job_panel || !chunk_slot || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null pointer");
   if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null row pointer");
-  if (!aligned16(vals) || !aligned16(pidx))
-    return set_error(FSP_EINVAL, "fsp_spmv_panels: vals and pidx must be 16-byte aligned");
+  if (!aligned16(vals) || !aligned16(pcol))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: vals and pcol must be 16-byte aligned");
   if (n_jobs == 0 && n_rows == 0) return FSP_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == FSP_F32) {
     if (acc_f64)
-      return launch_panels<float, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+      return launch_panels<float, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
                                           job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
                                           row_ptr, slots, n_rows, st);
-    return launch_panels<float, float>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+    return launch_panels<float, float>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
                                        job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
                                        row_ptr, slots, n_rows, st);
   }
-  return launch_panels<double, double>(vals, pidx, col_bits, x, x_len, y, row_map, jobs,
+  return launch_panels<double, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
                                        job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
                                        row_ptr, slots, n_rows, st);
 }

@@ -191,7 +191,7 @@ int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals, const int32_t*
  *   item_runs    int32 quadruples {first slot, first sum, sums, stored length}: an item's row
  *                run sums (in row order) [first sum, first sum + sums) go to partials[first
  *                slot ...], followed by zeros up to the stored length
- *   partials     8 bytes per stored slot
+ *   partials     the stored slots (8 bytes each with fp64 accumulation, else the value size)
  *   windows, dest, row_start
  *                the second launch (y written in row order), one workgroup per window:
  *                windows[w] = 8 int32 {row0, rows, first slot, stored length, sums, 0, 0, 0}:
@@ -217,16 +217,18 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  * a matrix in the panel layout: x is cut into panels of 2^col_bits columns, copied one at a
  * time into LDS, and the gathers read LDS.  Same reference launches as fsp_spmv_csr; used
  * beside fsp_spmv_xcs for power-law matrices, whose long rows put many entries in every panel.
- *   vals, pidx   n_entries entries (a multiple of fsp_panel_chunk(), 16-byte aligned) in
- *                (panel, row) order, each panel's run padded with val 0 entries of its last
- *                row: pidx = (i << col_bits) | (column - panel * 2^col_bits), i the index of
- *                the row in rows; inside each chunk the quad (4 entries) at logical position
- *                2L + h is stored at quad position 64h + L (L < 64, h < 2)
- *   col_bits     2^col_bits values must fit fsp_panel_bytes_cap() bytes
+ *   vals, pcol   n_entries entries (a multiple of fsp_panel_chunk(), both 16-byte aligned)
+ *                in (panel, row) order, each panel's run padded with val 0 entries of its
+ *                last row.  pcol (16 bits) = column - panel * 2^col_bits, | 0x8000 when the
+ *                entry starts a run: its row differs from the previous entry's (the first
+ *                entry of a chunk always starts one).  vals: inside each chunk the quad (4
+ *                entries) at logical position 2L + h is stored at quad position 64h + L
+ *                (L < 64, h < 2); pcol in logical order
+ *   col_bits     <= 15, and 2^col_bits values must fit fsp_panel_bytes_cap() bytes
  *   jobs         n_jobs + 1 increasing chunk indices: workgroup j copies panel job_panel[j] of
  *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])
  *   chunk_slot   per chunk the first partial slot (8 bytes each); a chunk writes one slot per
- *                row it holds, in entry order
+ *                run it holds, in entry order
  *   n_partials   slots in partials (n_partials * 8 < 2^31: the kernel stores through a buffer
  *                resource of that size)
  *   rows, row_ptr, slots
@@ -235,7 +237,7 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  *                k = l, l + 64, ... in order, then a fixed tree).  Calls sharing partials must
  *                not overlap.  Other rows of y are not written.
  */
-int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
+int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pcol,
                     int64_t n_entries, int col_bits, const void* x, int64_t x_len, void* y,
                     const int32_t* row_map, const int32_t* jobs, const int32_t* job_panel,
                     int64_t n_jobs, const int32_t* chunk_slot, void* partials,

@@ -162,3 +162,28 @@ def test_automatic_choice(dev):
     assert p._kernel(False).kind == "xcs-hybrid"
     _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
            exact_fp32=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_combine_unaligned_windows(dev, monkeypatch, dtype):
+    # runs and windows starting anywhere (not on a line); small windows, so that there are
+    # hundreds, some of one long row
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-l2")
+    monkeypatch.setattr(_spmv_layouts, "RUN_ALIGN", 1)
+    monkeypatch.setattr(_spmv_layouts, "WINDOW_ALIGN", 1)
+    monkeypatch.setattr(_spmv_layouts, "WINDOW_SLOTS", 128)
+    monkeypatch.setattr(_spmv_layouts, "WINDOW_ROWS", 64)
+    rng = np.random.default_rng(11)
+    # two rows long enough to have more sums than a window holds (one-row windows)
+    lengths = np.concatenate([rng.zipf(1.8, 30000).clip(max=20000), [400000, 3, 400000]])
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, 1 << 21, 23, dtype)
+    print(f"unaligned combine windows {dtype}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    lay = p._kernel(False)
+    assert lay.kind == "xcs"
+    w = lay.windows.cpu().numpy().reshape(-1, 8)
+    assert (w[:, 2] % 4 != 0).any() and (w[:, 2] % 4 == 0).any() and (w[:, 1] < 0).any()
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
+        _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))

@@ -81,13 +81,18 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
                     slot_row[first + j] = -2
             nxt = s0 + cnt
         assert nxt == len(sums)
-    # the combine windows: consecutive rows and consecutive stored ranges, every slot once
+    # the combine windows: consecutive rows and consecutive stored ranges, each starting on
+    # a line (WINDOW_ALIGN slots), every slot once; the slots between windows are never written
+    # and their dest is -1
     windows = layout.windows.numpy().reshape(-1, 8).astype(np.int64)
     dest = layout.dest.numpy().astype(np.int64)
     row_start = layout.row_start.numpy().astype(np.int64)
+    line = _spmv_layouts.WINDOW_ALIGN
     next_row, next_slot = 0, 0
     for row0, nr, base, ln, total, _, _, _ in windows:
-        assert row0 == next_row and base == next_slot
+        assert row0 == next_row and base == -(-next_slot // line) * line
+        gap = np.arange(next_slot, base)
+        assert np.all(slot_row[gap] == -1) and np.all(dest[gap] == -1)
         sl = np.arange(base, base + ln)
         next_slot = base + ln
         real = sl[slot_row[sl] >= 0] if ln else sl
@@ -123,8 +128,9 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
                 s = acc(s + v)
             y[out(row0 + i)] = s
         next_row = row0 + nr
-    assert next_row == layout.n_rows and next_slot == max(n_store, 1) or n_store == 1
-    assert np.all(slot_row != -1) or n_store == 1
+    tail = -(-next_slot // line) * line
+    assert next_row == layout.n_rows and tail == n_store or n_store == 1
+    assert np.all(dest[next_slot:] == -1) and np.all(slot_row[next_slot:] == -1)
     return y
 
 
@@ -169,11 +175,11 @@ def _check_structure(layout, data, cols, rowptr):
 
 def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
     """numpy restatement of spmv_panel_kernel + the combine over a PanelLayout: each chunk's
-    runs (a chunk start or a row change starts one) go to consecutive slots from
-    chunk_slot[c]; row i of the layout then gets its slots' sum in slot order."""
+    runs (a chunk start or an entry marked as a run start opens one) go to consecutive slots
+    from chunk_slot[c]; row i of the layout then gets its slots' sum in slot order."""
     chunk = _abi.caps()["panel_chunk"]
     cb = layout.col_bits
-    vals, pidx = _panel_logical(layout)
+    vals, pidx, start = _panel_logical(layout)
     vals = vals.astype(acc)
     jobs = layout.jobs.numpy()
     jp = layout.job_panel.numpy()
@@ -184,13 +190,12 @@ def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
         for c in range(jobs[j], jobs[j + 1]):
             sl = int(cslot[c])
             e = np.arange(c * chunk, (c + 1) * chunk)
-            rows = pidx[e] >> cb
             cols = base + (pidx[e] & ((1 << cb) - 1))
             prod = vals[e] * x[np.minimum(cols, x.size - 1)].astype(acc)
             assert np.all(cols[vals[e] != 0] < x.size)
             s = acc(0)
             for q in range(chunk):
-                if q > 0 and rows[q] != rows[q - 1]:
+                if q > 0 and start[e[q]]:
                     partials[sl] = s
                     sl += 1
                     s = acc(0)
@@ -209,15 +214,32 @@ def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
 
 
 def _panel_logical(layout):
-    """(vals, pidx as int64) of a PanelLayout in logical order: inside a chunk of 512, lane
-    L's quad h (logical quad 2L + h) is read from quad 64h + L."""
+    """(vals, pidx = row << col_bits | column in the panel, run-start flags) of a PanelLayout
+    in logical order.  Values: inside a chunk of 512, lane L's quad h (logical quad 2L + h) is
+    read from quad 64h + L.  The 16-bit entries hold no row: an entry's row is that of its
+    slot (chunk_slot of its chunk + the run starts before it in the chunk), read back through
+    the combine tables (row_ptr, slots) - so the check below also checks that the run starts
+    and the slot tables agree."""
     n = layout.n_entries
+    if n == 0:
+        return layout.vals.numpy()[:0], np.zeros(0, np.int64), np.zeros(0, bool)
     p = np.arange(n)
     lq = (p % 512) // 4
     mem = (p // 512) * 512 + ((lq % 2) * 64 + lq // 2) * 4 + p % 4
-    return (layout.vals.numpy()[:n][mem] if n else layout.vals.numpy()[:0],
-            layout.pidx.numpy().view(np.uint32)[:n][mem].astype(np.int64) if n else
-            np.zeros(0, np.int64))
+    pc = layout.pcol.numpy().view(np.uint16)[:n].astype(np.int64)
+    start = (pc & 0x8000) != 0
+    col = pc & 0x7FFF
+    assert np.all(col < (1 << layout.col_bits))
+    assert np.all(start[::512])  # every chunk opens a run
+    run_in_chunk = np.cumsum(start.reshape(-1, 512), axis=1).reshape(-1) - 1
+    slot = layout.chunk_slot.numpy().astype(np.int64)[p // 512] + run_in_chunk
+    rp, slots = layout.row_ptr.numpy(), layout.slots.numpy()
+    slot_row = np.full(layout.n_partials, -1, dtype=np.int64)
+    for i in range(layout.n_rows):
+        slot_row[slots[rp[i]:rp[i + 1]]] = i
+    assert np.all(slot_row >= 0)
+    row = slot_row[slot]
+    return layout.vals.numpy()[:n][mem], (row << layout.col_bits) | col, start
 
 
 def _check_panels(layout, data, cols, rowptr):
@@ -233,7 +255,11 @@ def _check_panels(layout, data, cols, rowptr):
     assert np.all(np.diff(jobs) >= 1)
     assert np.all(np.diff(jobs) <= _spmv_layouts.PANEL_JOB_CHUNKS)
     assert np.all(np.diff(jp) >= 0)
-    vals, pidx = _panel_logical(layout)
+    vals, pidx, start = _panel_logical(layout)
+    e = np.arange(layout.n_entries)
+    rows_all = pidx >> cb
+    # a run starts exactly where the row changes or a chunk opens
+    assert np.array_equal(start, (e % chunk == 0) | np.r_[True, rows_all[1:] != rows_all[:-1]])
     assert np.array_equal(np.sort(_spmv_layouts.panel_storage_positions(
         layout.n_entries, chunk, "cpu").numpy()), np.arange(layout.n_entries))  # a permutation
     got = []

@@ -275,7 +275,9 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
 // then the fixed workgroup tree.
 // A separate launch: the kernel boundary makes the first pass's partials visible on every
 // XCD, so neither pass needs a device-scope fence.
-constexpr int kWinPer = 8;  // loads per thread and round of the stream step
+// Loads per thread and round of the stream step: 16 covers a whole 4096-slot window in one
+// round (measured on MI355X: cfg3 49.1 us at 16, 50.8 at 8, 53.0 at 4; cfg4 14.7 / 14.4 / 13.8)
+constexpr int kWinPer = 16;
 constexpr int kWinRound = kWinPer * kBlock;
 
 template <typename T, typename A>
@@ -313,8 +315,9 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   }
 
   // Every load of a thread is issued before the first is used.  (Measured on MI355X, cfg3:
-  // 50.6 us as written, 52.1 / 53.0 us reading 4 slots per load - 16-byte sums, 8-byte dest
-  // words - in 2 / 4 groups per thread: more registers, fewer workgroups per CU.)
+  // reading 4 slots per load - 16-byte sums, 8-byte dest words - was slower, 52.1 / 53.0 us
+  // with 2 / 4 groups per thread against 50.6 us at 8 single loads: more registers, fewer
+  // workgroups per CU.)
   for (int c0 = 0; c0 < len; c0 += kWinRound) {  // uniform
     A v[kWinPer];
     int d[kWinPer];
@@ -549,18 +552,24 @@ int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void*
 }
 
 // Second pass of the panel layout: its rows have hundreds of slots each, so one wave adds a
-// row's slots - lane l the slots k = l, l + 64, ... in order, then a fixed wave tree.
+// row's slots - lane l the slots k = l, l + 64, ... in order, then a fixed wave tree.  A chunk
+// gives consecutive rows consecutive slots, so a line of partials serves 16 neighbouring rows:
+// workgroups are remapped so that each XCD takes one contiguous range of rows and fetches such
+// a line into its L2 once.
 template <typename T, typename A>
 __global__ __launch_bounds__(kBlock) void panel_combine_kernel(
     const int* __restrict__ rows, const int* __restrict__ row_ptr, const int* __restrict__ slots,
     const A* __restrict__ partials, T* __restrict__ y, const int* __restrict__ row_map,
     int n_rows) {
-  const int i = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x / kWave);
+  const int blk = xcd_logical_block((int)blockIdx.x, (int)gridDim.x);
+  const int i = blk * kWavesPerBlock + (int)(threadIdx.x / kWave);
   if (i >= n_rows) return;  // whole waves leave together
   const int lane = threadIdx.x & (kWave - 1);
   const int a = row_ptr[i], b = row_ptr[i + 1];
   A acc = A(0);
-  constexpr int kU = 4;  // slot indices, then partials, requested kU at a time
+  // slot indices, then partials, requested kU at a time (measured on MI355X, cfg3: 12.6 us
+  // in hardware order, 9.3 us remapped, 8.6 us with 8 instead of 4 at a time)
+  constexpr int kU = 8;
   for (int k0 = a + lane; k0 < b; k0 += kU * kWave) {
     int sl[kU];
     A pv[kU];

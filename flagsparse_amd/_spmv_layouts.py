@@ -645,6 +645,8 @@ class PanelLayout:
         self.chunk_slot = (torch.cumsum(runs, 0) - runs).to(torch.int32).contiguous()
         slot_row = rowpos[starts]
         self.n_partials = int(slot_row.numel())
+        if self.n_partials * 8 > _INDEX_LIMIT_INT32:
+            raise ValueError("more panel partial sums than the kernel's store range holds")
         self.slots = torch.sort(slot_row, stable=True)[1].to(torch.int32).contiguous()
         row_ptr = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
         torch.cumsum(torch.bincount(slot_row, minlength=n_rows), 0, out=row_ptr[1:])
@@ -780,7 +782,7 @@ def build_layout(data, cols, rowptr, n_cols, one_shot=False):
     """The layout for one CSR (or COO row-run) matrix: XCS when it pays, else row blocks.
     one_shot: the layout serves a single call (no prepared object), so the row-block layout,
     which builds in about a millisecond, is taken; the XCS layouts take tens of milliseconds to
-    build (cfg3: 43 ms for a 0.4 ms product, against 3.1 ms for the row-block product)."""
+    build (cfg3: 46 ms for a 0.32 ms product, against 3.3 ms for the row-block product)."""
     mode = FORCE
     nnz = int(data.numel())
     if mode is None and one_shot:

@@ -462,3 +462,15 @@ def test_sample_indices_stay_in_bounds():
         assert idx.numel() == min(n, 1 << 20)
         assert int(idx.min()) == 0 and int(idx.max()) == n - 1
         assert bool((idx[1:] >= idx[:-1]).all())
+
+
+def test_panel_partials_beyond_store_range(monkeypatch):
+    # the panel kernel stores its partial sums through a buffer of < 2^31 bytes; a layout
+    # needing more is refused at build time (build_layout then takes row blocks)
+    lengths = [9000, 20000, 5000]
+    vals, cols, ip, x = _case(lengths, 200000, 6)
+    rows = torch.arange(len(lengths))
+    lay = PanelLayout(vals, cols, ip, 200000, rows)
+    monkeypatch.setattr(_spmv_layouts, "_INDEX_LIMIT_INT32", 8 * lay.n_partials - 1)
+    with pytest.raises(ValueError):
+        PanelLayout(vals, cols, ip, 200000, rows)

@@ -16,7 +16,7 @@ Two layouts, chosen once per matrix at prepare time:
     are summed through partials in a fixed order (deterministic).
 
 ``PanelLayout`` (csrc/spmv_xcs.hip, ``spmv_panel_kernel``)
-    The long rows of a power-law matrix: x cut into panels of 64 KiB, the rows' entries ordered
+    The long rows of a power-law matrix: x cut into panels of 128 KiB, the rows' entries ordered
     by (panel, row); a workgroup copies one panel into LDS and its waves gather from there, so
     these gathers run at LDS speed instead of the L2 request rate.  One partial per (row,
     chunk of 512 entries), added per row in a fixed order.
@@ -74,10 +74,11 @@ BAND_MIN_SHARE = 0.2
 # Panel layout: chunks per job at most (a job copies its panel of x into LDS once), and the
 # long-row rule of the hybrid - rows with at least PANEL_RUNS entries per x panel go to the
 # panel layout when they hold at least PANEL_MIN_SHARE of the entries.  Measured on MI355X
-# for cfg3: PANEL_RUNS 8 (rows >= 4096 entries, 62 % of nnz) 466 us, 4: 498 us, 16: 474 us;
-# 256 chunks per job (one job per panel) 466 us, 128: 476 us.
-PANEL_JOB_CHUNKS = 256
-PANEL_RUNS = 8
+# for cfg3 with 128 KiB panels (256 of them; whole path): PANEL_RUNS 1 / 2 / 3 / 4 / 8 (rows
+# >= 256 / 512 / 768 / 1024 / 2048 entries) 0.302 / 0.289 / 0.289 / 0.290 / 0.309 ms with
+# 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms.
+PANEL_JOB_CHUNKS = 1024
+PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
 # Combine windows of the XCS layout: consecutive rows with at most this many partial slots
@@ -594,7 +595,7 @@ def panel_storage_positions(n_entries, chunk, device):
 
 
 class PanelLayout:
-    """Rows whose x gathers are served from LDS copies of 64 KiB x panels (module docstring).
+    """Rows whose x gathers are served from LDS copies of 128 KiB x panels (module docstring).
     ``rows`` are the output rows of the CSR rows given; built on the device."""
 
     kind = "panels"

@@ -24,7 +24,7 @@ constexpr int64_t kXcsRowsCap = 8192;                    // rows of one XCS tile
 constexpr int64_t kXcsWinSlotsCap = 4096;                // partial slots of one combine window
 constexpr int64_t kXcsWinRowsCap = 2048;                 // rows of one combine window
 constexpr int64_t kXcsItemRunsCap = 64;                  // stored runs (windows) of one XCS item
-constexpr int64_t kPanelBytes = 65536;                   // x panel copied to LDS (panel SpMV)
+constexpr int64_t kPanelBytes = 131072;                  // x panel copied to LDS (panel SpMV)
 constexpr int64_t kPanelChunk = 512;                     // entries per wave chunk (panel SpMV)
 
 // Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).

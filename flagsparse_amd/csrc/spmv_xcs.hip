@@ -30,7 +30,7 @@
 //           and invalidate the XCD's L2, which holds the x panel this layout exists to keep.
 //
 // Long rows of power-law matrices also have a second layout, "panels" (spmv_panel_kernel):
-// x is cut into panels of 2^col_bits columns, at most 64 KiB each, and a row with many entries
+// x is cut into panels of 2^col_bits columns, at most 128 KiB each, and a row with many entries
 // per panel gets them gathered from an LDS copy of the panel instead of from L2:
 //   entries  the long rows' entries ordered by (panel, row), each panel's run padded with
 //            zero entries of its last row to a multiple of kPanelChunk.  An entry is its value
@@ -350,7 +350,11 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
 // panel copy.  A wave's chunk: lane L holds entries [8L, 8L + 8), their rows non-decreasing;
 // the runs that end in a lane are emitted by it, the first one with the carry from the lanes
 // before (a segmented wave scan), into consecutive slots from chunk_slot[c] in entry order.
-constexpr int kPanelBlock = 512;
+// One workgroup of 16 waves per CU, holding a 128 KiB panel (measured on MI355X, cfg3 whole
+// path: 0.315 ms with 64 KiB panels and 2 workgroups of 512 per CU, 0.290 ms with 128 KiB
+// panels and 1024 threads, 0.300 ms with 128 KiB and 512 threads; the wider panels also
+// carry more rows - those with 4 entries per panel - at the same partial count).
+constexpr int kPanelBlock = 1024;
 // Word 3 of a raw buffer resource on gfx9-family GPUs (gfx950): 32-bit data format, no swizzle.
 constexpr int kBufferRsrcWord3 = 0x00020000;
 // A byte offset no buffer here reaches: a store there is dropped by the range check.

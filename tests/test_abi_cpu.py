@@ -231,8 +231,8 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert b"multiple" in L.fsp_last_error()
     assert panels(n_partials=1 << 28) == -1       # partials beyond the buffer resource range
     assert b"partial" in L.fsp_last_error()
-    assert panels(col_bits=15) == -1              # 2^15 fp32 > 64 KiB of LDS
-    assert panels(dtype=1, col_bits=14) == -1     # 2^14 fp64 > 64 KiB
+    assert panels(col_bits=16) == -1              # beyond the 16-bit entries (and 128 KiB)
+    assert panels(dtype=1, col_bits=15) == -1     # 2^15 fp64 > 128 KiB of LDS
     assert b"LDS" in L.fsp_last_error()
     assert panels(n_entries=512, n_jobs=1) == -1  # jobs without arrays
     assert panels(n_rows=3) == -1                 # combine without its arrays

@@ -376,7 +376,7 @@ def test_xcs_item_run_cap(monkeypatch):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_panel_layout(dtype, monkeypatch):
-    # long rows over 200k columns (13 or 12 bits per panel), jobs cut at PANEL_JOB_CHUNKS
+    # long rows over 200k columns (15 or 14 bits per panel), jobs cut at PANEL_JOB_CHUNKS
     monkeypatch.setattr(_spmv_layouts, "PANEL_JOB_CHUNKS", 3)
     lengths = [9000, 20000, 5000, 0, 12000, 30000, 7]
     vals, cols, ip, x = _case(lengths, 200000, 6, dtype)

@@ -105,6 +105,33 @@ __device__ __forceinline__ double dpp_add(double v) {
   return v + __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
 }
 
+// DPP move: the value of the lane that CTRL selects, or `old` where that lane lies outside the
+// control's range or ROW_MASK leaves the lane's row out (bound_ctrl off).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_mov(int old, int v) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __int_as_float(dpp_mov<CTRL, ROW_MASK>(__float_as_int(old), __float_as_int(v)));
+}
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_mov(double old, double v) {
+  const int64_t b = __double_as_longlong(v), o = __double_as_longlong(old);
+  const int lo = dpp_mov<CTRL, ROW_MASK>((int)(o & 0xffffffff), (int)(b & 0xffffffff));
+  const int hi = dpp_mov<CTRL, ROW_MASK>((int)(o >> 32), (int)(b >> 32));
+  return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
+}
+
+// DPP controls of the GFX9 family used for wave-wide scans.
+constexpr int kDppRowShr1 = 0x111;  // row_shr:n = 0x110 + n (inside a 16-lane row)
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+constexpr int kDppWaveShl1 = 0x130;  // lane i takes lane i + 1
+constexpr int kDppWaveShr1 = 0x138;  // lane i takes lane i - 1
+
 // Sum over aligned groups of g lanes (g a power of two, g <= 64); every lane of the group ends
 // with the total.  Inside a 16-lane row: quad permutes [1,0,3,2] and [2,3,0,1], then the
 // half-row mirror and the row mirror (DPP); across rows, lane exchanges (ds_bpermute).  The

@@ -360,6 +360,20 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // A byte offset no buffer here reaches: a store there is dropped by the range check.
 constexpr unsigned kDropOffset = 0xFFFFFFF0u;
 
+// One step of the panel kernel's wave scans: (h, v) a segmented inclusive scan (h: a run
+// starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c a plain
+// one, with the source lane that the DPP control CTRL selects.  Lanes without a source take
+// the identity (no start, -0.0, 0): -0.0 + v is v for every v.
+template <int CTRL, int ROW_MASK, typename A>
+__device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
+  const int ho = dpp_mov<CTRL, ROW_MASK>(0, h);
+  const A vo = dpp_mov<CTRL, ROW_MASK>(A(-0.0), v);
+  const int co = dpp_mov<CTRL, ROW_MASK>(0, c);
+  if (!h) v = vo + v;
+  h |= ho;
+  c += co;
+}
+
 template <typename A>
 __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned off, A v) {
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -370,6 +384,9 @@ __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned
   }
 }
 constexpr int kPanelPerLane = (int)kPanelChunk / kWave;
+// Chunk buffers per wave of spmv_panel_kernel (registers: 8 values + 4 words of 16-bit entries
+// + a slot each).  Measured on MI355X, cfg3: 3, 4, 5 and 6 buffers within 0.2 us of each other.
+constexpr int kPanelBuffers = 3;
 static_assert(kPanelPerLane == 8, "eight entries per lane");
 
 constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
@@ -428,10 +445,9 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       start[q] = (e & kRunStart) != 0;
     }
     constexpr int kLast = kPanelPerLane - 1;
-    // a chunk starts a run whatever its first entry says, and ends one
+    // a chunk starts a run whatever its first entry says, and ends one (lane 63 reads 1)
     const bool cont = lane > 0 && !start[0];
-    const int next_start = __shfl_down((int)start[0], 1, kWave);
-    const bool end_last = lane == kWave - 1 || next_start != 0;
+    const bool end_last = dpp_mov<kDppWaveShl1>(1, (int)start[0]) != 0;
     int has_head = cont ? 0 : 1;
     int n_end = end_last ? 1 : 0;
     A piece = A(0);
@@ -444,24 +460,20 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       }
       piece += prod[q];
     }
-    // segmented scan of (has_head, last piece) and a plain scan of n_end over the wave
+    // segmented scan of (has_head, last piece) and a plain scan of n_end over the wave, all
+    // through DPP: shifts by 1, 2, 4 and 8 inside each 16-lane row, then each row's last lane
+    // to the rows after it; then each lane takes the scans of the lane before it
     int h_in = has_head;
     A v_in = piece;
     int c_in = n_end;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int ho = __shfl_up(h_in, off, kWave);
-      const A vo = __shfl_up(v_in, off, kWave);
-      const int co = __shfl_up(c_in, off, kWave);
-      if (lane >= off) {
-        if (!h_in) v_in = vo + v_in;
-        h_in |= ho;
-        c_in += co;
-      }
-    }
-    A carry = __shfl_up(v_in, 1, kWave);
-    int slot = __shfl_up(c_in, 1, kWave);
-    if (lane == 0) { carry = A(0); slot = 0; }
+    seg_scan_step<kDppRowShr1, 0xF>(h_in, v_in, c_in);
+    seg_scan_step<kDppRowShr1 + 1, 0xF>(h_in, v_in, c_in);
+    seg_scan_step<kDppRowShr1 + 3, 0xF>(h_in, v_in, c_in);
+    seg_scan_step<kDppRowShr1 + 7, 0xF>(h_in, v_in, c_in);
+    seg_scan_step<kDppRowBcast15, 0xA>(h_in, v_in, c_in);
+    seg_scan_step<kDppRowBcast31, 0xC>(h_in, v_in, c_in);
+    const A carry = dpp_mov<kDppWaveShr1>(A(0), v_in);   // lane 0: 0
+    const int slot = dpp_mov<kDppWaveShr1>(0, c_in);
     // Emission: eight stores per lane, always issued - a lane without a run ending at q
     // stores past the end of the buffer, which the buffer range check drops.  Under per-lane
     // conditions the number of stores varied, and the compiler then waited for every
@@ -483,17 +495,24 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     }
   };
 
-  // Three chunk buffers per wave: while one chunk is reduced, the next two are in flight (with
-  // two, the next chunk was requested only one reduction before it was needed, and the waves
-  // waited on memory: 5.2 TB/s on cfg3's long rows).
+  // kNB chunk buffers per wave: while one chunk is reduced, the next kNB - 1 are in flight
+  // (with two buffers the next chunk was requested only one reduction before it was needed,
+  // and the waves waited on memory: 5.2 TB/s on cfg3's long rows).
   constexpr int kStride = kPanelBlock / kWave;
-  T va[kPanelPerLane], vb[kPanelPerLane], vc[kPanelPerLane];
-  i32x4 ca = {0, 0, 0, 0}, cb = {0, 0, 0, 0}, cc = {0, 0, 0, 0};
-  int sa = 0, sb = 0, sc = 0;
+  constexpr int kNB = kPanelBuffers;
+  T v[kNB][kPanelPerLane];
+  i32x4 c[kNB];
+  int sl[kNB];
+#pragma unroll
+  for (int b = 0; b < kNB; ++b) {
+    c[b] = i32x4{0, 0, 0, 0};
+    sl[b] = 0;
+  }
   int ch = jobs[job] + wid;
   // The first chunks' entries are requested before the panel copy, so the two overlap.
-  if (ch < c_hi) load_chunk(ch, va, ca, sa);
-  if (ch + kStride < c_hi) load_chunk(ch + kStride, vb, cb, sb);
+#pragma unroll
+  for (int b = 0; b + 1 < kNB; ++b)
+    if (ch + b * kStride < c_hi) load_chunk(ch + b * kStride, v[b], c[b], sl[b]);
 
   // Panel copy: every thread issues all its 16-byte loads before its first LDS store (one
   // memory round trip; as a load-store loop the copy waited for each load in turn).  A panel
@@ -519,15 +538,18 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   }
   __syncthreads();
 
-  for (; ch < c_hi; ch += 3 * kStride) {
-    if (ch + 2 * kStride < c_hi) load_chunk(ch + 2 * kStride, vc, cc, sc);
-    reduce_chunk(va, ca, sa);
-    if (ch + kStride >= c_hi) break;
-    if (ch + 3 * kStride < c_hi) load_chunk(ch + 3 * kStride, va, ca, sa);
-    reduce_chunk(vb, cb, sb);
-    if (ch + 2 * kStride >= c_hi) break;
-    if (ch + 4 * kStride < c_hi) load_chunk(ch + 4 * kStride, vb, cb, sb);
-    reduce_chunk(vc, cc, sc);
+  // Buffer b holds the chunks ch + b * kStride of each round; before reducing one, the chunk
+  // kNB - 1 strides ahead is requested into the buffer reduced last.
+  for (; ch < c_hi; ch += kNB * kStride) {
+#pragma unroll
+    for (int b = 0; b < kNB; ++b) {
+      const int cur = ch + b * kStride;
+      if (cur >= c_hi) break;
+      const int ahead = cur + (kNB - 1) * kStride;
+      if (ahead < c_hi) load_chunk(ahead, v[(b + kNB - 1) % kNB], c[(b + kNB - 1) % kNB],
+                                   sl[(b + kNB - 1) % kNB]);
+      reduce_chunk(v[b], c[b], sl[b]);
+    }
   }
 }
 

@@ -60,6 +60,32 @@ constexpr int kRowsCap = (int)kXcsRowsCap;
 constexpr int kItemRuns = (int)kXcsItemRunsCap;
 static_assert(kItemRuns <= kBlock, "an item's runs are loaded one per thread");
 
+// One step of the wave scans of the XCS and panel kernels: (h, v) a segmented inclusive scan
+// (h: a run starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c
+// a plain one, with the source lane that the DPP control CTRL selects.  Lanes without a source
+// take the identity (no start, -0.0, 0): -0.0 + v is v for every v.
+template <int CTRL, int ROW_MASK, typename A>
+__device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
+  const int ho = dpp_mov<CTRL, ROW_MASK>(0, h);
+  const A vo = dpp_mov<CTRL, ROW_MASK>(A(-0.0), v);
+  const int co = dpp_mov<CTRL, ROW_MASK>(0, c);
+  if (!h) v = vo + v;
+  h |= ho;
+  c += co;
+}
+
+// Inclusive scans over the wave (seg_scan_step): shifts by 1, 2, 4 and 8 inside each 16-lane
+// row, then each row's last lane to the rows after it - a fixed order of additions.
+template <typename A>
+__device__ __forceinline__ void wave_seg_scan(int& h, A& v, int& c) {
+  seg_scan_step<kDppRowShr1, 0xF>(h, v, c);
+  seg_scan_step<kDppRowShr1 + 1, 0xF>(h, v, c);
+  seg_scan_step<kDppRowShr1 + 3, 0xF>(h, v, c);
+  seg_scan_step<kDppRowShr1 + 7, 0xF>(h, v, c);
+  seg_scan_step<kDppRowBcast15, 0xA>(h, v, c);
+  seg_scan_step<kDppRowBcast31, 0xC>(h, v, c);
+}
+
 // Occupancy cap.  The kernel needs at most 16 KiB of LDS (its partial-sum buffer) and 64
 // VGPRs, so up to 8 workgroups would share a CU; measured on MI355X, 5 per CU gathers fastest
 // (cfg3: 562 us at 5, 574 at 6 and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue
@@ -203,26 +229,15 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   int h_in = has_head;
   A v_in = piece;
   int c_in = n_end;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int ho = __shfl_up(h_in, off, kWave);
-    const A vo = __shfl_up(v_in, off, kWave);
-    const int co = __shfl_up(c_in, off, kWave);
-    if (lane >= off) {
-      if (!h_in) v_in = vo + v_in;
-      h_in |= ho;
-      c_in += co;
-    }
-  }
+  wave_seg_scan(h_in, v_in, c_in);
   if (lane == kWave - 1) {
     s_wh[wid] = h_in;
     s_wv[wid] = v_in;
     s_wc[wid] = c_in;
   }
-  int h_ex = __shfl_up(h_in, 1, kWave);
-  A v_ex = __shfl_up(v_in, 1, kWave);
-  int c_ex = __shfl_up(c_in, 1, kWave);
-  if (lane == 0) { h_ex = 0; v_ex = A(0); c_ex = 0; }
+  const int h_ex = dpp_mov<kDppWaveShr1>(0, h_in);  // lane 0: (0, 0, 0)
+  const A v_ex = dpp_mov<kDppWaveShr1>(A(0), v_in);
+  const int c_ex = dpp_mov<kDppWaveShr1>(0, c_in);
   __syncthreads();
   A pv = A(0);
   int pc = 0;
@@ -360,20 +375,6 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // A byte offset no buffer here reaches: a store there is dropped by the range check.
 constexpr unsigned kDropOffset = 0xFFFFFFF0u;
 
-// One step of the panel kernel's wave scans: (h, v) a segmented inclusive scan (h: a run
-// starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c a plain
-// one, with the source lane that the DPP control CTRL selects.  Lanes without a source take
-// the identity (no start, -0.0, 0): -0.0 + v is v for every v.
-template <int CTRL, int ROW_MASK, typename A>
-__device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
-  const int ho = dpp_mov<CTRL, ROW_MASK>(0, h);
-  const A vo = dpp_mov<CTRL, ROW_MASK>(A(-0.0), v);
-  const int co = dpp_mov<CTRL, ROW_MASK>(0, c);
-  if (!h) v = vo + v;
-  h |= ho;
-  c += co;
-}
-
 template <typename A>
 __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned off, A v) {
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -466,12 +467,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     int h_in = has_head;
     A v_in = piece;
     int c_in = n_end;
-    seg_scan_step<kDppRowShr1, 0xF>(h_in, v_in, c_in);
-    seg_scan_step<kDppRowShr1 + 1, 0xF>(h_in, v_in, c_in);
-    seg_scan_step<kDppRowShr1 + 3, 0xF>(h_in, v_in, c_in);
-    seg_scan_step<kDppRowShr1 + 7, 0xF>(h_in, v_in, c_in);
-    seg_scan_step<kDppRowBcast15, 0xA>(h_in, v_in, c_in);
-    seg_scan_step<kDppRowBcast31, 0xC>(h_in, v_in, c_in);
+    wave_seg_scan(h_in, v_in, c_in);
     const A carry = dpp_mov<kDppWaveShr1>(A(0), v_in);   // lane 0: 0
     const int slot = dpp_mov<kDppWaveShr1>(0, c_in);
     // Emission: eight stores per lane, always issued - a lane without a run ending at q

@@ -449,23 +449,25 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     // a chunk starts a run whatever its first entry says, and ends one (lane 63 reads 1)
     const bool cont = lane > 0 && !start[0];
     const bool end_last = dpp_mov<kDppWaveShl1>(1, (int)start[0]) != 0;
+    // Running sums of the runs inside the lane (restarted where a run starts): the run that
+    // ends at q holds run[q]; the last one is the lane's piece of a run that may go on.
     int has_head = cont ? 0 : 1;
     int n_end = end_last ? 1 : 0;
-    A piece = A(0);
+    A run[kPanelPerLane];
+    run[0] = prod[0];
 #pragma unroll
-    for (int q = 0; q < kPanelPerLane; ++q) {
-      if (q > 0 && start[q]) {
+    for (int q = 1; q < kPanelPerLane; ++q) {
+      run[q] = start[q] ? prod[q] : run[q - 1] + prod[q];
+      if (start[q]) {
         has_head = 1;
         ++n_end;
-        piece = A(0);
       }
-      piece += prod[q];
     }
     // segmented scan of (has_head, last piece) and a plain scan of n_end over the wave, all
     // through DPP: shifts by 1, 2, 4 and 8 inside each 16-lane row, then each row's last lane
     // to the rows after it; then each lane takes the scans of the lane before it
     int h_in = has_head;
-    A v_in = piece;
+    A v_in = run[kPanelPerLane - 1];
     int c_in = n_end;
     wave_seg_scan(h_in, v_in, c_in);
     const A carry = dpp_mov<kDppWaveShr1>(A(0), v_in);   // lane 0: 0
@@ -474,19 +476,17 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     // stores past the end of the buffer, which the buffer range check drops.  Under per-lane
     // conditions the number of stores varied, and the compiler then waited for every
     // outstanding memory operation (the prefetched chunks included) before each chunk.
+    // The lane's first run, when it continues from the lanes before (cont), adds the carry.
     unsigned k = (unsigned)(slot0 + slot);
-    bool first = true;
-    A run = A(0);
+    bool first = cont;
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
-      run += prod[q];
       const bool ends = q < kLast ? start[q + 1] : end_last;
       store_partial(out_rsrc, ends ? k * (unsigned)sizeof(A) : kDropOffset,
-                    (first && cont) ? carry + run : run);
+                    first ? carry + run[q] : run[q]);
       if (ends) {
         ++k;
         first = false;
-        run = A(0);
       }
     }
   };

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 
@@ -39,6 +39,8 @@ SIGNATURES = {
     "fsp_xcs_item_runs_cap": (_i64, []),
     "fsp_panel_bytes_cap": (_i64, []),
     "fsp_panel_chunk": (_i64, []),
+    "fsp_panel_chunk_runs_cap": (_i64, []),
+    "fsp_plan_panel_chunks": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p]),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p,
                             _i64, _i64, _p, _p, _p, _p, _i64, _i32, _p]),
@@ -144,4 +146,5 @@ def caps():
         "xcs_item_runs": int(L.fsp_xcs_item_runs_cap()),
         "panel_bytes": int(L.fsp_panel_bytes_cap()),
         "panel_chunk": int(L.fsp_panel_chunk()),
+        "panel_chunk_runs": int(L.fsp_panel_chunk_runs_cap()),
     }

@@ -586,6 +586,21 @@ def panel_row_min(n_cols, value_bytes):
     return PANEL_RUNS * max(1, n_panels)
 
 
+def plan_panel_chunks(panel_runs, run_len, chunk, runs_cap):
+    """(run_pos, panel_end) of fsp_plan_panel_chunks for device (or host) int64 tensors, on
+    the device of run_len: where each run's first entry is stored, and where each panel ends."""
+    dev = run_len.device
+    pr = panel_runs.to("cpu", torch.int64).contiguous()
+    rl = run_len.to("cpu", torch.int64).contiguous()
+    n_panels = int(pr.numel()) - 1
+    pos = torch.empty(max(int(rl.numel()), 1), dtype=torch.int64)
+    end = torch.empty(max(n_panels, 1), dtype=torch.int64)
+    _abi.check(_abi.lib().fsp_plan_panel_chunks(pr.data_ptr(), n_panels, rl.data_ptr(),
+                                                int(chunk), int(runs_cap), pos.data_ptr(),
+                                                end.data_ptr()), "fsp_plan_panel_chunks")
+    return pos[:rl.numel()].to(dev), end[:n_panels].to(dev)
+
+
 def panel_storage_positions(n_entries, chunk, device):
     """Memory position of each logical entry of the panel layout: inside a chunk, lane L's
     h-th quad (logical quad 2L + h) is stored at quad 64h + L."""
@@ -619,22 +634,39 @@ class PanelLayout:
         n_panels = max(1, -(-self.n_cols >> cb))
         order = torch.sort(panel, stable=True)[1]
         panel = panel[order]
-        cnt = torch.bincount(panel, minlength=n_panels)
-        padded = (cnt + chunk - 1) // chunk * chunk
-        seg = torch.cumsum(padded, 0) - padded
-        first = torch.cumsum(cnt, 0) - cnt
-        n_entries = int(padded.sum().item())
-        dest = seg[panel] + torch.arange(self.nnz, device=dev) - first[panel]
         row_s = row[order]
+        del row
+        # runs: the entries of one row in one panel; chunks of at most `chunk` entries and
+        # panel_chunk_runs runs (the kernel stages a chunk's run sums one per lane), planned on
+        # the host run by run (fsp_plan_panel_chunks); the rest of a chunk closed early, and of
+        # each panel's last chunk, is padding
+        brk = torch.ones(self.nnz, dtype=torch.bool, device=dev)
+        if self.nnz > 1:
+            brk[1:] = (panel[1:] != panel[:-1]) | (row_s[1:] != row_s[:-1])
+        run_first = torch.nonzero(brk).flatten()
+        del brk
+        run_len = torch.diff(run_first, append=torch.tensor([self.nnz], device=dev))
+        panel_runs = torch.zeros(n_panels + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(torch.bincount(panel[run_first], minlength=n_panels), 0,
+                     out=panel_runs[1:])
+        run_pos, panel_end = plan_panel_chunks(panel_runs, run_len, chunk,
+                                               caps["panel_chunk_runs"])
+        panel_start = torch.cat([panel_end.new_zeros(1), panel_end[:-1]])
+        n_entries = int(panel_end[-1].item()) if n_panels else 0
+        run_of = torch.repeat_interleave(torch.arange(run_first.numel(), device=dev), run_len)
+        dest = run_pos[run_of] + (torch.arange(self.nnz, device=dev) - run_first[run_of])
+        del run_of, run_first, run_len, run_pos
         vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
         vals[dest] = data[order]
-        # padding: value 0 in the last row of its panel, so it adds no run
-        last = torch.zeros(n_panels, dtype=torch.int64, device=dev)
-        has = cnt > 0
-        last[has] = row_s[(first + cnt - 1)[has]]
-        pidx = torch.repeat_interleave(last, padded) << cb
+        # the row of every stored position: padding continues the entry before it (positions
+        # ascend with (panel, row), so a running maximum of that key fills the gaps)
+        key = torch.full((n_entries,), -1, dtype=torch.int64, device=dev)
+        key[dest] = panel * max(n_rows, 1) + row_s
+        if n_entries:
+            key = torch.cummax(key, 0)[0]
+        pidx = ((key % max(n_rows, 1)) << cb)
         pidx[dest] = (row_s << cb) | (c64[order] & ((1 << cb) - 1))
-        del order, row, row_s, c64, dest
+        del order, row_s, c64, dest, key, panel
         self.n_entries = n_entries
         # one partial slot per (chunk, run): runs start at a chunk start or a row change
         n_chunks = n_entries // chunk
@@ -643,6 +675,9 @@ class PanelLayout:
         starts[1:] = rowpos[1:] != rowpos[:-1]
         starts[::chunk] = True
         runs = starts.view(n_chunks, chunk).sum(1)
+        if n_chunks and int(runs.max().item()) > caps["panel_chunk_runs"]:
+            raise AssertionError("panel chunk plan: a chunk holds more runs than the kernel "
+                                 "stages")
         self.chunk_slot = (torch.cumsum(runs, 0) - runs).to(torch.int32).contiguous()
         slot_row = rowpos[starts]
         self.n_partials = int(slot_row.numel())
@@ -666,12 +701,12 @@ class PanelLayout:
         del pidx, rowpos, starts, slot_row, vals, pcol, mem
         # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
         # sizes keep the rounds of workgroups even)
-        per_panel = padded // chunk
+        per_panel = (panel_end - panel_start) // chunk
         n_jobs_p = (per_panel + PANEL_JOB_CHUNKS - 1) // PANEL_JOB_CHUNKS
         self.job_panel = torch.repeat_interleave(torch.arange(n_panels, device=dev), n_jobs_p)
         job_first = torch.cumsum(n_jobs_p, 0) - n_jobs_p
         k = torch.arange(self.job_panel.numel(), device=dev) - job_first[self.job_panel]
-        starts_c = (seg // chunk)[self.job_panel] + \
+        starts_c = (panel_start // chunk)[self.job_panel] + \
             k * per_panel[self.job_panel] // n_jobs_p[self.job_panel]
         self.jobs = torch.cat([starts_c, torch.tensor([n_chunks], device=dev)]).to(
             torch.int32).contiguous()
@@ -792,15 +827,18 @@ def build_layout(data, cols, rowptr, n_cols, one_shot=False):
         mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
     if mode in ("xcs", "xcs-l2", "xcs-hybrid") and nnz <= _INDEX_LIMIT_INT32 // 2 and \
             int(n_cols) <= (1 << 27) and int(rowptr.numel()) > 1:
-        try:
-            if mode != "xcs-l2":
-                rp = rowptr.to(torch.int64)
-                lengths = rp[1:] - rp[:-1]
-                long_mask = lengths >= panel_row_min(n_cols, data.element_size())
-                long_nnz = int(lengths[long_mask].sum().item())
-                if long_nnz > 0 and (mode == "xcs-hybrid" or long_nnz >= PANEL_MIN_SHARE * nnz):
+        if mode != "xcs-l2":
+            rp = rowptr.to(torch.int64)
+            lengths = rp[1:] - rp[:-1]
+            long_mask = lengths >= panel_row_min(n_cols, data.element_size())
+            long_nnz = int(lengths[long_mask].sum().item())
+            if long_nnz > 0 and (mode == "xcs-hybrid" or long_nnz >= PANEL_MIN_SHARE * nnz):
+                try:
                     return XcsHybridLayout(data, cols, rowptr, n_cols, long_mask,
                                            FORCE_PANELS_PER_XCD)
+                except ValueError:
+                    pass  # a part too large for its packing: XCS alone, else row blocks
+        try:
             return XcsLayout(data, cols, rowptr, n_cols, FORCE_PANELS_PER_XCD)
         except ValueError:
             pass  # too large for the packing: row blocks

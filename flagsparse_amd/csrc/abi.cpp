@@ -27,7 +27,7 @@ using namespace fsp;
 
 extern "C" const char* fsp_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int fsp_abi_version(void) { return 8; }
+extern "C" int fsp_abi_version(void) { return 9; }
 
 extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }
@@ -40,6 +40,7 @@ extern "C" int64_t fsp_xcs_window_rows_cap(void) { return kXcsWinRowsCap; }
 extern "C" int64_t fsp_xcs_item_runs_cap(void) { return kXcsItemRunsCap; }
 extern "C" int64_t fsp_panel_bytes_cap(void) { return kPanelBytes; }
 extern "C" int64_t fsp_panel_chunk(void) { return kPanelChunk; }
+extern "C" int64_t fsp_panel_chunk_runs_cap(void) { return kPanelChunkRunsCap; }
 
 extern "C" int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
                                    int64_t rows_cap, int64_t long_threshold, int64_t chunk,
@@ -94,5 +95,49 @@ extern "C" int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_
   *n_desc = nd;
   *n_parts = np;
   *n_split_rows = ns;
+  return FSP_OK;
+}
+
+// Chunks of the panel layout, greedily: each panel's runs (a row's entries in that panel) are
+// laid out one after the other; a chunk (chunk entries) closes when it is full, or after the
+// runs_cap-th run that starts or continues in it, in which case the rest of it is padding.  A
+// run longer than what is left of a chunk continues in the next one (and counts there too).
+extern "C" int fsp_plan_panel_chunks(const int64_t* panel_runs, int64_t n_panels,
+                                     const int64_t* run_len, int64_t chunk, int64_t runs_cap,
+                                     int64_t* run_pos, int64_t* panel_end) {
+  if (n_panels < 0 || chunk < 1 || runs_cap < 1)
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: need n_panels >= 0, chunk >= 1, "
+                                 "runs_cap >= 1");
+  if (n_panels > 0 && (!panel_runs || !panel_end))
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: null pointer");
+  if (n_panels > 0 && panel_runs[0] != 0)
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: panel_runs[0] must be 0");
+  int64_t pos = 0;
+  for (int64_t p = 0; p < n_panels; ++p) {
+    const int64_t r0 = panel_runs[p], r1 = panel_runs[p + 1];
+    if (r1 < r0) return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: panel_runs decreasing");
+    if (r1 > r0 && (!run_len || !run_pos))
+      return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: null run arrays");
+    int64_t used = 0, runs = 0;  // entries and runs of the open chunk
+    for (int64_t r = r0; r < r1; ++r) {
+      int64_t left = run_len[r];
+      if (left < 1) return set_error(FSP_EINVAL, "fsp_plan_panel_chunks: empty run");
+      if (runs == runs_cap) {  // close the chunk: the rest is padding
+        pos += chunk - used;
+        used = runs = 0;
+      }
+      run_pos[r] = pos;
+      while (left > 0) {
+        const int64_t piece = left < chunk - used ? left : chunk - used;
+        ++runs;
+        used += piece;
+        pos += piece;
+        left -= piece;
+        if (used == chunk) used = runs = 0;
+      }
+    }
+    if (used > 0) pos += chunk - used;  // the panel's last chunk
+    panel_end[p] = pos;
+  }
   return FSP_OK;
 }

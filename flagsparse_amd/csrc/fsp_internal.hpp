@@ -26,6 +26,7 @@ constexpr int64_t kXcsWinRowsCap = 2048;                 // rows of one combine 
 constexpr int64_t kXcsItemRunsCap = 64;                  // stored runs (windows) of one XCS item
 constexpr int64_t kPanelBytes = 131072;                  // x panel copied to LDS (panel SpMV)
 constexpr int64_t kPanelChunk = 512;                     // entries per wave chunk (panel SpMV)
+constexpr int64_t kPanelChunkRunsCap = 64;               // runs (rows) of one chunk, at most
 
 // Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).
 int fill_zero_f32(float* y, int64_t n, hipStream_t st);

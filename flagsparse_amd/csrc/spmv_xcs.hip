@@ -375,6 +375,14 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // A byte offset no buffer here reaches: a store there is dropped by the range check.
 constexpr unsigned kDropOffset = 0xFFFFFFF0u;
 
+// Orders the LDS accesses of one wave across its lanes (wavefront-scope fences around the
+// wave barrier): what a lane wrote before is visible to every lane after.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename A>
 __device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, unsigned off, A v) {
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -389,6 +397,7 @@ constexpr int kPanelPerLane = (int)kPanelChunk / kWave;
 // + a slot each).  Measured on MI355X, cfg3: 3, 4, 5 and 6 buffers within 0.2 us of each other.
 constexpr int kPanelBuffers = 3;
 static_assert(kPanelPerLane == 8, "eight entries per lane");
+static_assert(kPanelChunkRunsCap == kWave, "a chunk's runs are staged one per lane");
 
 constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
 
@@ -399,6 +408,8 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
     A* __restrict__ partials, int64_t n_partials) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
+  // Each wave's run sums of one chunk, in slot order, when the chunk has at most kWave runs.
+  __shared__ A s_stage[kPanelBlock / kWave][kWave];
   // The partial sums as a buffer resource of n_partials slots (< 2^32 bytes, checked by the
   // host): stores beyond it are dropped by the hardware.
   const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -411,8 +422,8 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
   const uint32_t cmask = (1u << col_bits) - 1u;
   const int c_hi = jobs[job + 1];
-  // The entries are streamed once with non-temporal loads, and the next chunk's loads are
-  // issued before the current chunk is reduced, so a wave keeps two chunks in flight.  The
+  // The entries are streamed once with non-temporal loads, and the next chunks' loads are
+  // issued before the current chunk is reduced, so a wave keeps chunks in flight.  The
   // chunk's first slot is loaded with its entries: loaded on its own after the next chunk's
   // loads, waiting for it (loads complete in order) also waited for the whole next chunk.
   auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], i32x4& c, int& slot0) {
@@ -472,23 +483,33 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     wave_seg_scan(h_in, v_in, c_in);
     const A carry = dpp_mov<kDppWaveShr1>(A(0), v_in);   // lane 0: 0
     const int slot = dpp_mov<kDppWaveShr1>(0, c_in);
-    // Emission: eight stores per lane, always issued - a lane without a run ending at q
-    // stores past the end of the buffer, which the buffer range check drops.  Under per-lane
-    // conditions the number of stores varied, and the compiler then waited for every
-    // outstanding memory operation (the prefetched chunks included) before each chunk.
-    // The lane's first run, when it continues from the lanes before (cont), adds the carry.
-    unsigned k = (unsigned)(slot0 + slot);
+    // The chunk's runs take slots slot0 .. slot0 + R - 1; the run ending at q in this lane is
+    // the lane's (j - slot)-th, j counting its ends.  The lane's first run, when it continues
+    // from the lanes before (cont), adds the carry.
+    const int n_runs = __builtin_amdgcn_readlane(c_in, kWave - 1);  // R, the same in all lanes
+    // The chunk's runs (at most kPanelChunkRunsCap = kWave, a layout rule) go to this wave's
+    // LDS row in slot order, and one store of 64 consecutive slots writes them in whole lines.
+    // Stored from the lanes where the runs end, eight stores per lane pieced the lines
+    // together: cfg3's panel kernel took 90 us that way, against 80 us with a single store.
+    // (Any store that only some paths issue also costs: the compiler then cannot count the
+    // memory operations in flight and waits for all of them, the prefetched chunks included.)
+    A* const st = s_stage[wid];
+    int j = slot;
     bool first = cont;
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
       const bool ends = q < kLast ? start[q + 1] : end_last;
-      store_partial(out_rsrc, ends ? k * (unsigned)sizeof(A) : kDropOffset,
-                    first ? carry + run[q] : run[q]);
+      if (ends && j < kWave) st[j] = first ? carry + run[q] : run[q];
       if (ends) {
-        ++k;
+        ++j;
         first = false;
       }
     }
+    wave_sync();  // the row is written and read by this wave only
+    const A staged = st[lane];
+    store_partial(out_rsrc, lane < n_runs ? (unsigned)(slot0 + lane) * (unsigned)sizeof(A)
+                                          : kDropOffset, staged);
+    wave_sync();  // read before the next chunk writes the row again
   };
 
   // kNB chunk buffers per wave: while one chunk is reduced, the next kNB - 1 are in flight

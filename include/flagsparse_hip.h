@@ -79,6 +79,7 @@ int64_t fsp_xcs_window_rows_cap(void);   /* max rows of one XCS combine window  
 int64_t fsp_xcs_item_runs_cap(void);     /* max stored runs (windows) of one XCS item */
 int64_t fsp_panel_bytes_cap(void);       /* max bytes of one x panel (panel SpMV)     */
 int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)            */
+int64_t fsp_panel_chunk_runs_cap(void);  /* runs (rows) per chunk, at most (panel SpMV) */
 
 /*
  * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
@@ -95,6 +96,19 @@ int fsp_plan_row_blocks(const int64_t* rowptr, int64_t n_rows, int64_t nnz_cap,
                         int64_t rows_cap, int64_t long_threshold, int64_t chunk,
                         int32_t* desc_out, int64_t* n_desc, int64_t* n_parts,
                         int64_t* n_split_rows);
+
+/*
+ * Chunk plan of the panel layout (fsp_spmv_panels), on the host: panel p's runs - the entries
+ * of one row inside the panel, run_len[r] >= 1 of them, r in [panel_runs[p], panel_runs[p+1])
+ * - are laid out one after the other from where panel p - 1 ended; a chunk of `chunk` entries
+ * closes when it is full or after the runs_cap-th run starting or continuing in it (its rest
+ * is then padding), and each panel ends on a chunk boundary.  Out: run_pos[r], the storage
+ * position of run r's first entry, and panel_end[p], the position after panel p.  No
+ * reference counterpart: it keeps every chunk within the run count fsp_spmv_panels stages
+ * (fsp_panel_chunk_runs_cap()); the reference has no panel layout.
+ */
+int fsp_plan_panel_chunks(const int64_t* panel_runs, int64_t n_panels, const int64_t* run_len,
+                          int64_t chunk, int64_t runs_cap, int64_t* run_pos, int64_t* panel_end);
 
 /*
  * The same plan built on the device in two passes (no host copy of rowptr, no host loop):
@@ -228,7 +242,8 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  *   jobs         n_jobs + 1 increasing chunk indices: workgroup j copies panel job_panel[j] of
  *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])
  *   chunk_slot   per chunk the first partial slot (8 bytes each); a chunk writes one slot per
- *                run it holds, in entry order
+ *                run it holds, in entry order, and holds at most fsp_panel_chunk_runs_cap()
+ *                runs (the sums of runs past that many are not written)
  *   n_partials   slots in partials (n_partials * 8 < 2^31: the kernel stores through a buffer
  *                resource of that size)
  *   rows, row_ptr, slots

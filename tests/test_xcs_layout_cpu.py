@@ -258,8 +258,11 @@ def _check_panels(layout, data, cols, rowptr):
     vals, pidx, start = _panel_logical(layout)
     e = np.arange(layout.n_entries)
     rows_all = pidx >> cb
-    # a run starts exactly where the row changes or a chunk opens
+    # a run starts exactly where the row changes or a chunk opens; no chunk holds more runs
+    # than the kernel stages
     assert np.array_equal(start, (e % chunk == 0) | np.r_[True, rows_all[1:] != rows_all[:-1]])
+    if layout.n_entries:
+        assert start.reshape(-1, chunk).sum(1).max() <= caps["panel_chunk_runs"]
     assert np.array_equal(np.sort(_spmv_layouts.panel_storage_positions(
         layout.n_entries, chunk, "cpu").numpy()), np.arange(layout.n_entries))  # a permutation
     got = []
@@ -474,3 +477,66 @@ def test_panel_partials_beyond_store_range(monkeypatch):
     monkeypatch.setattr(_spmv_layouts, "_INDEX_LIMIT_INT32", 8 * lay.n_partials - 1)
     with pytest.raises(ValueError):
         PanelLayout(vals, cols, ip, 200000, rows)
+
+
+def test_panel_chunk_plan_known_answers():
+    # chunk of 8 entries, at most 2 runs: the third run opens a new chunk (the rest of the
+    # first is padding); a run longer than a chunk continues across chunks and counts in each;
+    # every panel ends on a chunk boundary; an empty panel takes no room
+    plan = _spmv_layouts.plan_panel_chunks
+    pos, end = plan(torch.tensor([0, 3]), torch.tensor([3, 3, 3]), 8, 2)
+    assert pos.tolist() == [0, 3, 8] and end.tolist() == [16]
+    pos, end = plan(torch.tensor([0, 1, 1, 3]), torch.tensor([20, 5, 2]), 8, 2)
+    assert pos.tolist() == [0, 24, 29] and end.tolist() == [24, 24, 32]
+    # run 0 ends the chunk exactly, so run 1 opens a fresh one
+    pos, end = plan(torch.tensor([0, 2]), torch.tensor([8, 1]), 8, 1)
+    assert pos.tolist() == [0, 8] and end.tolist() == [16]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_panel_chunk_plan_properties(seed):
+    # random runs: runs in order, contiguous, never overlapping; each chunk within the entry
+    # and run caps; a chunk is cut short only when it holds the run cap (greedy)
+    rng = np.random.default_rng(seed)
+    chunk, cap = 16, 3
+    n_panels = 5
+    counts = rng.integers(0, 30, n_panels)
+    counts[2] = 0
+    lens = rng.integers(1, 40, int(counts.sum()))
+    short = rng.random(lens.size) < 0.5
+    lens[short] = rng.integers(1, 3, int(short.sum()))
+    pr = np.r_[0, np.cumsum(counts)]
+    pos, end = _spmv_layouts.plan_panel_chunks(torch.as_tensor(pr), torch.as_tensor(lens),
+                                                chunk, cap)
+    pos, end = pos.numpy(), end.numpy()
+    start = 0
+    for p in range(n_panels):
+        assert start % chunk == 0 and end[p] % chunk == 0
+        owner = np.full(end[p] - start, -1)
+        for r in range(pr[p], pr[p + 1]):
+            a = pos[r] - start
+            assert np.all(owner[a:a + lens[r]] == -1)
+            owner[a:a + lens[r]] = r
+        if pr[p + 1] > pr[p]:
+            assert pos[pr[p]] == start
+            assert np.all(np.diff(pos[pr[p]:pr[p + 1]]) >= lens[pr[p]:pr[p + 1] - 1])
+        for c in range(0, owner.size, chunk):
+            seg = owner[c:c + chunk]
+            runs = np.unique(seg[seg >= 0])
+            assert 1 <= runs.size <= cap
+            if (seg < 0).any() and c + chunk < owner.size:
+                assert runs.size == cap  # closed early only at the run cap
+        start = end[p]
+
+
+def test_panel_layout_short_runs():
+    # rows with one or two entries in each of many panels: chunks close at the run cap, and
+    # the sums still match the oracle
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(2, 120, 600)
+    vals, cols, ip, x = _case(lengths, 200000, 8)
+    rows = torch.arange(len(lengths))
+    lay = PanelLayout(vals, cols, ip, 200000, rows)
+    _check_panels(lay, vals, cols, ip)
+    y = _emulate_panels(lay, x.numpy(), np.full(len(lengths), np.nan))
+    np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)

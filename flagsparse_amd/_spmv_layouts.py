@@ -653,20 +653,33 @@ class PanelLayout:
                                                caps["panel_chunk_runs"])
         panel_start = torch.cat([panel_end.new_zeros(1), panel_end[:-1]])
         n_entries = int(panel_end[-1].item()) if n_panels else 0
-        run_of = torch.repeat_interleave(torch.arange(run_first.numel(), device=dev), run_len)
+        n_runs = int(run_first.numel())
+        run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), run_len)
         dest = run_pos[run_of] + (torch.arange(self.nnz, device=dev) - run_first[run_of])
-        del run_of, run_first, run_len, run_pos
+        del run_of
         vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
         vals[dest] = data[order]
-        # the row of every stored position: padding continues the entry before it (positions
-        # ascend with (panel, row), so a running maximum of that key fills the gaps)
-        key = torch.full((n_entries,), -1, dtype=torch.int64, device=dev)
-        key[dest] = panel * max(n_rows, 1) + row_s
-        if n_entries:
-            key = torch.cummax(key, 0)[0]
-        pidx = ((key % max(n_rows, 1)) << cb)
+        # padding continues the run before it: the gap after run r (up to the next run of its
+        # panel, or the panel's end) takes run r's row, value 0
+        run_panel = panel[run_first]
+        run_row = row_s[run_first]
+        nxt = panel_end[run_panel].clone()
+        if n_runs > 1:
+            same = run_panel[1:] == run_panel[:-1]
+            nxt[:-1] = torch.where(same, run_pos[1:], nxt[:-1])
+        run_end = run_pos + run_len
+        gap = nxt - run_end
+        pidx = torch.empty(n_entries, dtype=torch.int64, device=dev)
+        n_gap = int(gap.sum().item()) if n_runs else 0
+        if n_gap:
+            g_run = torch.repeat_interleave(torch.arange(n_runs, device=dev), gap)
+            g_first = torch.cumsum(gap, 0) - gap
+            g_pos = run_end[g_run] + (torch.arange(n_gap, device=dev) - g_first[g_run])
+            pidx[g_pos] = run_row[g_run] << cb
+            del g_run, g_first, g_pos
         pidx[dest] = (row_s << cb) | (c64[order] & ((1 << cb) - 1))
-        del order, row_s, c64, dest, key, panel
+        del order, row_s, c64, dest, panel, run_first, run_len, run_pos, run_panel, run_row
+        del nxt, run_end, gap
         self.n_entries = n_entries
         # one partial slot per (chunk, run): runs start at a chunk start or a row change
         n_chunks = n_entries // chunk

@@ -540,3 +540,22 @@ def test_panel_layout_short_runs():
     _check_panels(lay, vals, cols, ip)
     y = _emulate_panels(lay, x.numpy(), np.full(len(lengths), np.nan))
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
+
+
+def test_hybrid_falls_back_to_xcs(monkeypatch):
+    # a panel part that does not fit its packing (PanelLayout raises ValueError, as for too
+    # many partial sums) leaves the matrix to the XCS layout alone, not to row blocks
+    rng = np.random.default_rng(9)
+    lengths = np.concatenate([rng.zipf(2.0, 3000).clip(max=50), [30000] * 4])
+    vals, cols, ip, x = _case(lengths, 300000, 9)
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    assert _spmv_layouts.build_layout(vals, cols, ip, 300000).kind == "xcs-hybrid"
+
+    def refuse(*args, **kwargs):
+        raise ValueError("does not fit")
+
+    monkeypatch.setattr(_spmv_layouts.PanelLayout, "__init__", refuse)
+    lay = _spmv_layouts.build_layout(vals, cols, ip, 300000)
+    assert lay.kind == "xcs"
+    np.testing.assert_allclose(_emulate(lay, x.numpy()), oracle.spmv_csr(ip, cols, vals, x),
+                               rtol=1e-12, atol=1e-12)

@@ -23,7 +23,9 @@ roofline     the same bytes / the path's kernel time (all the kernels of one lau
              counts x (SpMV) or B (SpMM) once per entry instead of once, and
              ``frac_gather_inclusive`` is that count over the same time against the peak.
              ``gather_bound`` (cfg3, cfg5): the probe kernels timed in the same run on the
-             workload's own gather count and pattern - the rate the gathers alone reach
+             workload's own gather count and pattern - the rate the gathers alone reach;
+             ``kernel_ms_over_bound`` divides the whole path's kernel time by it, and for cfg3
+             ``part_ms_over_bound`` the XCS part's (its kernel and combine, ``parts_ms``)
 cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
              (a bounded row sample for SpMM), reported only, never a target
 cpu_reference_path
@@ -312,7 +314,7 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
     return {
         "step": lambda: fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y),
         "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
-        "parts": parts, "gather_bound": gather_bound,
+        "parts": parts, "gather_bound": gather_bound, "bound_part": "xcs_part",
         "bytes_gather_inclusive": nnz * (v + 4 + v) + (shape[0] + 1) * p_k + shape[0] * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
         "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), x, shape,
@@ -720,6 +722,10 @@ def _roofline(w, ms_kernel, kernel_runs, torch):
     if w.get("gather_bound"):
         gb = w["gather_bound"]()
         gb["kernel_ms_over_bound"] = round(ms_kernel / gb["ms"], 3)
+        if w.get("bound_part") and w["bound_part"] in out.get("parts_ms", {}):
+            # the part whose gathers the probe restates (its kernel and combine)
+            gb["part"] = w["bound_part"]
+            gb["part_ms_over_bound"] = round(out["parts_ms"][w["bound_part"]] / gb["ms"], 3)
         out["gather_bound"] = gb
     return out
 

@@ -1,6 +1,6 @@
 """Kernel-facing layouts of a CSR matrix for SpMV (CSR SpMV and COO row runs).
 
-Two layouts, chosen once per matrix at prepare time:
+The layouts below, chosen once per matrix at prepare time:
 
 ``RowBlockLayout`` (csrc/spmv.hip, ``spmv_rowblock_kernel``)
     The CSR arrays as given plus a descriptor table: short-row blocks of <= 1021 entries and
@@ -8,18 +8,19 @@ Two layouts, chosen once per matrix at prepare time:
     chunk order.  Right when the x entries a block gathers lie close together (banded,
     stencil, locally clustered columns) or x fits in one XCD's L2.
 
-``XcsLayout`` (csrc/spmv_xcs.hip, ``spmv_xcs_kernel``)
-    Columns split into eight panels of about equal nnz, one per XCD; entries regrouped by
-    (row tile, panel) so that every workgroup gathers from one panel only, and that panel is
-    resident in its XCD's L2.  Right when columns are spread over an x larger than an L2
-    (uniform random columns, power-law graphs).  Rows whose entries fall in several workgroups
-    are summed through partials in a fixed order (deterministic).
+``XcsLayout`` (csrc/spmv_xcs.hip, ``spmv_xcs_kernel``, ``xcs_window_combine_kernel``)
+    Columns split into panels of about equal nnz (P of them, P / 8 per XCD in turn, or shared
+    by two XCDs when P = 4); entries regrouped by (row tile, panel) so that every workgroup
+    gathers from one panel only, and that panel is resident in its XCD's L2.  Right when
+    columns are spread over an x larger than an L2 (uniform random columns, power-law graphs).
+    Each row's partial sums (one per workgroup holding entries of it) are added by a second
+    launch over windows of consecutive rows, in a fixed order (deterministic).
 
 ``PanelLayout`` (csrc/spmv_xcs.hip, ``spmv_panel_kernel``)
     The long rows of a power-law matrix: x cut into panels of 128 KiB, the rows' entries ordered
     by (panel, row); a workgroup copies one panel into LDS and its waves gather from there, so
     these gathers run at LDS speed instead of the L2 request rate.  One partial per (row,
-    chunk of 512 entries), added per row in a fixed order.
+    chunk of 512 entries; a chunk holds at most 64 rows), added per row in a fixed order.
 
 ``XcsHybridLayout``
     ``PanelLayout`` for the rows long enough to put several entries in every panel,

@@ -408,7 +408,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
     A* __restrict__ partials, int64_t n_partials) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
-  // Each wave's run sums of one chunk, in slot order, when the chunk has at most kWave runs.
+  // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule).
   __shared__ A s_stage[kPanelBlock / kWave][kWave];
   // The partial sums as a buffer resource of n_partials slots (< 2^32 bytes, checked by the
   // host): stores beyond it are dropped by the hardware.

@@ -160,6 +160,27 @@ def test_planner_rejects_bad_arguments():
     assert rc == -1
 
 
+def test_panel_chunk_planner_rejects_bad_arguments():
+    L = _abi.lib()
+    pr = np.array([0, 2], dtype=np.int64)
+    pos = np.zeros(2, dtype=np.int64)
+    end = np.zeros(1, dtype=np.int64)
+
+    def plan(run_len, panel_runs=pr, chunk=8, cap=2, n_panels=1):
+        rl = np.asarray(run_len, dtype=np.int64)
+        return L.fsp_plan_panel_chunks(panel_runs.ctypes.data, n_panels, rl.ctypes.data, chunk,
+                                       cap, pos.ctypes.data, end.ctypes.data)
+
+    assert plan([3, 4]) == 0 and pos.tolist() == [0, 3] and end.tolist() == [8]
+    assert plan([3, 0]) == -1 and b"empty run" in L.fsp_last_error()
+    assert plan([3, 4], chunk=0) == -1
+    assert plan([3, 4], cap=0) == -1
+    assert plan([3, 4], panel_runs=np.array([1, 2], dtype=np.int64)) == -1
+    assert plan([3, 4], panel_runs=np.array([0, 2, 1], dtype=np.int64), n_panels=2) == -1
+    assert L.fsp_plan_panel_chunks(None, 1, None, 8, 2, None, None) == -1  # null pointers
+    assert L.fsp_plan_panel_chunks(None, 0, None, 8, 2, None, None) == 0   # nothing to plan
+
+
 def test_device_planner_rejects_bad_arguments():
     L = _abi.lib()
     # (rowptr, bits, n_rows, window_rows, nnz_cap, rows_cap, long_threshold, chunk, counts,

@@ -353,8 +353,16 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   for (int m = 0; m < kRowsPer; ++m) {
     const int i = tid + m * kBlock;
     if (i < nr) {
+      // four sums requested at a time, added in order
       A acc = A(0);
-      for (int k = rs[m]; k < re[m]; ++k) acc += s_val[k];
+      for (int k = rs[m]; k < re[m]; k += 4) {
+        A t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = k + u < re[m] ? s_val[k + u] : A(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (k + u < re[m]) acc += t[u];
+      }
       const int row = row0 + i;
       y[row_map ? row_map[row] : row] = T(acc);
     }

@@ -349,22 +349,31 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   }
   __syncthreads();
 
+  // The first two sums of all the thread's rows are requested together (most rows have at
+  // most two); longer rows then take four at a time.  Added in order in every case.
+  A acc[kRowsPer];
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    const A t0 = rs[m] < re[m] ? s_val[rs[m]] : A(0);
+    const A t1 = rs[m] + 1 < re[m] ? s_val[rs[m] + 1] : A(0);
+    acc[m] = A(0);
+    if (rs[m] < re[m]) acc[m] += t0;
+    if (rs[m] + 1 < re[m]) acc[m] += t1;
+  }
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
     const int i = tid + m * kBlock;
     if (i < nr) {
-      // four sums requested at a time, added in order
-      A acc = A(0);
-      for (int k = rs[m]; k < re[m]; k += 4) {
+      for (int k = rs[m] + 2; k < re[m]; k += 4) {
         A t[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) t[u] = k + u < re[m] ? s_val[k + u] : A(0);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-          if (k + u < re[m]) acc += t[u];
+          if (k + u < re[m]) acc[m] += t[u];
       }
       const int row = row0 + i;
-      y[row_map ? row_map[row] : row] = T(acc);
+      y[row_map ? row_map[row] : row] = T(acc[m]);
     }
   }
 }

@@ -768,9 +768,11 @@ class PanelLayout:
 class XcsHybridLayout:
     """Long rows in a PanelLayout, the rest in an XcsLayout (module docstring).  The XCS part
     sees the long rows as rows without entries and writes them as 0; the panel part, launched
-    after it on the same stream, then writes their sums.  Run concurrently on two streams the
-    parts were slower on MI355X (cfg3 510 us vs 465 us): the panel part's entry stream evicts
-    the x panels the XCS part keeps in L2."""
+    after it on the same stream, then writes their sums.  Measured on MI355X (cfg3, 281 us in
+    this order): the panel kernel on a second stream beside the XCS kernel 277.5 us (a CU that
+    holds a panel workgroup, 128 KiB of LDS and 16 waves, has room for one XCS workgroup, so
+    the two mostly take turns), the two combines side by side 282.5 us, the panel kernel beside
+    the XCS combine 292 us (two HBM streams); not worth a second stream per call."""
 
     kind = "xcs-hybrid"
 

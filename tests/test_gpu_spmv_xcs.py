@@ -187,3 +187,33 @@ def test_combine_unaligned_windows(dev, monkeypatch, dtype):
     for use_opt in (False, True):
         y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
         _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))
+
+
+@pytest.mark.parametrize("layout", ["rowblock", "xcs-l2", "xcs-hybrid"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_unaligned_x_and_out(dev, monkeypatch, layout, dtype):
+    # x and out as views one element into their buffers (not 16-byte aligned): the panel
+    # kernel then copies its x panels element by element, and the result goes through a
+    # temporary into out, which is what the call returns
+    monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    lengths = [40, 0, 3, 100, 1] * 600
+    n_cols = 70001  # the last panel narrower than the others
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 29, dtype)
+    print(f"unaligned x/out {layout} {dtype}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    assert p._kernel(False).kind == {"xcs-l2": "xcs"}.get(layout, layout)
+    x_buf = torch.zeros(n_cols + 1, dtype=dtype, device=dev)
+    x_buf[1:] = x.to(dev)
+    x_view = x_buf[1:]
+    assert x_view.data_ptr() % 16 != 0
+    out_buf = torch.full((shape[0] + 1,), float("nan"), dtype=dtype, device=dev)
+    out = out_buf[1:]
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(x=x_view, prepared=p, out=out, use_opt=use_opt)
+        assert y is out
+        _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))
+        assert torch.isnan(out_buf[0])
+        # the same as with aligned x and no out, bit for bit
+        assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt))

@@ -1,0 +1,99 @@
+"""Seeded fuzz of the SpMV layouts on the GPU: random shapes and row-length mixes (power law,
+uniform, mostly empty, one huge row among empty ones), each forced through the row-block, XCS
+and XCS + panel layouts, CSR and COO, both accumulation modes, against the fp64 oracle.
+
+Bars as in test_gpu_spmv_csr.py: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
+allclose ratio, and for the default float32 path at most 1 ulp from float32(fp64 oracle).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import flagsparse_amd as fs
+from flagsparse_amd import _spmv_layouts, synthetic
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+# (row-length mix, number of columns) per seed
+CASES = (("zipf", 70001), ("uniform", 1 << 20), ("sparse", 1000), ("one_huge", 3_000_000),
+         ("zipf_heavy", 1 << 20), ("uniform", 7), ("zipf", 3_000_000), ("sparse", 70001),
+         ("one_huge", 70001), ("zipf_heavy", 5000), ("uniform", 70001), ("zipf", 1000))
+
+
+def _lengths(rng, kind, n_rows, n_cols):
+    if kind == "zipf":
+        lengths = rng.zipf(1.7, n_rows)
+    elif kind == "zipf_heavy":
+        lengths = rng.zipf(1.3, n_rows)
+    elif kind == "uniform":
+        lengths = rng.integers(0, 40, n_rows)
+    elif kind == "sparse":  # nine rows in ten empty
+        lengths = (rng.random(n_rows) < 0.1) * rng.integers(1, 6, n_rows)
+    else:  # one_huge: a single long row among empty ones
+        lengths = np.zeros(n_rows, dtype=np.int64)
+        lengths[int(rng.integers(0, n_rows))] = int(rng.integers(1, 150000))
+    # distinct columns per row: at most half the columns of a wide matrix (drawing nearly all
+    # of them takes long), all of them for a narrow one
+    cap = n_cols if n_cols <= 64 else n_cols // 2
+    lengths = np.minimum(lengths, min(cap, 150000)).astype(np.int64)
+    total = int(lengths.sum())
+    if total > 2_000_000:  # a few seconds of oracle and setup per case
+        lengths = (lengths * (2_000_000 / total)).astype(np.int64)
+    return lengths
+
+
+def _matrix(seed):
+    rng = np.random.default_rng(1000 + seed)
+    kind, n_cols = CASES[seed]
+    n_rows = int(rng.integers(1, 30000))
+    dtype = (torch.float32, torch.float64)[seed % 2]
+    lengths = _lengths(rng, kind, n_rows, n_cols)
+    keys = synthetic._distinct_sorted_columns(torch.as_tensor(lengths), n_cols, seed, 1)
+    ptr, cols = synthetic._csr_from_keys(keys, n_rows, n_cols)
+    vals = synthetic.uniform_values(seed, 2, cols.numel(), dtype, "cpu")
+    x = synthetic.uniform_values(seed, 3, n_cols, dtype, "cpu")
+    return kind, rng, vals, cols, ptr, x, (n_rows, n_cols)
+
+
+def _check(y, ref64, exact_fp32):
+    name = "float64" if y.dtype == torch.float64 else "float32"
+    err = oracle.rel_l2(y, ref64)
+    assert err <= oracle.REL_L2_BOUND[name], f"rel_l2 {err:.3e}"
+    atol, rtol = oracle.REF_SCRIPT_TOL[name]
+    assert oracle.allclose_ratio(y, ref64, atol, rtol) <= 1.0
+    if exact_fp32:
+        def ordered(v):
+            i = np.ascontiguousarray(v, dtype=np.float32).view(np.int32).astype(np.int64)
+            return np.where(i < 0, -(i & 0x7FFFFFFF), i)
+        u = np.abs(ordered(y.cpu().numpy()) - ordered(ref64.astype(np.float32)))
+        assert u.size == 0 or u.max() <= 1, u.max()
+
+
+@pytest.mark.parametrize("seed", range(len(CASES)))
+@pytest.mark.parametrize("layout", ["rowblock", "xcs-l2", "xcs-hybrid"])
+def test_fuzz_spmv(dev, monkeypatch, seed, layout):
+    kind, rng, vals, cols, ptr, x, shape = _matrix(seed)
+    monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", int(rng.integers(2, 64)))
+    print(f"fuzz seed={seed} {kind} {layout} shape={shape} nnz={vals.numel()} {vals.dtype}",
+          flush=True)
+    ref = oracle.spmv_csr(ptr, cols, vals, x)
+    d, c, p, xd = vals.to(dev), cols.to(torch.int32).to(dev), ptr.to(dev), x.to(dev)
+    prepared = fs.prepare_spmv_csr(d, c, p, shape)
+    built = prepared._kernel(False).kind
+    print(f"  layout built: {built}", flush=True)
+    # the forced layout is the one tested (the hybrid needs a row of FORCE_PANEL_ROW_MIN entries)
+    has_long = bool(((ptr[1:] - ptr[:-1]) >= _spmv_layouts.FORCE_PANEL_ROW_MIN).any())
+    expect = {"rowblock": "rowblock", "xcs-l2": "xcs",
+              "xcs-hybrid": "xcs-hybrid" if has_long else "xcs"}[layout]
+    assert built == expect
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(x=xd, prepared=prepared, use_opt=use_opt)
+        _check(y, ref, exact_fp32=(vals.dtype == torch.float32 and not use_opt))
+        # a second call reuses the layout's workspaces: the same result, bit for bit
+        assert torch.equal(y, fs.flagsparse_spmv_csr(x=xd, prepared=prepared, use_opt=use_opt))
+    rows = torch.repeat_interleave(torch.arange(shape[0]), ptr[1:] - ptr[:-1])
+    y = fs.flagsparse_spmv_coo(d, rows.to(dev), c, xd, shape)
+    _check(y, oracle.spmv_coo(rows, cols, vals, x, shape[0]), exact_fp32=False)

@@ -1,9 +1,11 @@
-"""Seeded fuzz of the SpMV layouts on the GPU: random shapes and row-length mixes (power law,
-uniform, mostly empty, one huge row among empty ones), each forced through the row-block, XCS
-and XCS + panel layouts, CSR and COO, both accumulation modes, against the fp64 oracle.
+"""Seeded fuzz on the GPU: random shapes and row-length mixes (power law, uniform, mostly
+empty, one huge row among empty ones).  SpMV is forced through the row-block, XCS and XCS +
+panel layouts, CSR and COO, both accumulation modes; the same matrices then go through CSR SpMM
+(base and opt, row- and column-major B), COO SpMM and SDDMM with a dense width drawn per case.
+All against the fp64 oracle.
 
 Bars as in test_gpu_spmv_csr.py: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
-allclose ratio, and for the default float32 path at most 1 ulp from float32(fp64 oracle).
+allclose ratio, and for the default float32 SpMV path at most 1 ulp from float32(fp64 oracle).
 """
 
 import numpy as np
@@ -97,3 +99,39 @@ def test_fuzz_spmv(dev, monkeypatch, seed, layout):
     rows = torch.repeat_interleave(torch.arange(shape[0]), ptr[1:] - ptr[:-1])
     y = fs.flagsparse_spmv_coo(d, rows.to(dev), c, xd, shape)
     _check(y, oracle.spmv_coo(rows, cols, vals, x, shape[0]), exact_fp32=False)
+
+
+def _check_dense(out, ref64):
+    name = "float64" if out.dtype == torch.float64 else "float32"
+    if ref64.size == 0:
+        return
+    err = oracle.rel_l2(out, ref64)
+    assert err <= oracle.REL_L2_BOUND[name], f"rel_l2 {err:.3e}"
+    atol, rtol = oracle.REF_SCRIPT_TOL[name]
+    assert oracle.allclose_ratio(out, ref64, atol, rtol) <= 1.0
+
+
+@pytest.mark.parametrize("seed", range(len(CASES)))
+def test_fuzz_spmm_sddmm(dev, seed):
+    # the same matrices with a dense operand of random width: CSR SpMM (base and opt), COO SpMM,
+    # a column-major B, and SDDMM with K = N
+    kind, rng, vals, cols, ptr, x, shape = _matrix(seed)
+    n_rows, n_cols = shape
+    N = int(rng.choice([1, 2, 3, 5, 16, 17, 64, 100]))
+    N = max(1, min(N, 20_000_000 // max(n_rows, n_cols)))  # B and C within 20M values
+    dtype = vals.dtype
+    print(f"fuzz spmm seed={seed} {kind} shape={shape} nnz={vals.numel()} N={N} {dtype}",
+          flush=True)
+    B = synthetic.uniform_values(seed, 4, n_cols * N, dtype, "cpu").reshape(n_cols, N)
+    ref = oracle.spmm_csr(ptr, cols, vals, B)
+    d, c, p, Bd = vals.to(dev), cols.to(torch.int32).to(dev), ptr.to(dev), B.to(dev)
+    _check_dense(fs.flagsparse_spmm_csr(d, c, p, Bd, shape), ref)
+    _check_dense(fs.flagsparse_spmm_csr_opt(d, c, p, Bd, shape), ref)
+    _check_dense(fs.flagsparse_spmm_csr(d, c, p, Bd.t().contiguous().t(), shape), ref)
+    rows = torch.repeat_interleave(torch.arange(n_rows), ptr[1:] - ptr[:-1])
+    _check_dense(fs.flagsparse_spmm_coo(d, rows.to(dev), c, Bd, shape),
+                 oracle.spmm_coo(rows, cols, vals, B, n_rows))
+    xs = synthetic.uniform_values(seed, 5, n_rows * N, dtype, "cpu").reshape(n_rows, N)
+    out = fs.flagsparse_sddmm_csr(data=d, indices=c, indptr=p, x=xs.to(dev), y=Bd, shape=shape,
+                                  alpha=0.5, beta=2.0)
+    _check_dense(out, oracle.sddmm_csr(ptr, cols, xs, B, vals, alpha=0.5, beta=2.0))

@@ -679,6 +679,8 @@ class PanelLayout:
             pidx[g_pos] = run_row[g_run] << cb
             del g_run, g_first, g_pos
         pidx[dest] = (row_s << cb) | (c64[order] & ((1 << cb) - 1))
+        real = torch.zeros(n_entries, dtype=torch.bool, device=dev)
+        real[dest] = True
         del order, row_s, c64, dest, panel, run_first, run_len, run_pos, run_panel, run_row
         del nxt, run_end, gap
         self.n_entries = n_entries
@@ -692,7 +694,18 @@ class PanelLayout:
         if n_chunks and int(runs.max().item()) > caps["panel_chunk_runs"]:
             raise AssertionError("panel chunk plan: a chunk holds more runs than the kernel "
                                  "stages")
-        self.chunk_slot = (torch.cumsum(runs, 0) - runs).to(torch.int32).contiguous()
+        # per chunk {first slot, entries in use}: the padding (a chunk closed early, or a
+        # panel's last chunk) is the chunk's tail, whose products the kernel takes as 0
+        used = real.view(n_chunks, chunk).sum(1)
+        if n_entries > 1:  # no entry in use after a padding entry of the same chunk
+            gap_then_use = ~real[:-1] & real[1:]
+            gap_then_use[chunk - 1::chunk] = False
+            if bool(gap_then_use.any()):
+                raise AssertionError("panel chunk plan: padding inside a chunk")
+            del gap_then_use
+        del real
+        self.chunk_info = torch.stack([torch.cumsum(runs, 0) - runs, used], 1) \
+            .to(torch.int32).contiguous()
         slot_row = rowpos[starts]
         self.n_partials = int(slot_row.numel())
         if self.n_partials * 8 > _INDEX_LIMIT_INT32:
@@ -736,7 +749,7 @@ class PanelLayout:
 
     def held_bytes(self, caller=()):
         """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
-        return tensor_bytes(self.vals, self.pcol, self.rows, self.chunk_slot, self.slots,
+        return tensor_bytes(self.vals, self.pcol, self.rows, self.chunk_info, self.slots,
                             self.row_ptr, self.jobs, self.job_panel, self.partials)
 
     def describe(self):
@@ -751,7 +764,7 @@ class PanelLayout:
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pcol),
                     self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
-                    p(self.job_panel), self.n_jobs, p(self.chunk_slot), p(self.partials),
+                    p(self.job_panel), self.n_jobs, p(self.chunk_info), p(self.partials),
                     int(self.partials.numel()), p(self.rows), p(self.row_ptr), p(self.slots),
                     self.n_rows, None]
             self._args[bool(acc_f64)] = args
@@ -759,7 +772,7 @@ class PanelLayout:
         a[6], a[8] = x.data_ptr(), y.data_ptr()
         a[9] = None if row_map is None else row_map.data_ptr()
         a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pcol, self.jobs,
-                                              self.job_panel, self.chunk_slot, self.rows,
+                                              self.job_panel, self.chunk_info, self.rows,
                                               self.row_ptr, self.slots))
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y

@@ -11,6 +11,7 @@ constexpr int kBlock = 256;               // threads per workgroup (4 waves)
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef double f64x2 __attribute__((ext_vector_type(2)));

@@ -40,8 +40,10 @@
 //            Values: inside a chunk, logical quad 2L + h (lane L's h-th quad) is stored at
 //            quad h * 64 + L, so each 16-byte load of a wave reads one contiguous kilobyte;
 //            pcol in logical order (lane L's 8 entries are the 16 bytes at 16 L)
-//   chunks   kPanelChunk consecutive entries, one wave's unit of work; chunk_slot[c] is the
-//            first partial slot of chunk c, which has one slot per run (row) it holds
+//   chunks   kPanelChunk consecutive entries, one wave's unit of work; chunk_info[c] = {the
+//            first partial slot of chunk c, which has one slot per run (row) it holds; the
+//            number of its entries in use - a chunk closed early, and each panel's last one,
+//            end in padding}
 //   jobs     workgroup j copies panel job_panel[j] into LDS and its waves take the chunks
 //            [jobs[j], jobs[j+1]) in turn; no barrier after the copy
 // Each long row's slots are then added by panel_combine_kernel (one wave per row, fixed order).
@@ -381,7 +383,9 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
 // Panel layout (see the file comment): one workgroup per job, waves independent after the
 // panel copy.  A wave's chunk: lane L holds entries [8L, 8L + 8), their rows non-decreasing;
 // the runs that end in a lane are emitted by it, the first one with the carry from the lanes
-// before (a segmented wave scan), into consecutive slots from chunk_slot[c] in entry order.
+// before (a segmented wave scan), into consecutive slots from chunk_info[c].x in entry order;
+// the chunk's entries past its first chunk_info[c].y are padding and add exactly 0 (a product
+// 0 * x would be NaN where x holds an infinity or a NaN).
 // One workgroup of 16 waves per CU, holding a 128 KiB panel (measured on MI355X, cfg3 whole
 // path: 0.315 ms with 64 KiB panels and 2 workgroups of 512 per CU, 0.290 ms with 128 KiB
 // panels and 1024 threads, 0.300 ms with 128 KiB and 512 threads; the wider panels also
@@ -422,7 +426,7 @@ template <typename T, typename A>
 __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const T* __restrict__ vals, const uint16_t* __restrict__ pcol, int col_bits,
     const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
-    const int* __restrict__ job_panel, const int* __restrict__ chunk_slot,
+    const int* __restrict__ job_panel, const i32x2* __restrict__ chunk_info,
     A* __restrict__ partials, int64_t n_partials) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
   // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule).
@@ -443,7 +447,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   // issued before the current chunk is reduced, so a wave keeps chunks in flight.  The
   // chunk's first slot is loaded with its entries: loaded on its own after the next chunk's
   // loads, waiting for it (loads complete in order) also waited for the whole next chunk.
-  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], i32x4& c, int& slot0) {
+  auto load_chunk = [&](int chunk, T (&v)[kPanelPerLane], i32x4& c, i32x2& info) {
     const int64_t e0 = (int64_t)chunk * kPanelChunk;
 #pragma unroll
     for (int h = 0; h < kPanelPerLane / 4; ++h) {
@@ -458,21 +462,35 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       }
     }
     c = ld_stream<true>(reinterpret_cast<const i32x4*>(pcol + e0) + lane);
-    slot0 = chunk_slot[chunk];
+    info = chunk_info[chunk];
   };
   // One chunk's reduction: products from the LDS panel, then the runs (rows) that end in each
   // lane are emitted, the first one with the carry from the lanes before (a segmented wave
-  // scan), into consecutive slots from the chunk's first.
-  auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const i32x4& cq, int slot0) {
+  // scan), into consecutive slots from the chunk's first (info.x); entries from info.y on are
+  // padding, whose products are 0 whatever x holds.
+  auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const i32x4& cq, const i32x2& info) {
+    const int slot0 = info.x, used = info.y;
     A prod[kPanelPerLane];
     bool start[kPanelPerLane];
+    T xg[kPanelPerLane];
     const uint32_t cw[4] = {(uint32_t)cq.x, (uint32_t)cq.y, (uint32_t)cq.z, (uint32_t)cq.w};
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
       const uint32_t e = (q & 1) ? cw[q >> 1] >> 16 : cw[q >> 1] & 0xffffu;
-      prod[q] = A(v[q]) * A(sx[e & cmask]);
+      xg[q] = sx[e & cmask];
       start[q] = (e & kRunStart) != 0;
     }
+    // Padding (value 0) takes x = 0 too, so that it adds exactly 0 whatever x holds.  Only a
+    // panel's last chunk and a chunk closed early have any (the same in all lanes), so the
+    // others skip this; with a select on every product the kernel took 1.8 us longer (cfg3).
+    if (used < (int)kPanelChunk) {
+      const int lim = used - kPanelPerLane * lane;
+#pragma unroll
+      for (int q = 0; q < kPanelPerLane; ++q)
+        if (q >= lim) xg[q] = T(0);
+    }
+#pragma unroll
+    for (int q = 0; q < kPanelPerLane; ++q) prod[q] = A(v[q]) * A(xg[q]);
     constexpr int kLast = kPanelPerLane - 1;
     // a chunk starts a run whatever its first entry says, and ends one (lane 63 reads 1)
     const bool cont = lane > 0 && !start[0];
@@ -536,11 +554,11 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   constexpr int kNB = kPanelBuffers;
   T v[kNB][kPanelPerLane];
   i32x4 c[kNB];
-  int sl[kNB];
+  i32x2 sl[kNB];
 #pragma unroll
   for (int b = 0; b < kNB; ++b) {
     c[b] = i32x4{0, 0, 0, 0};
-    sl[b] = 0;
+    sl[b] = i32x2{0, 0};
   }
   int ch = jobs[job] + wid;
   // The first chunks' entries are requested before the panel copy, so the two overlap.
@@ -650,7 +668,7 @@ __global__ __launch_bounds__(kBlock) void panel_combine_kernel(
 template <typename T, typename A>
 int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const void* x,
                   int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
-                  const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_slot,
+                  const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_info,
                   void* partials, int64_t n_partials, const int32_t* rows,
                   const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
                   hipStream_t st) {
@@ -658,7 +676,8 @@ int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const vo
     hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
                        ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
                        pcol, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
-                       chunk_slot, static_cast<A*>(partials), n_partials);
+                       reinterpret_cast<const i32x2*>(chunk_info), static_cast<A*>(partials),
+                       n_partials);
     int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
     if (rc) return rc;
   }
@@ -723,7 +742,7 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
                                int64_t n_entries, int col_bits, const void* x, int64_t x_len,
                                void* y, const int32_t* row_map, const int32_t* jobs,
                                const int32_t* job_panel, int64_t n_jobs,
-                               const int32_t* chunk_slot, void* partials, int64_t n_partials,
+                               const int32_t* chunk_info, void* partials, int64_t n_partials,
                                const int32_t* rows, const int32_t* row_ptr,
                                const int32_t* slots, int64_t n_rows, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
@@ -741,8 +760,10 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
     return set_error(FSP_EINVAL, "fsp_spmv_panels: col_bits must be <= 15 and a panel of "
                                  "2^col_bits values must fit " +
                                      std::to_string(kPanelBytes) + " bytes of LDS");
-  if (n_jobs > 0 && (!vals || !pcol || !x || !jobs || !job_panel || !chunk_slot || !partials))
+  if (n_jobs > 0 && (!vals || !pcol || !x || !jobs || !job_panel || !chunk_info || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null pointer");
+  if ((reinterpret_cast<uintptr_t>(chunk_info) & 7u) != 0)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: chunk_info must be 8-byte aligned");
   if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null row pointer");
   if (!aligned16(vals) || !aligned16(pcol))
@@ -752,13 +773,13 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
   if (dtype == FSP_F32) {
     if (acc_f64)
       return launch_panels<float, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                          job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                          job_panel, n_jobs, chunk_info, partials, n_partials, rows,
                                           row_ptr, slots, n_rows, st);
     return launch_panels<float, float>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                       job_panel, n_jobs, chunk_info, partials, n_partials, rows,
                                        row_ptr, slots, n_rows, st);
   }
   return launch_panels<double, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_slot, partials, n_partials, rows,
+                                       job_panel, n_jobs, chunk_info, partials, n_partials, rows,
                                        row_ptr, slots, n_rows, st);
 }

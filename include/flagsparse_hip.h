@@ -233,7 +233,7 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  * beside fsp_spmv_xcs for power-law matrices, whose long rows put many entries in every panel.
  *   vals, pcol   n_entries entries (a multiple of fsp_panel_chunk(), both 16-byte aligned)
  *                in (panel, row) order, each panel's run padded with val 0 entries of its
- *                last row.  pcol (16 bits) = column - panel * 2^col_bits, | 0x8000 when the
+ *                last row (padding only at the end of a chunk).  pcol (16 bits) = column - panel * 2^col_bits, | 0x8000 when the
  *                entry starts a run: its row differs from the previous entry's (the first
  *                entry of a chunk always starts one).  vals: inside each chunk the quad (4
  *                entries) at logical position 2L + h is stored at quad position 64h + L
@@ -241,9 +241,11 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
  *   col_bits     <= 15, and 2^col_bits values must fit fsp_panel_bytes_cap() bytes
  *   jobs         n_jobs + 1 increasing chunk indices: workgroup j copies panel job_panel[j] of
  *                x (x_len values in all) into LDS and runs chunks [jobs[j], jobs[j+1])
- *   chunk_slot   per chunk the first partial slot (8 bytes each); a chunk writes one slot per
- *                run it holds, in entry order, and holds at most fsp_panel_chunk_runs_cap()
- *                runs (the sums of runs past that many are not written)
+ *   chunk_info   per chunk two int32 (8-byte aligned): its first partial slot (8 bytes each)
+ *                and the number of its entries in use, the rest being padding that adds
+ *                exactly 0 whatever x holds; a chunk writes one slot per run it holds, in
+ *                entry order, and holds at most fsp_panel_chunk_runs_cap() runs (the sums of
+ *                runs past that many are not written)
  *   n_partials   slots in partials (n_partials * 8 < 2^31: the kernel stores through a buffer
  *                resource of that size)
  *   rows, row_ptr, slots
@@ -255,7 +257,7 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
 int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pcol,
                     int64_t n_entries, int col_bits, const void* x, int64_t x_len, void* y,
                     const int32_t* row_map, const int32_t* jobs, const int32_t* job_panel,
-                    int64_t n_jobs, const int32_t* chunk_slot, void* partials,
+                    int64_t n_jobs, const int32_t* chunk_info, void* partials,
                     int64_t n_partials, const int32_t* rows, const int32_t* row_ptr,
                     const int32_t* slots, int64_t n_rows, void* stream);
 

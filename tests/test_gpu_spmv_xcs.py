@@ -217,3 +217,44 @@ def test_unaligned_x_and_out(dev, monkeypatch, layout, dtype):
         assert torch.isnan(out_buf[0])
         # the same as with aligned x and no out, bit for bit
         assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt))
+
+
+@pytest.mark.parametrize("bad", [float("inf"), float("nan")])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype):
+    # x infinite or NaN in every panel's first column: the panel layout's padding entries point
+    # there with value 0 and must add exactly 0 (0 * inf would be NaN).  Without entries in
+    # those columns every row is finite; with them, the rows holding one are inf / NaN exactly
+    # as in the oracle (inf or NaN of a row does not depend on the summation order).
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    rng = np.random.default_rng(17)
+    lengths = np.concatenate([rng.integers(0, 30, 4000), rng.integers(32, 3000, 400)])
+    rng.shuffle(lengths)
+    n_cols = 300001
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 31, dtype)
+    cb = _spmv_layouts._panel_col_bits(n_cols, data.element_size())
+    x[::1 << cb] = bad
+    print(f"non-finite x at panel bases {bad} {dtype}", flush=True)
+    keep = (idx & ((1 << cb) - 1)) != 0
+    row = torch.repeat_interleave(torch.arange(len(lengths)), ptr[1:] - ptr[:-1])
+    for drop in (True, False):
+        if drop:
+            d, i = data[keep], idx[keep]
+            p = torch.zeros_like(ptr)
+            p[1:] = torch.cumsum(torch.bincount(row[keep], minlength=len(lengths)), 0)
+        else:
+            d, i, p = data, idx, ptr
+        prep = fs.prepare_spmv_csr(d.to(dev), i.to(torch.int32).to(dev), p.to(dev), shape)
+        lay = prep._kernel(False)
+        assert lay.kind == "xcs-hybrid"
+        assert int(lay.long.chunk_info[:, 1].min()) < 512  # padding present
+        ref = oracle.spmv_csr(p, i, d, x)
+        for use_opt in (False, True):
+            y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=prep, use_opt=use_opt).cpu().numpy()
+            fin = np.isfinite(ref)
+            assert drop == bool(fin.all())
+            assert np.array_equal(np.isnan(y), np.isnan(ref))
+            assert np.array_equal(y[np.isinf(ref)], ref[np.isinf(ref)].astype(y.dtype))
+            name = "float64" if dtype == torch.float64 else "float32"
+            assert oracle.rel_l2(torch.as_tensor(y[fin]), ref[fin]) <= oracle.REL_L2_BOUND[name]

@@ -176,14 +176,16 @@ def _check_structure(layout, data, cols, rowptr):
 def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
     """numpy restatement of spmv_panel_kernel + the combine over a PanelLayout: each chunk's
     runs (a chunk start or an entry marked as a run start opens one) go to consecutive slots
-    from chunk_slot[c]; row i of the layout then gets its slots' sum in slot order."""
+    from chunk_info[c, 0], its entries from chunk_info[c, 1] on (padding) adding 0; row i of the
+    layout then gets its slots' sum in slot order."""
     chunk = _abi.caps()["panel_chunk"]
     cb = layout.col_bits
     vals, pidx, start = _panel_logical(layout)
     vals = vals.astype(acc)
     jobs = layout.jobs.numpy()
     jp = layout.job_panel.numpy()
-    cslot = layout.chunk_slot.numpy()
+    info = layout.chunk_info.numpy()
+    cslot = info[:, 0]
     partials = np.full(max(layout.n_partials, 1), np.nan)
     for j in range(layout.n_jobs):
         base = int(jp[j]) << cb
@@ -191,8 +193,11 @@ def _emulate_panels(layout, x, y, row_map=None, acc=np.float64):
             sl = int(cslot[c])
             e = np.arange(c * chunk, (c + 1) * chunk)
             cols = base + (pidx[e] & ((1 << cb) - 1))
-            prod = vals[e] * x[np.minimum(cols, x.size - 1)].astype(acc)
-            assert np.all(cols[vals[e] != 0] < x.size)
+            in_use = np.arange(chunk) < info[c, 1]
+            with np.errstate(invalid="ignore"):
+                prod = np.where(in_use, vals[e] * x[np.minimum(cols, x.size - 1)].astype(acc),
+                                acc(0))
+            assert np.all(cols[in_use] < x.size)
             s = acc(0)
             for q in range(chunk):
                 if q > 0 and start[e[q]]:
@@ -217,7 +222,7 @@ def _panel_logical(layout):
     """(vals, pidx = row << col_bits | column in the panel, run-start flags) of a PanelLayout
     in logical order.  Values: inside a chunk of 512, lane L's quad h (logical quad 2L + h) is
     read from quad 64h + L.  The 16-bit entries hold no row: an entry's row is that of its
-    slot (chunk_slot of its chunk + the run starts before it in the chunk), read back through
+    slot (chunk_info[c, 0] of its chunk + the run starts before it in the chunk), read back through
     the combine tables (row_ptr, slots) - so the check below also checks that the run starts
     and the slot tables agree."""
     n = layout.n_entries
@@ -232,7 +237,7 @@ def _panel_logical(layout):
     assert np.all(col < (1 << layout.col_bits))
     assert np.all(start[::512])  # every chunk opens a run
     run_in_chunk = np.cumsum(start.reshape(-1, 512), axis=1).reshape(-1) - 1
-    slot = layout.chunk_slot.numpy().astype(np.int64)[p // 512] + run_in_chunk
+    slot = layout.chunk_info.numpy()[:, 0].astype(np.int64)[p // 512] + run_in_chunk
     rp, slots = layout.row_ptr.numpy(), layout.slots.numpy()
     slot_row = np.full(layout.n_partials, -1, dtype=np.int64)
     for i in range(layout.n_rows):
@@ -265,18 +270,24 @@ def _check_panels(layout, data, cols, rowptr):
         assert start.reshape(-1, chunk).sum(1).max() <= caps["panel_chunk_runs"]
     assert np.array_equal(np.sort(_spmv_layouts.panel_storage_positions(
         layout.n_entries, chunk, "cpu").numpy()), np.arange(layout.n_entries))  # a permutation
+    # entries in use: each chunk's first chunk_info[c, 1]; the rest (its tail) padding of
+    # value 0 in the row of the last run
+    info = layout.chunk_info.numpy().astype(np.int64)
+    assert np.all((info[:, 1] >= 1) & (info[:, 1] <= chunk))
+    in_use = (e % chunk) < np.repeat(info[:, 1], chunk)
+    assert np.all(vals[~in_use] == 0)
     got = []
     for j in range(layout.n_jobs):
         e = np.arange(jobs[j] * chunk, jobs[j + 1] * chunk)
         rows = pidx[e] >> cb
         assert np.all(np.diff(rows) >= 0)  # a job lies in one panel, whose rows ascend
         cols_e = (int(jp[j]) << cb) + (pidx[e] & ((1 << cb) - 1))
-        real = vals[e] != 0
-        got += list(zip(rows[real].tolist(), cols_e[real].tolist(), vals[e][real].tolist()))
+        u = in_use[e]
+        got += list(zip(rows[u].tolist(), cols_e[u].tolist(), vals[e][u].tolist()))
     rp = rowptr.numpy()
     want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
-            for i in range(rp[r], rp[r + 1]) if float(data[i]) != 0.0]
-    assert sorted(got) == sorted(want)
+            for i in range(rp[r], rp[r + 1])]
+    assert sorted(got) == sorted(want)  # every entry once, explicit zeros included
 
 
 def _case(lengths, n_cols, seed, dtype=torch.float32, unsorted=False):
@@ -540,6 +551,35 @@ def test_panel_layout_short_runs():
     _check_panels(lay, vals, cols, ip)
     y = _emulate_panels(lay, x.numpy(), np.full(len(lengths), np.nan))
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
+
+
+def _without_panel_bases(vals, cols, ip, cb):
+    """The matrix without its entries in each panel's first column (multiples of 2^cb)."""
+    keep = (cols.to(torch.int64) & ((1 << cb) - 1)) != 0
+    row = torch.repeat_interleave(torch.arange(ip.numel() - 1), ip[1:] - ip[:-1])[keep]
+    ip2 = torch.zeros_like(ip)
+    ip2[1:] = torch.cumsum(torch.bincount(row, minlength=ip.numel() - 1), 0)
+    return vals[keep], cols[keep], ip2
+
+
+@pytest.mark.parametrize("bad", [float("inf"), float("nan")])
+def test_panel_padding_adds_zero_for_nonfinite_x(bad):
+    # padding entries point at their panel's first column with value 0; with x infinite or NaN
+    # there (and no entry of the matrix in that column) they must still add exactly 0
+    rng = np.random.default_rng(6)
+    lengths = rng.integers(2, 120, 600)
+    vals, cols, ip, x = _case(lengths, 200000, 10)
+    cb = _spmv_layouts._panel_col_bits(200000, 4)
+    vals, cols, ip = _without_panel_bases(vals, cols, ip, cb)
+    lay = PanelLayout(vals, cols, ip, 200000, torch.arange(len(lengths)))
+    _check_panels(lay, vals, cols, ip)
+    assert int(lay.chunk_info[:, 1].min()) < _abi.caps()["panel_chunk"]  # there is padding
+    x = x.clone()
+    x[::1 << cb] = bad
+    y = _emulate_panels(lay, x.numpy(), np.full(len(lengths), np.nan))
+    ref = oracle.spmv_csr(ip, cols, vals, x)
+    assert np.all(np.isfinite(ref))
+    np.testing.assert_allclose(y, ref, rtol=1e-12, atol=1e-12)
 
 
 def test_hybrid_falls_back_to_xcs(monkeypatch):

@@ -1,8 +1,9 @@
 """Seeded fuzz on the GPU: random shapes and row-length mixes (power law, uniform, mostly
 empty, one huge row among empty ones).  SpMV is forced through the row-block, XCS and XCS +
 panel layouts, CSR and COO, both accumulation modes; the same matrices then go through CSR SpMM
-(base and opt, row- and column-major B), COO SpMM and SDDMM with a dense width drawn per case.
-All against the fp64 oracle.
+(base and opt, row- and column-major B), COO SpMM and SDDMM with a dense width drawn per case;
+and all of them once more with +inf, -inf and NaN in a few columns of x and B, where the NaN and
+infinity pattern must be the oracle's.  All against the fp64 oracle.
 
 Bars as in test_gpu_spmv_csr.py: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
 allclose ratio, and for the default float32 SpMV path at most 1 ulp from float32(fp64 oracle).
@@ -135,3 +136,53 @@ def test_fuzz_spmm_sddmm(dev, seed):
     out = fs.flagsparse_sddmm_csr(data=d, indices=c, indptr=p, x=xs.to(dev), y=Bd, shape=shape,
                                   alpha=0.5, beta=2.0)
     _check_dense(out, oracle.sddmm_csr(ptr, cols, xs, B, vals, alpha=0.5, beta=2.0))
+
+
+def _check_nonfinite(out, ref64):
+    """NaN and signed infinities exactly where the oracle has them (for a sum that does not
+    depend on the summation order), the finite values within the usual bars."""
+    out = out.cpu().numpy() if torch.is_tensor(out) else out
+    assert np.array_equal(np.isnan(out), np.isnan(ref64))
+    inf = np.isinf(ref64)
+    assert np.array_equal(np.isinf(out), inf)
+    assert np.array_equal(np.sign(out[inf]), np.sign(ref64[inf]))
+    fin = np.isfinite(ref64)
+    if fin.any():
+        _check_dense(torch.as_tensor(out[fin]), ref64[fin])
+
+
+@pytest.mark.parametrize("seed", range(len(CASES)))
+def test_fuzz_nonfinite(dev, monkeypatch, seed):
+    # x (and B, and SDDMM's y) with +inf, -inf and NaN in a few random columns: every path
+    # gives the oracle's NaN / inf pattern - padding and masked lanes must add exactly 0
+    kind, rng, vals, cols, ptr, x, shape = _matrix(seed)
+    n_rows, n_cols = shape
+    bad_cols = rng.choice(n_cols, size=min(n_cols, 3), replace=False)
+    x = x.clone()
+    for c, v in zip(bad_cols, (float("inf"), float("-inf"), float("nan"))):
+        x[int(c)] = v
+    print(f"fuzz non-finite seed={seed} {kind} shape={shape} nnz={vals.numel()}", flush=True)
+    ref = oracle.spmv_csr(ptr, cols, vals, x)
+    d, c, p, xd = vals.to(dev), cols.to(torch.int32).to(dev), ptr.to(dev), x.to(dev)
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", int(rng.integers(2, 64)))
+    for layout in ("rowblock", "xcs-l2", "xcs-hybrid"):
+        monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+        prepared = fs.prepare_spmv_csr(d, c, p, shape)
+        for use_opt in (False, True):
+            _check_nonfinite(fs.flagsparse_spmv_csr(x=xd, prepared=prepared, use_opt=use_opt),
+                             ref)
+    rows = torch.repeat_interleave(torch.arange(n_rows), ptr[1:] - ptr[:-1])
+    for sort_by_row in (True, False):
+        _check_nonfinite(fs.flagsparse_spmv_coo(d, rows.to(dev), c, xd, shape,
+                                                sort_by_row=sort_by_row), ref)
+    N = 5
+    B = synthetic.uniform_values(seed, 4, n_cols * N, vals.dtype, "cpu").reshape(n_cols, N)
+    B[torch.as_tensor(bad_cols)] = x[torch.as_tensor(bad_cols)].unsqueeze(1)
+    ref_c = oracle.spmm_csr(ptr, cols, vals, B)
+    Bd = B.to(dev)
+    _check_nonfinite(fs.flagsparse_spmm_csr(d, c, p, Bd, shape), ref_c)
+    _check_nonfinite(fs.flagsparse_spmm_csr_opt(d, c, p, Bd, shape), ref_c)
+    _check_nonfinite(fs.flagsparse_spmm_coo(d, rows.to(dev), c, Bd, shape), ref_c)
+    xs = synthetic.uniform_values(seed, 5, n_rows * N, vals.dtype, "cpu").reshape(n_rows, N)
+    out = fs.flagsparse_sddmm_csr(data=d, indices=c, indptr=p, x=xs.to(dev), y=Bd, shape=shape)
+    _check_nonfinite(out, oracle.sddmm_csr(ptr, cols, xs, B))

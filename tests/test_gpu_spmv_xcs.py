@@ -258,3 +258,24 @@ def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype):
             assert np.array_equal(y[np.isinf(ref)], ref[np.isinf(ref)].astype(y.dtype))
             name = "float64" if dtype == torch.float64 else "float32"
             assert oracle.rel_l2(torch.as_tensor(y[fin]), ref[fin]) <= oracle.REL_L2_BOUND[name]
+
+
+@pytest.mark.parametrize("n_rows,n_cols,lengths", [
+    (1000, 7, [0] * 1000),          # no entries
+    (3, 1, [1, 0, 1]),              # one column
+    (1, 5, [5]),                    # one row holding every column
+    (5, 3, [0, 3, 0, 0, 3]),
+    (2, 100000, [0, 0]),            # wide, empty
+])
+@pytest.mark.parametrize("layout", ["xcs-l2", "xcs-hybrid"])
+def test_degenerate_shapes(dev, monkeypatch, n_rows, n_cols, lengths, layout):
+    monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 2)
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 37, torch.float32)
+    print(f"degenerate {layout} {shape} nnz={data.numel()}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
+        assert y.shape == (n_rows,)
+        np.testing.assert_allclose(y.cpu().numpy(), ref, rtol=1e-6, atol=1e-6)

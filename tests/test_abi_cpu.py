@@ -258,3 +258,9 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert panels(n_entries=512, n_jobs=1) == -1  # jobs without arrays
     assert panels(n_rows=3) == -1                 # combine without its arrays
     assert b"null" in L.fsp_last_error()
+    # a chunk table that is not 8-byte aligned (two int32 per chunk): refused before any
+    # launch (the other pointers are never dereferenced on the host)
+    fake = 1 << 20
+    assert L.fsp_spmv_panels(0, 0, fake, fake, 512, 10, fake, 1024, None, None, fake, fake, 1,
+                             fake + 4, fake, 64, None, None, None, 0, None) == -1
+    assert b"chunk_info" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()

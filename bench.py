@@ -46,7 +46,10 @@ targets      north_star's two targets measured in the same run, each with the sa
 Probe workloads (measurement only; the access patterns the kernels are bound by, alone):
   probe-gather  random 4-byte gathers (fsp_probe_gather) from an fp32 x of --probe-bytes
                 (default 33.5 MB, cfg3's x), 16 per thread in flight; --probe-xcd restricts
-                the gathers of XCD k to the k-th eighth of x (the XCS layout's placement)
+                the gathers of XCD k to the k-th eighth of x (the XCS layout's placement);
+                --probe-group G --probe-range W [--probe-sorted]: each group of G gathers
+                (an XCS item's worth) draws from one range of W bytes of its eighth, sorted
+                and laid out lane-major on request (neighbouring lanes, neighbouring lines)
   probe-rows    random 256-byte row gathers (fsp_probe_rows) from an fp32 B[rows, 64] of
                 --probe-bytes (default 268 MB, cfg5 N=64's B): 16.8M gathers, cfg5's random half
   --cfg5-part band|random   cfg5 with only its banded or only its random half (16 entries per
@@ -117,6 +120,16 @@ def _parse():
                     help="probe workloads: number of gathers")
     ap.add_argument("--probe-xcd", action="store_true",
                     help="probe-gather: XCD k gathers only from the k-th eighth of x")
+    ap.add_argument("--probe-group", type=int, default=0,
+                    help="probe-gather with --probe-xcd: gathers per group (a multiple of 1024 "
+                         "dividing 4096, one workgroup's share or half of it); each group draws "
+                         "from one --probe-range of its XCD's eighth")
+    ap.add_argument("--probe-range", type=int, default=0,
+                    help="probe-gather with --probe-group: bytes of x one group draws from")
+    ap.add_argument("--probe-sorted", action="store_true",
+                    help="probe-gather with --probe-group: each group sorted and laid out "
+                         "lane-major (the 64 lanes of a gather instruction take neighbouring "
+                         "sorted indices)")
     return ap.parse_args()
 
 
@@ -532,26 +545,41 @@ def _sddmm_workload(dev, dtype_name, K, torch, fs, synthetic):
     }
 
 
-def _probe_indices(n, hi, xcd, dev, torch, per_block):
+def _probe_indices(n, hi, xcd, dev, torch, per_block, group=0, range_len=0, sort=False):
     """n int32 indices uniform in [0, hi) (seed fixed); with xcd, the indices of workgroup b
     (per_block consecutive ones) lie in the (b mod 8)-th eighth of [0, hi) - workgroup b runs
-    on XCD b mod 8."""
+    on XCD b mod 8.  With a group size, each group of that many consecutive indices draws from
+    one range of range_len values (chosen at random) inside its eighth, and with sort the group
+    is sorted and laid out lane-major: a thread of fsp_probe_gather takes 16 consecutive
+    indices, so sorted index 64k + lane of a wave's 1024 goes to position 16 * lane + k."""
     g = torch.Generator(device=dev)
     g.manual_seed(20260)
     if not xcd:
         return torch.randint(0, hi, (n,), generator=g, device=dev, dtype=torch.int32)
     w = max(1, hi // 8)
     blk = torch.arange(n, device=dev, dtype=torch.int64) // per_block
-    r = torch.randint(0, w, (n,), generator=g, device=dev, dtype=torch.int64)
-    return ((blk % 8) * w + r).to(torch.int32)
+    if not group:
+        r = torch.randint(0, w, (n,), generator=g, device=dev, dtype=torch.int64)
+        return ((blk % 8) * w + r).to(torch.int32)
+    if group % 1024 or per_block % group or n % per_block:
+        raise SystemExit("--probe-group must be a multiple of 1024 dividing 4096, and the "
+                         "gather count a multiple of 4096")
+    span = min(w, range_len or w)
+    n_groups = n // group
+    first = (torch.arange(n_groups, device=dev) * group // per_block % 8) * w +         torch.randint(0, w // span, (n_groups,), generator=g, device=dev) * span
+    idx = first.repeat_interleave(group) +         torch.randint(0, span, (n,), generator=g, device=dev, dtype=torch.int64)
+    if sort:
+        idx = torch.sort(idx.view(n_groups, group), dim=1)[0]
+        idx = idx.view(-1, 16, 64).transpose(1, 2).contiguous().view(-1)
+    return idx.to(torch.int32)
 
 
-def _probe_gather_call(x_len, n, xcd, dev, torch):
+def _probe_gather_call(x_len, n, xcd, dev, torch, group=0, range_len=0, sort=False):
     from flagsparse_amd import _abi
 
     L = _abi.lib()
     x = torch.ones(x_len, dtype=torch.float32, device=dev)
-    idx = _probe_indices(n, x_len, xcd, dev, torch, 256 * 16)
+    idx = _probe_indices(n, x_len, xcd, dev, torch, 256 * 16, group, range_len, sort)
     out = torch.empty(max(1, int(L.fsp_probe_gather_blocks(n))), dtype=torch.float32, device=dev)
     args = (x.data_ptr(), x_len, idx.data_ptr(), n, out.data_ptr())
 
@@ -599,11 +627,20 @@ def _probe_workload(name, args, dev, torch):
     if name == "probe-gather":
         x_len = (args.probe_bytes or 8 * (1 << 20) * 4) // 4
         n = (args.probe_n or 100 * (1 << 20)) // 4 * 4
-        call = _probe_gather_call(x_len, n, args.probe_xcd, dev, torch)
+        group = args.probe_group if args.probe_xcd else 0
+        if group:
+            n = n // 4096 * 4096
+        call = _probe_gather_call(x_len, n, args.probe_xcd, dev, torch, group,
+                                  args.probe_range // 4, args.probe_sorted)
         nbytes = n * 8  # an index and a gathered value per gather
         info = {"x_bytes": x_len * 4, "gathers": n, "xcd_panels": bool(args.probe_xcd),
                 "bytes_counted": "4-byte index + 4-byte value per gather"}
         tag = f"probe_gather_{x_len * 4}{'_xcd' if args.probe_xcd else ''}"
+        if group:
+            span = min(x_len // 8, args.probe_range // 4 or x_len // 8) * 4
+            info.update({"group": group, "group_range_bytes": span,
+                         "sorted_lane_major": bool(args.probe_sorted)})
+            tag += f"_g{group}_r{span}{'_sorted' if args.probe_sorted else ''}"
     else:
         n_rows = (args.probe_bytes or (1 << 20) * 256) // 256
         n = args.probe_n or 16 * (1 << 20)

@@ -30,3 +30,27 @@ def test_profiles_parse():
             assert 0.0 <= v <= 1.0, (f, k)
     assert bench._profile("no_such_profile") == {}
     json.dumps(prof)
+
+
+def test_probe_group_indices():
+    # --probe-group / --probe-range / --probe-sorted: every index inside its workgroup's XCD
+    # eighth and inside one range per group; sorted groups laid out lane-major
+    import torch
+
+    hi, n, group, span = 1 << 20, 4 * 4096, 2048, 1 << 14
+    for sort in (False, True):
+        idx = bench._probe_indices(n, hi, True, "cpu", torch, 4096, group, span, sort)
+        idx = idx.to(torch.int64)
+        assert idx.numel() == n and int(idx.min()) >= 0 and int(idx.max()) < hi
+        w = hi // 8
+        blk = torch.arange(n) // 4096
+        assert torch.equal(idx // w, blk % 8)                     # the XCD's eighth
+        g = idx.view(-1, group)
+        assert torch.equal(g.min(1)[0] // span, g.max(1)[0] // span)  # one range per group
+        if sort:
+            # thread t takes positions 16t..16t+15; instruction k of a wave gathers sorted
+            # indices 64k .. 64k + 63 of that wave's 1024, one per lane, in lane order
+            wave = idx.view(-1, 64, 16).transpose(1, 2).reshape(-1, 1024)
+            assert bool((wave[:, 1:] >= wave[:, :-1]).all())
+    plain = bench._probe_indices(n, hi, True, "cpu", torch, 4096)
+    assert torch.equal(plain.to(torch.int64) // (hi // 8), torch.arange(n) // 4096 % 8)

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lib = None
 
@@ -37,6 +37,8 @@ SIGNATURES = {
     "fsp_xcs_window_slots_cap": (_i64, []),
     "fsp_xcs_window_rows_cap": (_i64, []),
     "fsp_xcs_item_runs_cap": (_i64, []),
+    "fsp_xcs_sorted_item_cap": (_i64, []),
+    "fsp_xcs_sorted_col_bits": (_i64, []),
     "fsp_panel_bytes_cap": (_i64, []),
     "fsp_panel_chunk": (_i64, []),
     "fsp_panel_chunk_runs_cap": (_i64, []),
@@ -48,7 +50,7 @@ SIGNATURES = {
     "fsp_spmv_csr_static": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p,
                                    _p, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p]),
     "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64, _p, _p,
-                            _p, _i64, _i64, _p, _p, _p]),
+                            _p, _i64, _i64, _p, _p, _i32, _p]),
     "fsp_spmv_panels": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i64,
                                _p, _p, _i64, _p, _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
@@ -144,6 +146,8 @@ def caps():
         "xcs_window_slots": int(L.fsp_xcs_window_slots_cap()),
         "xcs_window_rows": int(L.fsp_xcs_window_rows_cap()),
         "xcs_item_runs": int(L.fsp_xcs_item_runs_cap()),
+        "xcs_sorted_item": int(L.fsp_xcs_sorted_item_cap()),
+        "xcs_sorted_col_bits": int(L.fsp_xcs_sorted_col_bits()),
         "panel_bytes": int(L.fsp_panel_bytes_cap()),
         "panel_chunk": int(L.fsp_panel_chunk()),
         "panel_chunk_runs": int(L.fsp_panel_chunk_runs_cap()),

@@ -91,6 +91,18 @@ WINDOW_ROWS = 2048
 RUN_ALIGN = 16
 # Every combine window's stored range starts on a multiple of this many slots (a line).
 WINDOW_ALIGN = 16
+# XCS items with sorted gathers (item format 1, spmv_xcs_sorted_kernel): up to 4096 entries
+# per item, the gathers issued in column order so that the lanes of one instruction reach
+# neighbouring lines; used when the panels need at most 19 column bits.  Tiles of up to
+# SORTED_TILE_ROWS rows, so that a tile's share of a panel fills an item.
+SORTED_ITEMS = True
+SORTED_TILE_ROWS = 16384
+# ... for matrices whose rows put at least this many entries, on average, into each panel they
+# reach.  Measured on MI355X: cfg4 (rows of 21 entries over 4 panels, 5.3 per panel) 193 ->
+# 186 us in the XCS kernel; cfg3's short rows (2.0 per panel: most rows put one entry into
+# each panel they reach, so most entries are row runs of their own) 142 us with row-order
+# items, 144-155 us with sorted ones for tiles of 6144 to 16384 rows.
+SORTED_MIN_RUN = 3.0
 
 
 class RowBlockLayout:
@@ -234,7 +246,9 @@ class XcsLayout:
 
     kind = "xcs"
 
-    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None):
+    def __init__(self, data, cols, rowptr, n_cols, panels_per_xcd=None, item_format=None):
+        """item_format: 1 (sorted gathers) or 0; None - 1 when SORTED_ITEMS is set and the
+        panels need at most xcs_sorted_col_bits column bits."""
         dev = data.device
         caps = _abi.caps()
         item_cap, rows_cap = caps["xcs_item"], caps["xcs_rows"]
@@ -275,8 +289,17 @@ class XcsLayout:
         assert int(widths.max()) <= wmax
         self.panel_base_host = cb
         self.col_bits = _ceil_log2(max(int(widths.max()), 2))
-        row_bits = 32 - self.col_bits
-        self.rows_cap = min(rows_cap, 1 << row_bits)
+        if item_format is None:
+            item_format = 1 if SORTED_ITEMS and \
+                _entries_per_panel_run(lengths, P) >= SORTED_MIN_RUN else 0
+        self.item_format = 1 if item_format == 1 and \
+            self.col_bits <= caps["xcs_sorted_col_bits"] else 0
+        if self.item_format == 1:  # rows are not packed into the entries
+            item_cap = caps["xcs_sorted_item"]
+            self.rows_cap = SORTED_TILE_ROWS
+        else:
+            row_bits = 32 - self.col_bits
+            self.rows_cap = min(rows_cap, 1 << row_bits)
         self.panel_base = torch.tensor(cb[:P], dtype=torch.int32, device=dev)
         if self.rows_cap < 256:
             raise ValueError("column panels too wide for the XCS packing")
@@ -340,6 +363,8 @@ class XcsLayout:
         qp = torch.clamp((q_tot + 255) // 256, min=1)
         nt = (q_tot + qp - 1) // qp
         padded = 4 * nt * qp
+        if self.item_format == 1:  # 8 entries per thread of 512, in whole waves
+            padded = (item_len + 511) // 512 * 512
         item_start = torch.cumsum(padded, 0) - padded
         n_entries = int(padded.sum().item()) if n_items else 0
         if n_entries > _INDEX_LIMIT_INT32:
@@ -355,22 +380,48 @@ class XcsLayout:
         j = torch.where(o < big, o // (b + 1), rm + (o - big) // b.clamp(min=1))
         item_of = piece_first_item[key_sorted] + j
         oi = o - item_off[item_of]  # logical position inside the item
-        qpi = qp[item_of]
-        lq = oi // 4
-        dest = item_start[item_of] + 4 * (lq // qpi + nt[item_of] * (lq % qpi)) + oi % 4
-        del oi, qpi, lq
         del o, b, rm, big, j
-        vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
-        vals[dest] = data[perm]
-        loc_row = (entry_row[perm] - t_r0_d[key_sorted // P]).to(torch.int64)
         pan = key_sorted % P
         colp = cols[perm].to(torch.int64) - self.panel_base.to(torch.int64)[pan]
-        packed = (loc_row << self.col_bits) | colp
+        del pan
         pidx = torch.zeros(max(n_entries, 4), dtype=torch.int64, device=dev)
-        pidx[dest] = packed
+        if self.item_format == 1:
+            # values in row order: position 8t + e at quad (e/4) * P/8 + t, element e % 4
+            thr = padded[item_of] // 8
+            dest = item_start[item_of] + 4 * ((oi % 8) // 4 * thr + oi // 8) + oi % 4
+            # gather words in column order: the k-th gather of thread t is entry
+            # (t/64)*512 + 64k + t%64 of the item's column order, at the same quads
+            er = entry_row[perm]
+            start = torch.ones_like(oi, dtype=torch.bool)
+            if nnz > 1:
+                start[1:] = (oi[1:] == 0) | (er[1:] != er[:-1])
+            del er
+            sb = caps["xcs_sorted_col_bits"]
+            word = (oi << (sb + 1)) | (start.to(torch.int64) << sb) | colp
+            del start
+            by_col = torch.sort(item_of * (1 << 20) + colp, stable=True)[1]
+            first_entry = torch.cumsum(item_len, 0) - item_len  # items are contiguous
+            it_c = item_of[by_col]
+            gr = torch.arange(nnz, device=dev) - first_entry[it_c]
+            t_g = (gr // 512) * 64 + gr % 64
+            kk = (gr % 512) // 64
+            gdest = item_start[it_c] + 4 * (kk // 4 * thr[by_col] + t_g) + kk % 4
+            pidx[gdest] = word[by_col]
+            del word, by_col, it_c, gr, t_g, kk, gdest, thr
+        else:
+            qpi = qp[item_of]
+            lq = oi // 4
+            dest = item_start[item_of] + 4 * (lq // qpi + nt[item_of] * (lq % qpi)) + oi % 4
+            del qpi, lq
+            loc_row = (entry_row[perm] - t_r0_d[key_sorted // P]).to(torch.int64)
+            pidx[dest] = (loc_row << self.col_bits) | colp
+            del loc_row
+        del oi, colp
+        vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
+        vals[dest] = data[perm]
         self.vals = vals
         self.pidx = torch.where(pidx >= (1 << 31), pidx - (1 << 32), pidx).to(torch.int32)
-        del packed, colp, pan, loc_row, pidx, dest
+        del pidx, dest
 
         # 6. Partial sums: one per (item, row run it holds); per row they are added in item
         #    order (the combine's summation order).  Where each is stored: the combine tables.
@@ -533,7 +584,7 @@ class XcsLayout:
         self.window_slots = win_slots
 
     def kernel_name(self):
-        return "spmv_xcs_kernel"
+        return "spmv_xcs_sorted_kernel" if self.item_format == 1 else "spmv_xcs_kernel"
 
     def held_bytes(self, caller=()):
         """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
@@ -547,7 +598,8 @@ class XcsLayout:
                 "slots": self.n_slots, "split_rows": self.n_split_rows,
                 "partials": self.n_partials, "combine_windows": self.n_windows,
                 "panel_base": self.panel_base_host,
-                "col_bits": self.col_bits, "padded_entries": self.n_entries}
+                "col_bits": self.col_bits, "padded_entries": self.n_entries,
+                "item_format": self.item_format}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
         # static arguments converted once per accumulation mode (see RowBlockLayout.launch)
@@ -559,13 +611,14 @@ class XcsLayout:
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
                     self.n_slots, p(self.item_runs), p(self.partials), p(self.windows),
-                    self.n_windows, self.window_slots, p(self.dest), p(self.row_start), None]
+                    self.n_windows, self.window_slots, p(self.dest), p(self.row_start),
+                    self.item_format, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[7] = x.data_ptr(), y.data_ptr()
         a[8] = None if row_map is None else row_map.data_ptr()
         a[9] = n_out
-        a[19] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.items,
+        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.items,
                                               self.item_runs, self.windows, self.dest,
                                               self.row_start))
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
@@ -797,8 +850,8 @@ class XcsHybridLayout:
         entry_long = torch.repeat_interleave(long_mask, lengths)
         short_ptr = torch.zeros_like(rp)
         torch.cumsum(torch.where(long_mask, 0, lengths), 0, out=short_ptr[1:])
-        self.short = XcsLayout(data[~entry_long], cols[~entry_long], short_ptr, n_cols,
-                               panels_per_xcd)
+        self.short = xcs_layout(data[~entry_long], cols[~entry_long], short_ptr, n_cols,
+                                panels_per_xcd)
         long_rows = torch.nonzero(long_mask).flatten()
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
@@ -843,6 +896,26 @@ def prefers_xcs(cols, rowptr, n_cols, value_bytes):
     return bool(far.to(torch.float32).mean().item() > 0.5)
 
 
+def _entries_per_panel_run(lengths, P):
+    """Expected entries per (row, panel) pair for rows of the given lengths with columns spread
+    evenly over P panels: a row of k entries reaches P (1 - (1 - 1/P)^k) panels."""
+    k = lengths.to(torch.float64)
+    reached = float((P * (1.0 - torch.pow(1.0 - 1.0 / P, k))).sum().item())
+    return float(k.sum().item()) / reached if reached > 0 else 0.0
+
+
+def xcs_layout(data, cols, rowptr, n_cols, panels_per_xcd=None):
+    """XcsLayout with sorted-gather items where they fit, else the row-order items: the taller
+    tiles of the sorted format can reach more combine windows than an item's run table holds
+    (rows with many sums, small windows).  ValueError when neither packing fits."""
+    try:
+        return XcsLayout(data, cols, rowptr, n_cols, panels_per_xcd)
+    except ValueError:
+        if not SORTED_ITEMS:
+            raise
+    return XcsLayout(data, cols, rowptr, n_cols, panels_per_xcd, item_format=0)
+
+
 def build_layout(data, cols, rowptr, n_cols, one_shot=False):
     """The layout for one CSR (or COO row-run) matrix: XCS when it pays, else row blocks.
     one_shot: the layout serves a single call (no prepared object), so the row-block layout,
@@ -868,11 +941,12 @@ def build_layout(data, cols, rowptr, n_cols, one_shot=False):
                 except ValueError:
                     pass  # a part too large for its packing: XCS alone, else row blocks
         try:
-            return XcsLayout(data, cols, rowptr, n_cols, FORCE_PANELS_PER_XCD)
+            return xcs_layout(data, cols, rowptr, n_cols, FORCE_PANELS_PER_XCD)
         except ValueError:
             pass  # too large for the packing: row blocks
     return RowBlockLayout(data, cols, rowptr)
 
 
 __all__ = ["RowBlockLayout", "XcsLayout", "PanelLayout", "XcsHybridLayout", "build_layout",
+           "xcs_layout",
            "prefers_xcs", "sample_indices", "FORCE"]

@@ -27,7 +27,7 @@ using namespace fsp;
 
 extern "C" const char* fsp_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int fsp_abi_version(void) { return 10; }
+extern "C" int fsp_abi_version(void) { return 11; }
 
 extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }
@@ -38,6 +38,8 @@ extern "C" int64_t fsp_xcs_rows_cap(void) { return kXcsRowsCap; }
 extern "C" int64_t fsp_xcs_window_slots_cap(void) { return kXcsWinSlotsCap; }
 extern "C" int64_t fsp_xcs_window_rows_cap(void) { return kXcsWinRowsCap; }
 extern "C" int64_t fsp_xcs_item_runs_cap(void) { return kXcsItemRunsCap; }
+extern "C" int64_t fsp_xcs_sorted_item_cap(void) { return kXcsSortedItemCap; }
+extern "C" int64_t fsp_xcs_sorted_col_bits(void) { return kXcsSortedColBits; }
 extern "C" int64_t fsp_panel_bytes_cap(void) { return kPanelBytes; }
 extern "C" int64_t fsp_panel_chunk(void) { return kPanelChunk; }
 extern "C" int64_t fsp_panel_chunk_runs_cap(void) { return kPanelChunkRunsCap; }

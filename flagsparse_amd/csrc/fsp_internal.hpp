@@ -24,6 +24,8 @@ constexpr int64_t kXcsRowsCap = 8192;                    // rows of one XCS tile
 constexpr int64_t kXcsWinSlotsCap = 4096;                // partial slots of one combine window
 constexpr int64_t kXcsWinRowsCap = 2048;                 // rows of one combine window
 constexpr int64_t kXcsItemRunsCap = 64;                  // stored runs (windows) of one XCS item
+constexpr int64_t kXcsSortedItemCap = 4096;              // entries of one sorted-gather XCS item
+constexpr int64_t kXcsSortedColBits = 19;                // column bits of a sorted-gather entry
 constexpr int64_t kPanelBytes = 131072;                  // x panel copied to LDS (panel SpMV)
 constexpr int64_t kPanelChunk = 512;                     // entries per wave chunk (panel SpMV)
 constexpr int64_t kPanelChunkRunsCap = 64;               // runs (rows) of one chunk, at most

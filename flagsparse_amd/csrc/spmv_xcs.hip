@@ -277,6 +277,185 @@ __global__ __launch_bounds__(kBlock) void spmv_xcs_kernel(
   }
 }
 
+// Sorted-gather items (item format 1).  The rate of random 4-byte gathers from L2 depends on
+// how close together the 64 lanes of one gather instruction reach: measured on MI355X with
+// groups of 2048 gathers in a 2 MiB range, 137 us in random order and 131 us sorted and laid
+// out lane-major; with the lanes about one line apart (2048 gathers in 256 KiB) 98 us.  An
+// item here holds up to 4096 entries (a workgroup of 512 threads), and its gather entries are
+// stored in column order, lane-major: gather k of thread t is entry (t/64)*512 + 64k + t%64 of
+// the column order.  Each gather entry carries the entry's position in row order and whether
+// it starts a row run there, so the gathered x values go to LDS in row order, and after one
+// barrier every thread reads back its 8 consecutive row-order positions - the layout of the
+// thread-major kernel above, whose segmented scan and emission follow unchanged (run starts
+// from the flags instead of row comparisons).
+//   vals   row order: position 8t + e of thread t at quad (e/4) * P/8 + t, element e % 4
+//   gidx   column order, the same quads: (row-order position << 20) | run start << 19 | column
+//          in the panel (19 bits); P = the item's length rounded up to 512
+constexpr int kSortedBlock = 512;
+constexpr int kSortedWaves = kSortedBlock / kWave;
+constexpr int kSortedCap = (int)kXcsSortedItemCap;
+constexpr int kSortedPer = kSortedCap / kSortedBlock;
+static_assert(kSortedPer == 8, "eight entries per thread");
+constexpr unsigned kSortedColBits = (unsigned)kXcsSortedColBits;
+constexpr unsigned kSortedColMask = (1u << kSortedColBits) - 1u;
+constexpr unsigned kSortedPosShift = kSortedColBits + 1u;
+static_assert(kSortedPosShift + 12 <= 32, "a position below 4096 fits the word");
+
+// LDS of the sorted-gather kernel: the item's x values and run-start flags in row order, then
+// (the same bytes, after the scan's barrier) its run sums.
+template <typename T, typename A>
+constexpr int sorted_lds_bytes() {
+  constexpr int stage = kSortedCap * ((int)sizeof(T) + 1);
+  constexpr int part = kSortedCap * (int)sizeof(A);
+  return stage > part ? stage : part;
+}
+// Workgroups per CU of the sorted-gather kernel, set by the LDS each one claims.
+constexpr unsigned kXcsSortedLdsPerWorkgroup = 40u * 1024u;
+
+template <typename T, typename A>
+__global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
+    const T* __restrict__ vals, const uint32_t* __restrict__ gidx, const T* __restrict__ x,
+    const i32x4* __restrict__ items, int n_slots, const i32x4* __restrict__ item_runs,
+    A* __restrict__ partials) {
+  constexpr int kPer = kSortedPer;
+  __shared__ __align__(16) unsigned char s_buf[sorted_lds_bytes<T, A>()];
+  T* const s_x = reinterpret_cast<T*>(s_buf);
+  unsigned char* const s_fl = s_buf + kSortedCap * sizeof(T);
+  A* const s_part = reinterpret_cast<A*>(s_buf);
+  __shared__ int s_wh[kSortedWaves];
+  __shared__ int s_wc[kSortedWaves];
+  __shared__ A s_wv[kSortedWaves];
+  __shared__ i32x4 s_runs[kItemRuns];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  const int slot = xcd_logical_block(blockIdx.x, n_slots);
+  const i32x4 d0 = items[3 * slot];
+  const i32x4 d1 = items[3 * slot + 1];
+  const i32x4 d2 = items[3 * slot + 2];
+  if (d2.z < 0) return;  // empty slot
+  const int e0 = d0.x, len = d0.y, run0 = d0.w;
+  const int cbase = d1.z, n_ir = d1.w;
+  if (len <= 0 || len > kSortedCap || n_ir < 0 || n_ir > kItemRuns) return;  // no planner item
+  i32x4 my_run = {0, 0, 0, 0};
+  if (tid < n_ir) my_run = item_runs[run0 + tid];
+
+  // Threads [0, P/8) hold entries; the others re-read thread 0's quads and drop them.
+  const int n_thr = (len + kSortedBlock - 1) / kSortedBlock * (kSortedBlock / kPer);
+  const int tt = tid < n_thr ? tid : 0;
+  T v[kPer];
+  uint32_t g[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer / 4; ++u) {
+    const int m = e0 + 4 * (u * n_thr + tt);
+    if constexpr (sizeof(T) == 4) {
+      const f32x4 vv = ld_stream<true>(reinterpret_cast<const f32x4*>(vals + m));
+      v[4 * u] = vv.x; v[4 * u + 1] = vv.y; v[4 * u + 2] = vv.z; v[4 * u + 3] = vv.w;
+    } else {
+      const f64x2 a = ld_stream<true>(reinterpret_cast<const f64x2*>(vals + m));
+      const f64x2 b = ld_stream<true>(reinterpret_cast<const f64x2*>(vals + m + 2));
+      v[4 * u] = a.x; v[4 * u + 1] = a.y; v[4 * u + 2] = b.x; v[4 * u + 3] = b.y;
+    }
+    const i32x4 gg = ld_stream<true>(reinterpret_cast<const i32x4*>(gidx + m));
+    g[4 * u] = (uint32_t)gg.x; g[4 * u + 1] = (uint32_t)gg.y;
+    g[4 * u + 2] = (uint32_t)gg.z; g[4 * u + 3] = (uint32_t)gg.w;
+  }
+  // Gathers in column order, all issued (positions past the item read the panel's first
+  // value), then each value stored at its row-order position.
+  T xv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const bool ok = tid < n_thr && wid * kSortedBlock + k * kWave + lane < len;
+    xv[k] = x[cbase + (ok ? (int)(g[k] & kSortedColMask) : 0)];
+  }
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (tid < n_thr && wid * kSortedBlock + k * kWave + lane < len) {
+      const int p = (int)(g[k] >> kSortedPosShift);
+      s_x[p] = xv[k];
+      s_fl[p] = (unsigned char)((g[k] >> kSortedColBits) & 1u);
+    }
+  }
+  if (tid < n_ir) s_runs[tid] = my_run;
+  __syncthreads();
+
+  // Row order: this thread's positions [i0, i0 + nm).
+  const int i0 = kPer * tid;
+  const int nm = len - i0 < 0 ? 0 : (len - i0 > kPer ? kPer : len - i0);
+  A prod[kPer];
+  bool st[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const bool in = q < nm;
+    prod[q] = in ? A(v[q]) * A(s_x[in ? i0 + q : 0]) : A(0);
+    st[q] = in && s_fl[i0 + q] != 0;
+  }
+  const bool next_starts = i0 + kPer < len ? s_fl[i0 + kPer] != 0 : true;
+
+  // As spmv_xcs_kernel: pass 1 (run starts, the last run piece, runs ending here), the
+  // workgroup scans, pass 2 (each run to the item's next slot), the stored runs written out.
+  const bool cont = nm > 0 && !st[0];
+  const bool last_ends = nm > 0 && next_starts;
+  int has_head = (nm > 0 && !cont) ? 1 : 0;
+  int n_end = last_ends ? 1 : 0;
+  A piece = A(0);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    if (q < nm) {
+      if (q > 0 && st[q]) {
+        has_head = 1;
+        ++n_end;
+        piece = A(0);
+      }
+      piece += prod[q];
+    }
+  }
+  int h_in = has_head;
+  A v_in = piece;
+  int c_in = n_end;
+  wave_seg_scan(h_in, v_in, c_in);
+  if (lane == kWave - 1) {
+    s_wh[wid] = h_in;
+    s_wv[wid] = v_in;
+    s_wc[wid] = c_in;
+  }
+  const int h_ex = dpp_mov<kDppWaveShr1>(0, h_in);  // lane 0: (0, 0, 0)
+  const A v_ex = dpp_mov<kDppWaveShr1>(A(0), v_in);
+  const int c_ex = dpp_mov<kDppWaveShr1>(0, c_in);
+  __syncthreads();  // also: every row-order read of s_x / s_fl is done before s_part reuses them
+  A pv = A(0);
+  int pc = 0;
+  for (int j = 0; j < kSortedWaves; ++j) {
+    if (j < wid) {
+      const A wv = s_wv[j];
+      if (!s_wh[j]) pv = pv + wv; else pv = wv;
+      pc += s_wc[j];
+    }
+  }
+  const A carry = h_ex ? v_ex : pv + v_ex;
+  A* out = s_part + pc + c_ex;
+  bool first = true;
+  A run = A(0);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    if (q < nm) {
+      if (q > 0 && st[q]) {
+        *out++ = (first && cont) ? carry + run : run;
+        first = false;
+        run = A(0);
+      }
+      run += prod[q];
+    }
+  }
+  if (last_ends) *out = (first && cont) ? carry + run : run;
+  __syncthreads();
+  for (int j = 0; j < n_ir; ++j) {
+    const i32x4 r = s_runs[j];
+    for (int l = tid; l < r.w; l += kSortedBlock)
+      partials[r.x + l] = l < r.z ? s_part[r.y + l] : A(0);
+  }
+}
+
 // Second pass: row r gets y = the sum of its partial sums in item order (a fixed order, so the
 // result does not depend on timing), 0 without any.  Rows are grouped into windows of
 // consecutive rows whose sums fit LDS (<= kXcsWinSlotsCap sums, <= kXcsWinRowsCap rows), and
@@ -606,12 +785,28 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
 }
 
 template <typename T, typename A>
-int launch_xcs(const void* vals, const uint32_t* pidx, int col_bits, const void* x, void* y,
-               const int32_t* row_map, const int32_t* items, int64_t n_slots,
-               const int32_t* item_runs, void* partials, const int32_t* windows,
-               int64_t n_windows, int64_t window_slots, const int16_t* dest,
-               const int16_t* row_start, hipStream_t st) {
-  if (n_slots > 0) {
+constexpr unsigned xcs_sorted_lds_reserve() {
+  constexpr unsigned used = (unsigned)sorted_lds_bytes<T, A>() +
+                            (unsigned)(kSortedWaves * (2 * sizeof(int) + sizeof(A))) +
+                            (unsigned)(kItemRuns * sizeof(i32x4));
+  return used < kXcsSortedLdsPerWorkgroup ? kXcsSortedLdsPerWorkgroup - used : 0u;
+}
+
+template <typename T, typename A>
+int launch_xcs(int item_format, const void* vals, const uint32_t* pidx, int col_bits,
+               const void* x, void* y, const int32_t* row_map, const int32_t* items,
+               int64_t n_slots, const int32_t* item_runs, void* partials,
+               const int32_t* windows, int64_t n_windows, int64_t window_slots,
+               const int16_t* dest, const int16_t* row_start, hipStream_t st) {
+  if (n_slots > 0 && item_format == 1) {
+    hipLaunchKernelGGL((spmv_xcs_sorted_kernel<T, A>), dim3((unsigned)n_slots),
+                       dim3(kSortedBlock), (xcs_sorted_lds_reserve<T, A>()), st,
+                       static_cast<const T*>(vals), pidx, static_cast<const T*>(x),
+                       reinterpret_cast<const i32x4*>(items), (int)n_slots,
+                       reinterpret_cast<const i32x4*>(item_runs), static_cast<A*>(partials));
+    int rc = check_hip(hipGetLastError(), "spmv_xcs_sorted_kernel launch");
+    if (rc) return rc;
+  } else if (n_slots > 0) {
     hipLaunchKernelGGL((spmv_xcs_kernel<T, A, true>), dim3((unsigned)n_slots), dim3(kBlock),
                        xcs_lds_reserve<A>(), st, static_cast<const T*>(vals), pidx, col_bits,
                        static_cast<const T*>(x), reinterpret_cast<const i32x4*>(items),
@@ -701,11 +896,17 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
                             const int32_t* row_map, int64_t n_out, const int32_t* items,
                             int64_t n_slots, const int32_t* item_runs, void* partials,
                             const int32_t* windows, int64_t n_windows, int64_t window_slots,
-                            const int16_t* dest, const int16_t* row_start, void* stream) {
+                            const int16_t* dest, const int16_t* row_start, int item_format,
+                            void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
+  if (item_format != 0 && item_format != 1)
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: item_format must be 0 or 1");
+  if (item_format == 1 && col_bits > (int)kXcsSortedColBits)
+    return set_error(FSP_EINVAL, "fsp_spmv_xcs: sorted-gather items take col_bits <= " +
+                                     std::to_string(kXcsSortedColBits));
   if (n_entries < 0 || n_slots < 0 || n_out < 0 || n_windows < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: negative size");
-  if (n_entries > 0x7fffffffLL - kXcsItemCap || n_slots > 0x3fffffffLL ||
+  if (n_entries > 0x7fffffffLL - kXcsSortedItemCap || n_slots > 0x3fffffffLL ||
       n_windows > 0x3fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: too many entries, slots or windows");
   if (col_bits < 1 || col_bits > 24)
@@ -728,8 +929,8 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
                                 : fill_zero<double>(static_cast<double*>(y), n_out, st);
     if (rc) return rc;
   }
-#define FSP_XCS_ARGS vals, pidx, col_bits, x, y, row_map, items, n_slots, item_runs, partials, \
-                     windows, n_windows, window_slots, dest, row_start, st
+#define FSP_XCS_ARGS item_format, vals, pidx, col_bits, x, y, row_map, items, n_slots, item_runs, \
+                     partials, windows, n_windows, window_slots, dest, row_start, st
   if (dtype == FSP_F32) {
     if (acc_f64) return launch_xcs<float, double>(FSP_XCS_ARGS);
     return launch_xcs<float, float>(FSP_XCS_ARGS);

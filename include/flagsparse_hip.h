@@ -77,6 +77,8 @@ int64_t fsp_xcs_rows_cap(void);          /* max rows of one XCS tile            
 int64_t fsp_xcs_window_slots_cap(void);  /* max partial slots of one XCS combine window */
 int64_t fsp_xcs_window_rows_cap(void);   /* max rows of one XCS combine window        */
 int64_t fsp_xcs_item_runs_cap(void);     /* max stored runs (windows) of one XCS item */
+int64_t fsp_xcs_sorted_item_cap(void);   /* max entries of a sorted-gather XCS item     */
+int64_t fsp_xcs_sorted_col_bits(void);   /* max col_bits of sorted-gather XCS items     */
 int64_t fsp_panel_bytes_cap(void);       /* max bytes of one x panel (panel SpMV)     */
 int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)            */
 int64_t fsp_panel_chunk_runs_cap(void);  /* runs (rows) per chunk, at most (panel SpMV) */
@@ -194,9 +196,18 @@ int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals, const int32_t*
 
 /*
  * y = A @ x in the XCD column-split layout (fp32/fp64 values, fp64 or native accumulation).
- *   vals, pidx   n_entries padded entries (16-byte aligned): pidx = (local row << col_bits) |
- *                (column - the panel's first column); every item starts on a multiple of 4
- *   col_bits     in [1, 24]
+ *   vals, pidx   n_entries padded entries (16-byte aligned), by item_format:
+ *                0: items of <= fsp_xcs_item_cap() entries in row order, pidx = (local row <<
+ *                   col_bits) | (column - the panel's first column), every item starting on a
+ *                   multiple of 4 and stored thread-major (256 threads);
+ *                1: items of <= fsp_xcs_sorted_item_cap() entries padded to a multiple of 512,
+ *                   one workgroup of 512 threads; vals in row order, position 8t + e at quad
+ *                   (e / 4) * P/8 + t (P the padded length), element e % 4; pidx in column
+ *                   order in the same quads, entry (t/64)*512 + 64k + t%64 of the column order
+ *                   as element k of thread t, each = (its row-order position << (B + 1)) |
+ *                   (1 << B when it starts a row run there) | (column - the panel's first
+ *                   column), B = fsp_xcs_sorted_col_bits()
+ *   col_bits     in [1, 24] (format 1: <= fsp_xcs_sorted_col_bits())
  *   row_map      NULL: layout row r is y[r]; else y[row_map[r]] and y[0..n_out) is zeroed first
  *   items        n_slots slots of 12 int32 in launch order (slot j runs on XCD j / (n_slots/8)
  *                when n_slots is a multiple of 8): {entry start, count, rank k in tile, first
@@ -224,7 +235,7 @@ int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
                  const int32_t* item_runs, void* partials, const int32_t* windows,
                  int64_t n_windows, int64_t window_slots, const int16_t* dest,
-                 const int16_t* row_start, void* stream);
+                 const int16_t* row_start, int item_format, void* stream);
 
 /*
  * y[rows[i]] (y[row_map[rows[i]]] when row_map != NULL) = row i of A @ x for the long rows of

@@ -223,9 +223,9 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert b"static workspace" in L.fsp_last_error()
     assert spmm(lanes=3) == -1                    # lanes_per_row not a power of two
     assert spmm(dtype=1, lanes=4, vec=4) == -1    # 4-wide vectors are fp32 only
-    def xcs(col_bits=10, n_windows=0):
+    def xcs(col_bits=10, n_windows=0, item_format=0):
         return L.fsp_spmv_xcs(0, 0, None, None, 0, col_bits, None, None, None, 0, None, 0, None,
-                              None, None, n_windows, 1024, None, None, None)
+                              None, None, n_windows, 1024, None, None, item_format, None)
 
     # fsp_index_stats(a, a_bits, b, b_bits, n, partial, out, stream)
     assert L.fsp_index_stats(None, 16, None, 32, 0, None, None, None) == -1
@@ -239,6 +239,10 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert xcs(col_bits=25) == -1                 # col_bits > 24
     assert xcs(n_windows=4) == -1                 # combine without its tables
     assert b"null" in L.fsp_last_error()
+    assert xcs(item_format=2) == -1               # no such item format
+    assert xcs(col_bits=20, item_format=1) == -1  # sorted-gather items take <= 19 column bits
+    assert b"col_bits" in L.fsp_last_error()
+    assert xcs(col_bits=19, item_format=1) == 0
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1
 
     def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0, n_partials=0):

@@ -18,14 +18,19 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["xcs-l2", "xcs-hybrid"])
+@pytest.fixture(params=[("xcs-l2", 0), ("xcs-l2", 1), ("xcs-hybrid", 0), ("xcs-hybrid", 1)],
+                ids=["xcs-rows", "xcs-sorted", "hybrid-rows", "hybrid-sorted"])
 def force_xcs(request, monkeypatch):
     # the hybrid with rows of >= 32 entries in the panel part, so that these small matrices
-    # have long rows in every case that checks the layout kind
-    monkeypatch.setattr(_spmv_layouts, "FORCE", request.param)
-    if request.param == "xcs-hybrid":
+    # have long rows in every case that checks the layout kind; the XCS items in row order
+    # (format 0) or with sorted gathers (format 1) wherever the panels allow it
+    mode, fmt = request.param
+    monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_ITEMS", fmt == 1)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 0.0)
+    if mode == "xcs-hybrid":
         monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
-    return request.param
+    return mode
 
 
 def _kind(mode):
@@ -174,8 +179,9 @@ def test_combine_unaligned_windows(dev, monkeypatch, dtype):
     monkeypatch.setattr(_spmv_layouts, "WINDOW_SLOTS", 128)
     monkeypatch.setattr(_spmv_layouts, "WINDOW_ROWS", 64)
     rng = np.random.default_rng(11)
-    # two rows long enough to have more sums than a window holds (one-row windows)
-    lengths = np.concatenate([rng.zipf(1.8, 30000).clip(max=20000), [400000, 3, 400000]])
+    # two rows long enough to have more sums than a window holds (one-row windows) with
+    # either item size
+    lengths = np.concatenate([rng.zipf(1.8, 30000).clip(max=20000), [900000, 3, 900000]])
     data, idx, ptr, x, shape = _csr_from_lengths(lengths, 1 << 21, 23, dtype)
     print(f"unaligned combine windows {dtype}", flush=True)
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)

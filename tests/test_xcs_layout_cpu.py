@@ -18,6 +18,62 @@ from flagsparse_amd._spmv_layouts import (PanelLayout, XcsHybridLayout, XcsLayou
 from oracle import oracle
 
 
+@pytest.fixture(autouse=True, params=[0, 1], ids=["rows", "sorted"])
+def item_format(request, monkeypatch):
+    """Every test runs with both XCS item formats: 0 (entries in row order, rows packed in
+    the index words) and 1 (gathers in column order; wherever the panels allow it)."""
+    monkeypatch.setattr(_spmv_layouts, "SORTED_ITEMS", request.param == 1)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 0.0)  # whatever the row lengths
+    return request.param
+
+
+def _sorted_item(layout, e0, ln):
+    """Decode a format-1 item: (memory positions of its values in row order, column in the
+    panel and run-start flag of each row-order position).  Values: position 8t + e at quad
+    (e/4) * P/8 + t; gather words in column order at the same quads, entry (t/64)*512 + 64k +
+    t%64 as element k of thread t.  Checks that the words name every row-order position once,
+    in non-decreasing column order."""
+    sb = _abi.caps()["xcs_sorted_col_bits"]
+    P = -(-ln // 512) * 512
+    thr = P // 8
+    o = np.arange(ln)
+    vpos = e0 + 4 * ((o % 8) // 4 * thr + o // 8) + o % 4
+    t_g = (o // 512) * 64 + o % 64
+    k = (o % 512) // 64
+    gpos = e0 + 4 * (k // 4 * thr + t_g) + k % 4
+    w = layout.pidx.numpy().view(np.uint32)[gpos].astype(np.int64)
+    pos = w >> (sb + 1)
+    colg = w & ((1 << sb) - 1)
+    assert sorted(pos.tolist()) == list(range(ln))  # a permutation of the positions
+    assert np.all(np.diff(colg) >= 0)               # gathers in column order
+    col = np.empty(ln, dtype=np.int64)
+    col[pos] = colg
+    flag = np.empty(ln, dtype=bool)
+    flag[pos] = ((w >> sb) & 1) == 1
+    assert ln == 0 or flag[0]
+    return vpos, col, flag
+
+
+def _combine_slot_rows(layout):
+    """The row of every stored slot according to the combine tables (-1: padding or unused):
+    slot s of window w is at position dest[s], inside row r's positions [row_start[r],
+    row_start[r + 1])."""
+    windows = layout.windows.numpy().reshape(-1, 8).astype(np.int64)
+    dest = layout.dest.numpy().astype(np.int64)
+    row_start = layout.row_start.numpy().astype(np.int64)
+    rows = np.full(layout.n_partials, -1, dtype=np.int64)
+    for row0, nr, base, ln, total, _, _, _ in windows:
+        sl = np.arange(base, base + ln)
+        if nr < 0:
+            rows[sl] = row0
+            continue
+        d = dest[sl]
+        ok = d >= 0
+        starts = row_start[row0:row0 + nr]
+        rows[sl[ok]] = row0 + np.searchsorted(starts, d[ok], side="right") - 1
+    return rows
+
+
 def _item_positions(e0, ln):
     """Memory positions of an item's entries in logical (row) order: thread-major storage with
     Q = ceil(ln/4) quads, qp = ceil(Q/256) quads per thread, nt = ceil(Q/qp) threads, logical
@@ -50,23 +106,39 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
     partials = np.full(n_store, np.nan)
     slot_row = np.full(n_store, -1, dtype=np.int64)  # -2: padding
     slot_item = np.full(n_store, -1, dtype=np.int64)
+    comb_rows = _combine_slot_rows(layout) if layout.item_format == 1 else None
     for e0, ln, k, run0, r0, R, cbase, n_ir, _, _, tile, _ in items:
         if tile < 0:
             continue
         assert 0 <= n_ir <= caps["xcs_item_runs"]
-        pos = _item_positions(e0, ln)
-        p = pidx[pos]
-        lrow = (p >> cbits).astype(np.int64)
-        col = cbase + (p & ((1 << cbits) - 1)).astype(np.int64)
+        if layout.item_format == 1:
+            assert ln <= caps["xcs_sorted_item"]
+            pos, colp, flag = _sorted_item(layout, e0, ln)
+            col = cbase + colp
+            run_of = np.cumsum(flag) - 1  # run index of every row-order position
+        else:
+            pos = _item_positions(e0, ln)
+            p = pidx[pos]
+            lrow = (p >> cbits).astype(np.int64)
+            col = cbase + (p & ((1 << cbits) - 1)).astype(np.int64)
+            assert np.all(np.diff(lrow) >= 0) and np.all(lrow < R)
+            run_of = np.unique(lrow, return_inverse=True)[1].ravel()
         prod = vals[pos] * x[col].astype(acc)
-        assert np.all(np.diff(lrow) >= 0) and np.all(lrow < R)
-        sums, rows = [], []
-        for r in np.unique(lrow):  # runs in row order
+        sums = []
+        for r in range(int(run_of.max()) + 1 if ln else 0):  # runs in row order
             s = acc(0)
-            for v in prod[lrow == r]:
+            for v in prod[run_of == r]:
                 s = acc(s + v)
             sums.append(s)
-            rows.append(r0 + r)
+        if layout.item_format == 1:  # a run's row: where the combine tables place its sum
+            rows = [None] * len(sums)
+            for first, s0, cnt, stored in item_runs[run0:run0 + n_ir]:
+                for j in range(cnt):
+                    rows[s0 + j] = int(comb_rows[first + j])
+            assert all(r is not None and r >= 0 for r in rows)
+            assert all(a < b for a, b in zip(rows, rows[1:]))  # one sum per row, in row order
+        else:
+            rows = [r0 + int(r) for r in np.unique(lrow)]
         nxt = 0
         for first, s0, cnt, stored in item_runs[run0:run0 + n_ir]:
             assert s0 == nxt and stored >= cnt  # the runs take the sums in order
@@ -138,7 +210,8 @@ def _check_structure(layout, data, cols, rowptr):
     caps = _abi.caps()
     items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
     real = items[items[:, 10] >= 0]
-    assert np.all(real[:, 0] % 4 == 0) and np.all(real[:, 1] <= caps["xcs_item"])
+    cap = caps["xcs_sorted_item"] if layout.item_format == 1 else caps["xcs_item"]
+    assert np.all(real[:, 0] % 4 == 0) and np.all(real[:, 1] <= cap)
     assert np.all(real[:, 5] <= layout.rows_cap)
     # slot x*q + j runs on XCD x: every real item of XCD x's range gathers from a panel
     # p with p % 8 == x, and the panels come one after the other
@@ -156,17 +229,32 @@ def _check_structure(layout, data, cols, rowptr):
     vals = layout.vals.numpy()
     cb = layout.panel_base.numpy()
     got = []
+    if layout.item_format == 1:
+        assert np.all(real[:, 0] % 512 == 0) and np.all(real[:, 1] <= caps["xcs_sorted_item"])
+        comb_rows = _combine_slot_rows(layout)
+        item_runs = layout.item_runs.numpy().astype(np.int64)
     for e0, ln, k, S, r0, R, cbase, moff, plo, phi, tile, _ in real:
         panel = max(i for i, b in enumerate(cb) if b == cbase)
-        pos = _item_positions(e0, ln)
+        if layout.item_format == 1:
+            pos, colp, flag = _sorted_item(layout, e0, ln)
+            c = cbase + colp
+            run_of = np.cumsum(flag) - 1
+            run_row = np.full(int(run_of.max()) + 1 if ln else 0, -1, dtype=np.int64)
+            for first, s0, cnt, stored in item_runs[S:S + moff]:
+                run_row[s0:s0 + cnt] = comb_rows[first:first + cnt]
+            assert np.all(run_row >= r0) and np.all(run_row < r0 + R)
+            rows_e = run_row[run_of]
+        else:
+            pos = _item_positions(e0, ln)
+            p = pidx[pos]
+            lr = (p >> layout.col_bits).astype(np.int64)
+            assert np.all(lr < R)
+            c = cbase + (p & ((1 << layout.col_bits) - 1)).astype(np.int64)
+            rows_e = r0 + lr
         assert pos.size == 0 or pos.max() < layout.n_entries
-        p = pidx[pos]
-        lr = (p >> layout.col_bits).astype(np.int64)
-        assert np.all(lr < R)
-        c = cbase + (p & ((1 << layout.col_bits) - 1)).astype(np.int64)
         hi = cb[panel + 1] if panel + 1 < len(cb) else layout.n_cols
         assert np.all((c >= cbase) & (c < hi))
-        got += list(zip((r0 + lr).tolist(), c.tolist(), vals[pos].tolist()))
+        got += list(zip(rows_e.tolist(), c.tolist(), vals[pos].tolist()))
     rp = rowptr.numpy()
     want = [(r, int(cols[i]), float(data[i])) for r in range(rp.size - 1)
             for i in range(rp[r], rp[r + 1])]
@@ -369,22 +457,35 @@ def test_xcs_combine_windows(win_slots, win_rows, monkeypatch):
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
 
 
-def test_xcs_item_run_cap(monkeypatch):
+def test_xcs_item_run_cap(monkeypatch, item_format):
     # an item stores its sums through at most the kernel's number of runs (one per combine
-    # window its rows reach); a layout that needs more is refused, and build_layout then falls
-    # back to row blocks
+    # window its rows reach); a layout that needs more is refused, and build_layout then takes
+    # the row-order items (shorter tiles, fewer windows per item) or, when those do not fit
+    # either, row blocks
     real = _abi.caps()
     rng = np.random.default_rng(3)
     lengths = rng.zipf(2.0, 20000).clip(max=200)
     vals, cols, ip, x = _case(lengths, 60000, 3)
     lay = XcsLayout(vals, cols, ip, 60000, panels_per_xcd=1)
+    assert lay.item_format == item_format
     most = int(lay.item_n_runs.max())
     assert 2 <= most <= real["xcs_item_runs"]
+    fmt0 = XcsLayout(vals, cols, ip, 60000, panels_per_xcd=1, item_format=0)
+    most0 = int(fmt0.item_n_runs.max())
     monkeypatch.setattr(_spmv_layouts._abi, "caps", lambda: dict(real, xcs_item_runs=most - 1))
     with pytest.raises(ValueError):
         XcsLayout(vals, cols, ip, 60000, panels_per_xcd=1)
     monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-l2")
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANELS_PER_XCD", 1)
+    got = _spmv_layouts.build_layout(vals, cols, ip, 60000)
+    if item_format == 1 and most0 < most:
+        assert got.kind == "xcs" and got.item_format == 0
+        np.testing.assert_allclose(_emulate(got, x.numpy()), oracle.spmv_csr(ip, cols, vals, x),
+                                   rtol=1e-12, atol=1e-12)
+    else:
+        assert got.kind == "rowblock"
+    monkeypatch.setattr(_spmv_layouts._abi, "caps",
+                        lambda: dict(real, xcs_item_runs=min(most, most0) - 1))
     assert _spmv_layouts.build_layout(vals, cols, ip, 60000).kind == "rowblock"
 
 
@@ -467,6 +568,23 @@ def test_layout_choice():
     d, i, p, _, shape = synthetic.csr_poisson2d(1024)
     assert not prefers_xcs(i, p, shape[1], 8)
     assert not prefers_xcs(cols, ip, 1 << 20, 4)  # x of 4 MiB fits one L2
+
+
+def test_sorted_item_choice(monkeypatch):
+    # sorted-gather items by default for rows that put several entries into each panel
+    # (cfg4's kind), row-order items for rows of about one entry per panel (cfg3's short rows)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_ITEMS", True)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 3.0)
+    est = _spmv_layouts._entries_per_panel_run
+    assert est(torch.full((1000,), 21), 4) > 5.0
+    assert est(torch.ones(1000, dtype=torch.int64), 16) == 1.0
+    assert est(torch.zeros(10, dtype=torch.int64), 16) == 0.0
+    vals, cols, ip, x = _case([21] * 3000, 60000, 4)
+    assert XcsLayout(vals, cols, ip, 60000).item_format == 1
+    vals, cols, ip, x = _case([2] * 3000, 60000, 4)
+    assert XcsLayout(vals, cols, ip, 60000, panels_per_xcd=2).item_format == 0
+    # mostly one entry per row and panel reached (cfg3's short rows): row-order items
+    assert est(torch.tensor([1] * 100 + [2] * 20 + [50] * 2), 16) < 3.0
 
 
 def test_sample_indices_stay_in_bounds():

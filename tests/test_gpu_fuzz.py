@@ -74,19 +74,34 @@ def _check(y, ref64, exact_fp32):
         assert u.size == 0 or u.max() <= 1, u.max()
 
 
+def _force(monkeypatch, layout):
+    """Force a layout; "-sorted" takes the XCS items with sorted gathers (format 1) wherever
+    the panels allow it, else row-order items (format 0)."""
+    mode = layout.replace("-sorted", "")
+    monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
+    monkeypatch.setattr(_spmv_layouts, "SORTED_ITEMS", layout.endswith("-sorted"))
+    monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 0.0)
+    return mode
+
+
+LAYOUTS = ["rowblock", "xcs-l2", "xcs-l2-sorted", "xcs-hybrid", "xcs-hybrid-sorted"]
+
+
 @pytest.mark.parametrize("seed", range(len(CASES)))
-@pytest.mark.parametrize("layout", ["rowblock", "xcs-l2", "xcs-hybrid"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_fuzz_spmv(dev, monkeypatch, seed, layout):
     kind, rng, vals, cols, ptr, x, shape = _matrix(seed)
-    monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+    layout = _force(monkeypatch, layout)
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", int(rng.integers(2, 64)))
     print(f"fuzz seed={seed} {kind} {layout} shape={shape} nnz={vals.numel()} {vals.dtype}",
           flush=True)
     ref = oracle.spmv_csr(ptr, cols, vals, x)
     d, c, p, xd = vals.to(dev), cols.to(torch.int32).to(dev), ptr.to(dev), x.to(dev)
     prepared = fs.prepare_spmv_csr(d, c, p, shape)
-    built = prepared._kernel(False).kind
-    print(f"  layout built: {built}", flush=True)
+    lay = prepared._kernel(False)
+    built = lay.kind
+    xcs = getattr(lay, "short", lay)
+    print(f"  layout built: {built} item format {getattr(xcs, 'item_format', '-')}", flush=True)
     # the forced layout is the one tested (the hybrid needs a row of FORCE_PANEL_ROW_MIN entries)
     has_long = bool(((ptr[1:] - ptr[:-1]) >= _spmv_layouts.FORCE_PANEL_ROW_MIN).any())
     expect = {"rowblock": "rowblock", "xcs-l2": "xcs",
@@ -165,8 +180,8 @@ def test_fuzz_nonfinite(dev, monkeypatch, seed):
     ref = oracle.spmv_csr(ptr, cols, vals, x)
     d, c, p, xd = vals.to(dev), cols.to(torch.int32).to(dev), ptr.to(dev), x.to(dev)
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", int(rng.integers(2, 64)))
-    for layout in ("rowblock", "xcs-l2", "xcs-hybrid"):
-        monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
+    for layout in LAYOUTS:
+        _force(monkeypatch, layout)
         prepared = fs.prepare_spmv_csr(d, c, p, shape)
         for use_opt in (False, True):
             _check_nonfinite(fs.flagsparse_spmv_csr(x=xd, prepared=prepared, use_opt=use_opt),

@@ -94,9 +94,14 @@ WINDOW_ALIGN = 16
 # XCS items with sorted gathers (item format 1, spmv_xcs_sorted_kernel): up to 4096 entries
 # per item, the gathers issued in column order so that the lanes of one instruction reach
 # neighbouring lines; used when the panels need at most 19 column bits.  Tiles of up to
-# SORTED_TILE_ROWS rows, so that a tile's share of a panel fills an item.
+# SORTED_TILE_ROWS rows (rows are not packed into the entries).
 SORTED_ITEMS = True
 SORTED_TILE_ROWS = 16384
+# A tile holds up to this many items' worth of entries per panel, so that its pieces split
+# into nearly full items (tiles of one item per panel left pieces just over 4096 entries as
+# two half items: cfg4 items of 2771 entries on average, 3856 here; 203.9 -> 199.4 us a call,
+# 2 and 4 in between).
+SORTED_TILE_ITEMS = 8
 # ... for matrices whose rows put at least this many entries, on average, into each panel they
 # reach.  Measured on MI355X: cfg4 (rows of 21 entries over 4 panels, 5.3 per panel) 193 ->
 # 186 us in the XCS kernel; cfg3's short rows (2.0 per panel: most rows put one entry into
@@ -308,7 +313,7 @@ class XcsLayout:
         #    partials are one value per item).  The other rows are covered greedily by tiles
         #    of <= rows_cap consecutive rows and <= 8 * item_cap entries, in which the long
         #    rows are rows without entries - they do not cut the run of short rows.
-        tile_nnz = P * item_cap
+        tile_nnz = P * item_cap * (SORTED_TILE_ITEMS if self.item_format == 1 else 1)
         long_mask = lengths > tile_nnz
         long_rows = torch.nonzero(long_mask).flatten()
         short_ptr = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)

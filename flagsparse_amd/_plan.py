@@ -91,6 +91,12 @@ class StreamOrder:
         """The raw handle of torch's current stream on ``device``, ordered after the previous
         user's work when it differs."""
         s = _abi.raw_stream(device)
+        if torch.cuda.is_current_stream_capturing():
+            # A graph being captured: nothing runs now, and a wait on an event recorded
+            # outside the capture cannot be recorded into it.  Replays run in the order of
+            # the stream they are replayed on; ordering them against eager calls of the
+            # same object on other streams is the caller's (as for the graph's inputs).
+            return s
         last = self._last
         if last is not None and s != last:
             old = torch.cuda.ExternalStream(last, device=device)

@@ -24,7 +24,8 @@ The layouts below, chosen once per matrix at prepare time:
 
 ``XcsHybridLayout``
     ``PanelLayout`` for the rows long enough to put several entries in every panel,
-    ``XcsLayout`` for the others; two launches one after the other on the same stream.
+    ``XcsLayout`` for the others; the panel kernel runs on a second stream beside the XCS
+    kernel, and the panel combine follows the XCS part's on the caller's stream.
 
 Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produce the same
 row sums up to floating-point summation order.
@@ -79,6 +80,9 @@ BAND_MIN_SHARE = 0.2
 # >= 256 / 512 / 768 / 1024 / 2048 entries) 0.302 / 0.289 / 0.289 / 0.290 / 0.309 ms with
 # 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms.
 PANEL_JOB_CHUNKS = 1024
+# The XCS + panel hybrid runs its panel kernel on a second stream beside the XCS kernel
+# (False: the two parts one after the other on the caller's stream).
+HYBRID_SIDE_STREAM = True
 PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
@@ -816,7 +820,9 @@ class PanelLayout:
                 "chunks": self.n_entries // _abi.caps()["panel_chunk"],
                 "partials": self.n_partials, "padded_entries": self.n_entries}
 
-    def launch(self, x, y, acc_f64, row_map=None):
+    def launch(self, x, y, acc_f64, row_map=None, passes=3, stream=None):
+        """Both passes on the caller's stream (passes=3), or only the entry pass (1) or only
+        the combine (2) on the raw ``stream`` given."""
         args = self._args.get(bool(acc_f64))
         if args is None:  # static arguments converted once per accumulation mode
             p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
@@ -829,21 +835,27 @@ class PanelLayout:
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
         a[9] = None if row_map is None else row_map.data_ptr()
-        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pcol, self.jobs,
-                                              self.job_panel, self.chunk_info, self.rows,
-                                              self.row_ptr, self.slots))
+        if not passes & 1:
+            a[12] = 0
+        if not passes & 2:
+            a[19] = 0
+        a[20] = stream if stream is not None else self._order.stream(
+            y.device, (self.partials, self.vals, self.pcol, self.jobs, self.job_panel,
+                       self.chunk_info, self.rows, self.row_ptr, self.slots))
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 
 
 class XcsHybridLayout:
     """Long rows in a PanelLayout, the rest in an XcsLayout (module docstring).  The XCS part
-    sees the long rows as rows without entries and writes them as 0; the panel part, launched
-    after it on the same stream, then writes their sums.  Measured on MI355X (cfg3, 281 us in
-    this order): the panel kernel on a second stream beside the XCS kernel 277.5 us (a CU that
-    holds a panel workgroup, 128 KiB of LDS and 16 waves, has room for one XCS workgroup, so
-    the two mostly take turns), the two combines side by side 282.5 us, the panel kernel beside
-    the XCS combine 292 us (two HBM streams); not worth a second stream per call."""
+    sees the long rows as rows without entries and writes them as 0; the panel part's combine,
+    launched after it on the caller's stream, then writes their sums.  The panel kernel runs
+    on a second stream beside the XCS kernel (HYBRID_SIDE_STREAM): measured on MI355X, cfg3,
+    277.5 us against 281 us with everything on one stream (a CU that holds a panel workgroup,
+    128 KiB of LDS and 16 waves, has room for one XCS workgroup, so the two kernels mostly
+    take turns, and the gain is the tail of one filled by the other).  Also measured: the two
+    combines side by side 282.5 us, the panel kernel beside the XCS combine 292 us (two HBM
+    streams)."""
 
     kind = "xcs-hybrid"
 
@@ -861,6 +873,7 @@ class XcsHybridLayout:
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
         self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
+        self._side = {}  # device index -> (second stream, fork event, join event)
 
     def kernel_name(self):
         return "spmv_xcs_kernel+spmv_panel_kernel"
@@ -874,8 +887,29 @@ class XcsHybridLayout:
                 "panel_part": self.long.describe()}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
+        if not HYBRID_SIDE_STREAM:
+            self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
+            self.long.launch(x, y, acc_f64, row_map)
+            return y
+        # The panel kernel on a second stream (default priority) that starts after the work
+        # queued on the caller's stream and that the caller's stream waits for before the
+        # panel combine: the fork and join are inside the caller's order, so a graph capture
+        # records them too.
+        dev = y.device
+        main = self.long._order.stream(dev, (self.long.partials,))
+        side = self._side.get(dev.index)
+        if side is None:
+            side = (torch.cuda.Stream(device=dev), torch.cuda.Event(), torch.cuda.Event())
+            self._side[dev.index] = side
+        s2, ev_fork, ev_join = side
+        cur = torch.cuda.current_stream(dev)
+        ev_fork.record(cur)
+        s2.wait_event(ev_fork)
+        self.long.launch(x, y, acc_f64, row_map, passes=1, stream=s2.cuda_stream)
         self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
-        self.long.launch(x, y, acc_f64, row_map)
+        ev_join.record(s2)
+        cur.wait_event(ev_join)
+        self.long.launch(x, y, acc_f64, row_map, passes=2, stream=main)
         return y
 
 

@@ -83,6 +83,7 @@ PANEL_JOB_CHUNKS = 1024
 # The XCS + panel hybrid runs its panel kernel on a second stream beside the XCS kernel
 # (False: the two parts one after the other on the caller's stream).
 HYBRID_SIDE_STREAM = True
+_SIDE_STREAMS = {}  # device index -> the second stream (default priority)
 PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
@@ -873,7 +874,7 @@ class XcsHybridLayout:
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
         self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
-        self._side = {}  # device index -> (second stream, fork event, join event)
+        self._events = {}  # device index -> (fork event, join event)
 
     def kernel_name(self):
         return "spmv_xcs_kernel+spmv_panel_kernel"
@@ -897,11 +898,13 @@ class XcsHybridLayout:
         # records them too.
         dev = y.device
         main = self.long._order.stream(dev, (self.long.partials,))
-        side = self._side.get(dev.index)
-        if side is None:
-            side = (torch.cuda.Stream(device=dev), torch.cuda.Event(), torch.cuda.Event())
-            self._side[dev.index] = side
-        s2, ev_fork, ev_join = side
+        s2 = _SIDE_STREAMS.get(dev.index)
+        if s2 is None:  # one per device, shared by every hybrid layout on it
+            s2 = _SIDE_STREAMS.setdefault(dev.index, torch.cuda.Stream(device=dev))
+        events = self._events.get(dev.index)
+        if events is None:
+            events = self._events.setdefault(dev.index, (torch.cuda.Event(), torch.cuda.Event()))
+        ev_fork, ev_join = events
         cur = torch.cuda.current_stream(dev)
         ev_fork.record(cur)
         s2.wait_event(ev_fork)

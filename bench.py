@@ -26,12 +26,15 @@ roofline     the same bytes / the path's kernel time (all the kernels of one lau
              workload's own gather count and pattern - the rate the gathers alone reach;
              ``kernel_ms_over_bound`` divides the whole path's kernel time by it, and for cfg3
              ``part_ms_over_bound`` the XCS part's (its kernel and combine, ``parts_ms``)
-cpu_baseline the C oracle (fp64 restatement, one core) on the same arrays for ~10 s of passes
-             (a bounded row sample for SpMM), reported only, never a target
+cpu_baseline the reference's own CPU path (its tests' torch comparison): torch.sparse.mm on
+             CPU sparse tensors of the same matrix, on all of torch's host threads (``cores``,
+             OMP_NUM_THREADS: the box's CPU share), ~10 s of full products, with the same byte
+             and flop counts ("kind": "reference"); reported only, never a target.  For the
+             workloads without one (SDDMM, COO SpMM) the C oracle
+cpu_port     the C oracle (fp64 restatement, one core) on the same arrays, ~5 s of passes (a
+             bounded row sample for SpMM)
 cpu_reference_path
-             the reference's own CPU path - scipy.sparse (one core) and torch's CPU sparse
-             product (torch's thread count) - on the same matrix, a few seconds each, with
-             the same byte and flop counts; reported only
+             scipy.sparse (one core) on the same matrix, ~5 s
 config       also ``lib_load_ms`` (loading the HIP library, once per process), ``prepare_ms``
              (the prepare call and the first layout build, synchronised; ``prepare_call_ms``
              and ``layout_build_ms`` separately), ``plan.layout_bytes`` (device memory the
@@ -110,7 +113,8 @@ def _parse():
     ap.add_argument("--opt", action="store_true",
                     help="SpMV: use_opt=True (native accumulation) instead of the default path")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="CPU baseline: seconds of oracle passes")
+                    help="CPU baseline: seconds of torch CPU products (the C oracle and "
+                         "scipy half as long each)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-targets", action="store_true",
                     help="skip the north_star target measurements")
@@ -209,34 +213,17 @@ def _time_passes(fn, seconds, max_passes=10000):
             return passes, secs
 
 
-def _cpu_reference_path(fmt, mats, rhs, shape, seconds, nbytes, flops, torch):
-    """The reference's CPU path for the product: scipy.sparse (single-threaded) and torch's CPU
-    sparse tensors (torch.get_num_threads() threads), each on the host copy of the same
-    matrix and right-hand side.  fmt "csr": mats = (indptr, indices, data); "coo": (row, col,
-    data)."""
+def _cpu_torch(fmt, mats, rhs, shape, seconds, nbytes, flops, torch):
+    """The reference's CPU path (its tests' torch comparison, tests/test_spmv.py:143-174):
+    torch.sparse.mm on CPU sparse tensors built from the host copy of the same matrix and
+    right-hand side, on all of torch's host threads (torch.get_num_threads(), which follows
+    OMP_NUM_THREADS: the box's CPU share).  fmt "csr": mats = (indptr, indices, data); "coo":
+    (row, col, data)."""
     import warnings
-
-    import numpy as np
-    import scipy.sparse as sp
 
     warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
     a, b, data = (t.detach().cpu() for t in mats)
     r = rhs.detach().cpu()
-    out = {}
-    try:
-        if fmt == "csr":
-            A = sp.csr_matrix((data.numpy(), b.numpy(), a.numpy()), shape=shape)
-        else:
-            A = sp.coo_matrix((data.numpy(), (a.numpy(), b.numpy())), shape=shape).tocsr()
-        rn = np.ascontiguousarray(r.numpy())
-        passes, secs = _time_passes(lambda: A @ rn, seconds)
-        out["scipy"] = {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
-                        "gflops": round(flops * passes / secs / 1e9, 3), "cores": 1,
-                        "sample": f"{passes} full products (scipy.sparse csr_matrix @ dense, "
-                                  f"{data.dtype}) in {secs:.1f} s"
-                                  + ("; COO converted to CSR first" if fmt == "coo" else "")}
-    except Exception as exc:  # report, never fail the benchmark
-        out["scipy"] = {"error": f"{type(exc).__name__}: {exc}"}
     try:
         if fmt == "csr":
             At = torch.sparse_csr_tensor(a.to(torch.int64), b.to(torch.int64), data, size=shape)
@@ -245,14 +232,45 @@ def _cpu_reference_path(fmt, mats, rhs, shape, seconds, nbytes, flops, torch):
                                          size=shape).coalesce()
         rt = r if r.dim() == 2 else r.unsqueeze(1)
         passes, secs = _time_passes(lambda: torch.sparse.mm(At, rt), seconds)
-        out["torch"] = {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
-                        "gflops": round(flops * passes / secs / 1e9, 3),
-                        "cores": torch.get_num_threads(),
-                        "sample": f"{passes} full products (torch.sparse.mm, {fmt.upper()} "
-                                  f"on the CPU, {data.dtype}) in {secs:.1f} s"}
-    except Exception as exc:
-        out["torch"] = {"error": f"{type(exc).__name__}: {exc}"}
-    return out
+    except Exception as exc:  # report, never fail the benchmark
+        return {"error": f"{type(exc).__name__}: {exc}", "kind": "reference"}
+    return {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "reference",
+            "path": f"torch.sparse.mm, {fmt.upper()} on the CPU",
+            "sample": f"{passes} full products (torch.sparse.mm, {fmt.upper()} on the CPU, "
+                      f"{data.dtype}, {torch.get_num_threads()} threads) over the whole "
+                      f"matrix in {secs:.1f} s",
+            "gflops": round(flops * passes / secs / 1e9, 3)}
+
+
+def _cpu_scipy(fmt, mats, rhs, shape, seconds, nbytes, flops):
+    """scipy.sparse (single-threaded) on the host copy of the same matrix and right-hand side:
+    the other CPU library the reference's scripts compare against."""
+    import numpy as np
+    import scipy.sparse as sp
+
+    a, b, data = (t.detach().cpu() for t in mats)
+    r = rhs.detach().cpu()
+    try:
+        if fmt == "csr":
+            A = sp.csr_matrix((data.numpy(), b.numpy(), a.numpy()), shape=shape)
+        else:
+            A = sp.coo_matrix((data.numpy(), (a.numpy(), b.numpy())), shape=shape).tocsr()
+        rn = np.ascontiguousarray(r.numpy())
+        passes, secs = _time_passes(lambda: A @ rn, seconds)
+    except Exception as exc:  # report, never fail the benchmark
+        return {"error": f"{type(exc).__name__}: {exc}"}
+    return {"value": round(nbytes * passes / secs / 1e9, 3), "unit": "GB/s",
+            "gflops": round(flops * passes / secs / 1e9, 3), "cores": 1,
+            "sample": f"{passes} full products (scipy.sparse csr_matrix @ dense, "
+                      f"{data.dtype}) in {secs:.1f} s"
+                      + ("; COO converted to CSR first" if fmt == "coo" else "")}
+
+
+def _cpu_lib(fmt, mats, rhs, shape, nbytes, flops, torch):
+    """(torch timer, scipy timer) for a workload: each takes the seconds to spend."""
+    return (lambda s: _cpu_torch(fmt, mats, rhs, shape, s, nbytes, flops, torch),
+            lambda s: _cpu_scipy(fmt, mats, rhs, shape, s, nbytes, flops))
 
 
 def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
@@ -330,8 +348,7 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         "parts": parts, "gather_bound": gather_bound, "bound_part": "xcs_part",
         "bytes_gather_inclusive": nnz * (v + 4 + v) + (shape[0] + 1) * p_k + shape[0] * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
-        "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), x, shape,
-                                                       seconds, nbytes, 2 * nnz, torch),
+        "cpu_lib": _cpu_lib("csr", (ptr, idx, data), x, shape, nbytes, 2 * nnz, torch),
         "dtype": "f64" if data.dtype == torch.float64 else "f32",
         "kernel": kc.kernel_name(), "tag": f"{_tag(kc.kernel_name())}_{name}",
     }
@@ -373,8 +390,7 @@ def _spmv_coo_workload(dev, torch, fs, synthetic):
         "launch": lambda: mod._run_spmv_coo(prepared, x, y, 256),
         "bytes_gather_inclusive": nbytes - shape[1] * v + nnz * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu, "dtype": "f32",
-        "cpu_lib": lambda seconds: _cpu_reference_path("coo", (row, col, data), x, shape,
-                                                       seconds, nbytes, 2 * nnz, torch),
+        "cpu_lib": _cpu_lib("coo", (row, col, data), x, shape, nbytes, 2 * nnz, torch),
         "kernel": prepared._kernel_name(), "tag": f"{_tag(prepared._kernel_name())}_cfg4",
     }
 
@@ -436,8 +452,7 @@ def _spmm_workload(dev, dtype_name, N, torch, fs, synthetic, part="all"):
         "bytes_gather_inclusive": nnz * (v + 4 + N * v) + (shape[0] + 1) * p_k +
         shape[0] * N * v,
         "nbytes": nbytes, "flops": 2 * nnz * N, "info": info, "cpu": cpu,
-        "cpu_lib": lambda seconds: _cpu_reference_path("csr", (ptr, idx, data), B, shape,
-                                                       seconds, nbytes, 2 * nnz * N, torch),
+        "cpu_lib": _cpu_lib("csr", (ptr, idx, data), B, shape, nbytes, 2 * nnz * N, torch),
         "dtype": dtype_name, "kernel": kc.kernel_name(),
         "tag": f"{kc.kernel_name()}_cfg5_{dtype_name}_n{N}" + ("" if part == "all" else
                                                                 f"_{part}_half"),
@@ -767,6 +782,22 @@ def _roofline(w, ms_kernel, kernel_runs, torch):
     return out
 
 
+def _cpu_baselines(w, seconds, torch):
+    """(cpu_baseline, cpu_port, cpu_reference_path) of a workload.  cpu_baseline: the
+    reference's own CPU path (torch.sparse.mm on all of torch's host threads) for ``seconds``
+    where the workload has one, else the C oracle; cpu_port: the fp64 C oracle on one core;
+    cpu_reference_path: scipy.sparse on one core.  Reported only, never a target."""
+    host = _host_info(torch)
+    if w.get("cpu_lib") is None:
+        port = w["cpu"](seconds)
+        port["host"] = host
+        return port, None, None
+    torch_fn, scipy_fn = w["cpu_lib"]
+    base = torch_fn(seconds)
+    base["host"] = host
+    return base, w["cpu"](seconds / 2), {"scipy": scipy_fn(seconds / 2)}
+
+
 def _target(name, args, dev, torch, steps, cpu_seconds):
     class A:
         pass
@@ -781,9 +812,8 @@ def _target(name, args, dev, torch, steps, cpu_seconds):
            "roofline": _roofline(w, ms_kernel, runs, torch),
            "prepare_ms": w["info"].get("prepare_ms"), "plan": w["info"].get("plan")}
     if cpu_seconds > 0 and w["cpu"] is not None:
-        out["cpu_baseline"] = w["cpu"](cpu_seconds)
-        if w.get("cpu_lib") is not None:
-            out["cpu_reference_path"] = w["cpu_lib"](cpu_seconds / 2)
+        out["cpu_baseline"], out["cpu_port"], out["cpu_reference_path"] = \
+            _cpu_baselines(w, cpu_seconds, torch)
     del w
     torch.cuda.empty_cache()
     return out
@@ -818,12 +848,9 @@ def main():
     nbytes, flops = w["nbytes"], w["flops"]
     value = nbytes / (ms_step * 1e-3) / 1e9
     roofline = _roofline(w, ms_kernel, kernel_runs, torch)
-    cpu = cpu_lib = None
+    cpu = cpu_port = cpu_lib = None
     if w["cpu"] is not None and not args.no_cpu and args.cpu_seconds > 0:
-        cpu = w["cpu"](args.cpu_seconds)
-        cpu["host"] = _host_info(torch)
-        if w.get("cpu_lib") is not None:
-            cpu_lib = w["cpu_lib"](args.cpu_seconds / 2)
+        cpu, cpu_port, cpu_lib = _cpu_baselines(w, args.cpu_seconds, torch)
     workload = f"{args.workload}: {WORKLOADS[args.workload]}"
     if args.workload in ("cfg5", "coo5"):
         workload = f"{args.workload} ({w['dtype']}, N={args.n}): {WORKLOADS[args.workload]}"
@@ -873,6 +900,7 @@ def main():
                        host_wall_ms_per_step=round(wall_ms, 6)),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_port": cpu_port,
         "cpu_reference_path": cpu_lib,
         "targets": targets,
     }

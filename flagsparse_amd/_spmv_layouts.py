@@ -31,6 +31,8 @@ Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produ
 row sums up to floating-point summation order.
 """
 
+import threading
+
 import numpy as np
 import torch
 
@@ -83,7 +85,10 @@ PANEL_JOB_CHUNKS = 1024
 # The XCS + panel hybrid runs its panel kernel on a second stream beside the XCS kernel
 # (False: the two parts one after the other on the caller's stream).
 HYBRID_SIDE_STREAM = True
-_SIDE_STREAMS = {}  # device index -> the second stream (default priority)
+# The second streams, one per (thread, device), default priority: a thread capturing a graph
+# holds its own side stream in capture state between the fork and the join, and eager calls
+# made meanwhile from other threads go to theirs.
+_SIDE_STREAMS = threading.local()
 PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
@@ -804,6 +809,9 @@ class PanelLayout:
         self.n_jobs = int(self.job_panel.numel())
         self.n_panels = n_panels
         self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+        # every array a launch reads or writes (marked as used on a new caller stream)
+        self._keep = (self.partials, self.vals, self.pcol, self.jobs, self.job_panel,
+                      self.chunk_info, self.rows, self.row_ptr, self.slots)
         self._args = {}
         self._order = StreamOrder(dev)
 
@@ -840,9 +848,7 @@ class PanelLayout:
             a[12] = 0
         if not passes & 2:
             a[19] = 0
-        a[20] = stream if stream is not None else self._order.stream(
-            y.device, (self.partials, self.vals, self.pcol, self.jobs, self.job_panel,
-                       self.chunk_info, self.rows, self.row_ptr, self.slots))
+        a[20] = stream if stream is not None else self._order.stream(y.device, self._keep)
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 
@@ -897,10 +903,10 @@ class XcsHybridLayout:
         # panel combine: the fork and join are inside the caller's order, so a graph capture
         # records them too.
         dev = y.device
-        main = self.long._order.stream(dev, (self.long.partials,))
-        s2 = _SIDE_STREAMS.get(dev.index)
-        if s2 is None:  # one per device, shared by every hybrid layout on it
-            s2 = _SIDE_STREAMS.setdefault(dev.index, torch.cuda.Stream(device=dev))
+        # both passes read the panel part's arrays: ordered after their previous user, and
+        # marked as used on the caller's stream, which waits for the side stream at the join
+        main = self.long._order.stream(dev, self.long._keep)
+        s2 = side_stream(dev)
         events = self._events.get(dev.index)
         if events is None:
             events = self._events.setdefault(dev.index, (torch.cuda.Event(), torch.cuda.Event()))
@@ -914,6 +920,17 @@ class XcsHybridLayout:
         cur.wait_event(ev_join)
         self.long.launch(x, y, acc_f64, row_map, passes=2, stream=main)
         return y
+
+
+def side_stream(dev):
+    """The calling thread's second stream on ``dev`` (created on first use)."""
+    streams = getattr(_SIDE_STREAMS, "by_device", None)
+    if streams is None:
+        streams = _SIDE_STREAMS.by_device = {}
+    s2 = streams.get(dev.index)
+    if s2 is None:
+        s2 = streams[dev.index] = torch.cuda.Stream(device=dev)
+    return s2
 
 
 def sample_indices(n, k, device):

@@ -54,3 +54,24 @@ def test_probe_group_indices():
             assert bool((wave[:, 1:] >= wave[:, :-1]).all())
     plain = bench._probe_indices(n, hi, True, "cpu", torch, 4096)
     assert torch.equal(plain.to(torch.int64) // (hi // 8), torch.arange(n) // 4096 % 8)
+
+
+def test_cpu_baselines_block():
+    # cpu_baseline is the reference's own CPU path (torch.sparse.mm on torch's host threads);
+    # the C oracle port and scipy are reported beside it under their own keys
+    import torch
+
+    ptr = torch.tensor([0, 2, 3, 5], dtype=torch.int64)
+    idx = torch.tensor([0, 2, 1, 0, 2], dtype=torch.int64)
+    data = torch.tensor([1.0, 2.0, 3.0, 4.0, 5.0])
+    x = torch.tensor([1.0, -1.0, 0.5])
+    w = {"cpu": lambda s: {"value": 1.0, "unit": "GB/s", "cores": 1, "kind": "port"},
+         "cpu_lib": bench._cpu_lib("csr", (ptr, idx, data), x, (3, 3), 100, 10, torch)}
+    base, port, ref = bench._cpu_baselines(w, 0.01, torch)
+    assert base["kind"] == "reference" and "torch.sparse.mm" in base["path"], base
+    assert base["cores"] == torch.get_num_threads() and base["value"] > 0
+    assert "host" in base and port["kind"] == "port"
+    assert ref["scipy"]["cores"] == 1 and ref["scipy"]["value"] > 0
+    # a workload without a library path reports the port as its baseline
+    only_port = bench._cpu_baselines({"cpu": w["cpu"]}, 0.01, torch)
+    assert only_port[0]["kind"] == "port" and only_port[1] is None and only_port[2] is None

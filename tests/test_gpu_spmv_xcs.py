@@ -92,12 +92,15 @@ def test_edges(dev, force_xcs, lengths, dtype):
                exact_fp32=(dtype == torch.float32 and not use_opt))
 
 
-@pytest.mark.parametrize("lengths,n_cols", [
+HYBRID_EDGES = [
     ([40] * 3000, 1 << 20),                              # every row long: empty XCS part
     ([40, 0, 3, 100, 1] * 600, 5000),                    # x of one small panel (13 bits)
     ([33] * 1000 + [31] * 1000 + [32] * 1000, 70001),    # rows at the threshold; ragged panels
     ([5000] + [0] * 3000 + [2] * 3000 + [7000], 300000),  # two long rows, short rows between
-])
+]
+
+
+@pytest.mark.parametrize("lengths,n_cols", HYBRID_EDGES)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype):
     monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
@@ -112,6 +115,63 @@ def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype):
         _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))
     # a second call on the same layout reuses its partial buffers: same result, bit for bit
     assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=True))
+
+
+@pytest.mark.parametrize("lengths,n_cols", HYBRID_EDGES[1:])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_hybrid_side_stream_bit_identical(dev, monkeypatch, lengths, n_cols, dtype):
+    # the panel kernel on the second stream beside the XCS kernel, or both parts one after
+    # the other on the caller's stream: the same kernels over the same arrays, so the same
+    # bits, and both within the oracle bars
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 22, dtype)
+    print(f"hybrid side stream rows={len(lengths)} n_cols={n_cols} {dtype}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    assert p._kernel(False).kind == "xcs-hybrid"
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        ys = {}
+        for side in (True, False):
+            monkeypatch.setattr(_spmv_layouts, "HYBRID_SIDE_STREAM", side)
+            ys[side] = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
+            _check(ys[side], ref, exact_fp32=(dtype == torch.float32 and not use_opt))
+        assert torch.equal(ys[True], ys[False])
+
+
+def test_hybrid_marks_every_panel_array(dev, monkeypatch):
+    # A hybrid built on one stream and called from another: the caller's stream must be
+    # ordered after the build stream, and every array the panel kernel and its combine read
+    # must be marked as used on it (the side stream's work is joined into it), so that the
+    # allocator does not hand their memory out while the panel kernel may still read it.
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    lengths, n_cols = HYBRID_EDGES[3]
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 23, torch.float32)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    layout = p._kernel(False)
+    assert layout.kind == "xcs-hybrid"
+    seen = []
+    real = _spmv_layouts.StreamOrder.stream
+
+    def spy(self, device, tensors=()):
+        seen.append((self, tuple(tensors)))
+        return real(self, device, tensors)
+
+    monkeypatch.setattr(_spmv_layouts.StreamOrder, "stream", spy)
+    side = torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p)
+    torch.cuda.synchronize()
+    panel = layout.long
+    wanted = (panel.partials, panel.vals, panel.pcol, panel.jobs, panel.job_panel,
+              panel.chunk_info, panel.rows, panel.row_ptr, panel.slots)
+    got = [ts for order, ts in seen if order is panel._order]
+    assert got, "the panel part's stream order was not consulted"
+    for t in wanted:
+        assert any(any(u is t for u in ts) for ts in got), "a panel array was not marked"
+    _check(y, oracle.spmv_csr(ptr, idx, data, x), exact_fp32=True)
 
 
 def test_unsorted_duplicates_and_truncation(dev, force_xcs):

@@ -24,14 +24,11 @@ The layouts below, chosen once per matrix at prepare time:
 
 ``XcsHybridLayout``
     ``PanelLayout`` for the rows long enough to put several entries in every panel,
-    ``XcsLayout`` for the others; the panel kernel runs on a second stream beside the XCS
-    kernel, and the panel combine follows the XCS part's on the caller's stream.
+    ``XcsLayout`` for the others; both parts run one after the other on the caller's stream.
 
 Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produce the same
 row sums up to floating-point summation order.
 """
-
-import threading
 
 import numpy as np
 import torch
@@ -82,13 +79,6 @@ BAND_MIN_SHARE = 0.2
 # >= 256 / 512 / 768 / 1024 / 2048 entries) 0.302 / 0.289 / 0.289 / 0.290 / 0.309 ms with
 # 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms.
 PANEL_JOB_CHUNKS = 1024
-# The XCS + panel hybrid runs its panel kernel on a second stream beside the XCS kernel
-# (False: the two parts one after the other on the caller's stream).
-HYBRID_SIDE_STREAM = True
-# The second streams, one per (thread, device), default priority: a thread capturing a graph
-# holds its own side stream in capture state between the fork and the join, and eager calls
-# made meanwhile from other threads go to theirs.
-_SIDE_STREAMS = threading.local()
 PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
@@ -856,12 +846,15 @@ class PanelLayout:
 class XcsHybridLayout:
     """Long rows in a PanelLayout, the rest in an XcsLayout (module docstring).  The XCS part
     sees the long rows as rows without entries and writes them as 0; the panel part's combine,
-    launched after it on the caller's stream, then writes their sums.  The panel kernel runs
-    on a second stream beside the XCS kernel (HYBRID_SIDE_STREAM): measured on MI355X, cfg3,
-    277.5 us against 281 us with everything on one stream (a CU that holds a panel workgroup,
-    128 KiB of LDS and 16 waves, has room for one XCS workgroup, so the two kernels mostly
-    take turns, and the gain is the tail of one filled by the other).  Also measured: the two
-    combines side by side 282.5 us, the panel kernel beside the XCS combine 292 us (two HBM
+    launched after it on the caller's stream, then writes their sums.
+
+    Both parts run one after the other on the caller's stream.  Measured on MI355X, cfg3: the
+    panel kernel on a second stream beside the XCS kernel (fork and join events around it)
+    took 275.8 us per call against 279.2 us serial, 1.2 %: a CU that holds a panel workgroup
+    (128 KiB of LDS) has no room for an XCS workgroup, so the two kernels take turns and only
+    their tails overlap; with the XCS kernel's LDS claim cut so that one of its workgroups
+    fits beside a panel workgroup, 282.0 us.  Also measured: the two combines side by side
+    282.5 us against 281 us, the panel kernel beside the XCS combine 292 us (two HBM
     streams)."""
 
     kind = "xcs-hybrid"
@@ -880,7 +873,6 @@ class XcsHybridLayout:
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
         self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
-        self._events = {}  # device index -> (fork event, join event)
 
     def kernel_name(self):
         return "spmv_xcs_kernel+spmv_panel_kernel"
@@ -894,43 +886,9 @@ class XcsHybridLayout:
                 "panel_part": self.long.describe()}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
-        if not HYBRID_SIDE_STREAM:
-            self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
-            self.long.launch(x, y, acc_f64, row_map)
-            return y
-        # The panel kernel on a second stream (default priority) that starts after the work
-        # queued on the caller's stream and that the caller's stream waits for before the
-        # panel combine: the fork and join are inside the caller's order, so a graph capture
-        # records them too.
-        dev = y.device
-        # both passes read the panel part's arrays: ordered after their previous user, and
-        # marked as used on the caller's stream, which waits for the side stream at the join
-        main = self.long._order.stream(dev, self.long._keep)
-        s2 = side_stream(dev)
-        events = self._events.get(dev.index)
-        if events is None:
-            events = self._events.setdefault(dev.index, (torch.cuda.Event(), torch.cuda.Event()))
-        ev_fork, ev_join = events
-        cur = torch.cuda.current_stream(dev)
-        ev_fork.record(cur)
-        s2.wait_event(ev_fork)
-        self.long.launch(x, y, acc_f64, row_map, passes=1, stream=s2.cuda_stream)
         self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
-        ev_join.record(s2)
-        cur.wait_event(ev_join)
-        self.long.launch(x, y, acc_f64, row_map, passes=2, stream=main)
+        self.long.launch(x, y, acc_f64, row_map)
         return y
-
-
-def side_stream(dev):
-    """The calling thread's second stream on ``dev`` (created on first use)."""
-    streams = getattr(_SIDE_STREAMS, "by_device", None)
-    if streams is None:
-        streams = _SIDE_STREAMS.by_device = {}
-    s2 = streams.get(dev.index)
-    if s2 is None:
-        s2 = streams[dev.index] = torch.cuda.Stream(device=dev)
-    return s2
 
 
 def sample_indices(n, k, device):

@@ -117,33 +117,11 @@ def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype):
     assert torch.equal(y, fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=True))
 
 
-@pytest.mark.parametrize("lengths,n_cols", HYBRID_EDGES[1:])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_hybrid_side_stream_bit_identical(dev, monkeypatch, lengths, n_cols, dtype):
-    # the panel kernel on the second stream beside the XCS kernel, or both parts one after
-    # the other on the caller's stream: the same kernels over the same arrays, so the same
-    # bits, and both within the oracle bars
-    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
-    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
-    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 22, dtype)
-    print(f"hybrid side stream rows={len(lengths)} n_cols={n_cols} {dtype}", flush=True)
-    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
-    assert p._kernel(False).kind == "xcs-hybrid"
-    ref = oracle.spmv_csr(ptr, idx, data, x)
-    for use_opt in (False, True):
-        ys = {}
-        for side in (True, False):
-            monkeypatch.setattr(_spmv_layouts, "HYBRID_SIDE_STREAM", side)
-            ys[side] = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
-            _check(ys[side], ref, exact_fp32=(dtype == torch.float32 and not use_opt))
-        assert torch.equal(ys[True], ys[False])
-
-
 def test_hybrid_marks_every_panel_array(dev, monkeypatch):
     # A hybrid built on one stream and called from another: the caller's stream must be
     # ordered after the build stream, and every array the panel kernel and its combine read
-    # must be marked as used on it (the side stream's work is joined into it), so that the
-    # allocator does not hand their memory out while the panel kernel may still read it.
+    # must be marked as used on it, so that the allocator does not hand their memory out while
+    # the panel kernel may still read it.
     monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
     lengths, n_cols = HYBRID_EDGES[3]

@@ -470,17 +470,20 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 //      and shared out among all the threads (measured on MI355X, cfg3: 42.5 -> 40.8 us; each
 //      wave had run its row loops as long as its longest row).
 // A window of one row with more sums than LDS holds ({row, -1, ...}: a row longer than a
-// tile) is summed by the whole workgroup - thread t takes its slots t, t + 256, ... in order,
+// tile) is summed by the whole workgroup - thread t takes its slots t, t + NB, ... in order,
 // then the fixed workgroup tree.
 // A separate launch: the kernel boundary makes the first pass's partials visible on every
 // XCD, so neither pass needs a device-scope fence.
-// Loads per thread and round of the stream step: 16 covers a whole 4096-slot window in one
-// round (measured on MI355X: cfg3 49.1 us at 16, 50.8 at 8, 53.0 at 4; cfg4 14.7 / 14.4 / 13.8)
-constexpr int kWinPer = 16;
-constexpr int kWinRound = kWinPer * kBlock;
+// Loads per thread and round of the stream step: a whole 4096-slot window in one round
+// (measured on MI355X with 256 threads: cfg3 49.1 us at 16 per thread, 50.8 at 8, 53.0 at 4;
+// cfg4 14.7 / 14.4 / 13.8).
+// Threads per combine workgroup.  A window's LDS (its 4096 sums, 32 KiB, and the row list)
+// allows 4 workgroups per CU: with 512 threads that is every wave slot of the CU.  Measured on
+// MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024.
+constexpr int kCombBlock = 512;
 
-template <typename T, typename A>
-__global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
+template <typename T, typename A, int NB>
+__global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
     const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
     const int16_t* __restrict__ row_start, const A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int win_cap) {
@@ -488,7 +491,10 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   // workgroups per CU, whose stream and sum phases then overlap.
   extern __shared__ __align__(16) unsigned char s_dyn[];
   A* const s_val = reinterpret_cast<A*>(s_dyn);
-  __shared__ A s_red[kWavesPerBlock];
+  constexpr int kWaves = NB / kWave;
+  constexpr int kPer = (int)kXcsWinSlotsCap / NB;  // loads per thread: a whole window at once
+  constexpr int kRound = kPer * NB;
+  __shared__ A s_red[kWaves];
   // Rows with more than two sums, listed for a second pass (at most one per row).
   __shared__ int s_nlong;
   __shared__ int16_t s_long[kXcsWinRowsCap];
@@ -500,19 +506,24 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
 
   if (nr < 0) {  // one row with more sums than LDS holds: a workgroup sum in a fixed order
     A acc = A(0);
-    for (int l = tid; l < len; l += kBlock) acc += partials[base + l];
-    acc = block_sum(acc, s_red);
+    for (int l = tid; l < len; l += NB) acc += partials[base + l];
+    acc = wave_sum(acc);
+    if ((tid & (kWave - 1)) == 0) s_red[tid / kWave] = acc;
+    __syncthreads();
+    acc = s_red[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) acc += s_red[w];
     if (tid == 0) y[row_map ? row_map[row0] : row0] = T(acc);
     return;
   }
   if (nr > (int)kXcsWinRowsCap || total > win_cap) return;  // not a layout window (uniform)
 
   // Row starts of this thread's rows, requested first (they do not depend on LDS).
-  constexpr int kRowsPer = (int)(kXcsWinRowsCap / kBlock);
+  constexpr int kRowsPer = (int)(kXcsWinRowsCap / NB);
   int rs[kRowsPer], re[kRowsPer];
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    const int i = tid + m * kBlock;
+    const int i = tid + m * NB;
     rs[m] = i < nr ? (int)row_start[row0 + i] : 0;
     re[m] = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
   }
@@ -521,19 +532,19 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   // reading 4 slots per load - 16-byte sums, 8-byte dest words - was slower, 52.1 / 53.0 us
   // with 2 / 4 groups per thread against 50.6 us at 8 single loads: more registers, fewer
   // workgroups per CU.)
-  for (int c0 = 0; c0 < len; c0 += kWinRound) {  // uniform
-    A v[kWinPer];
-    int d[kWinPer];
+  for (int c0 = 0; c0 < len; c0 += kRound) {  // uniform
+    A v[kPer];
+    int d[kPer];
 #pragma unroll
-    for (int k = 0; k < kWinPer; ++k) {
-      const int j = c0 + tid + k * kBlock;
+    for (int k = 0; k < kPer; ++k) {
+      const int j = c0 + tid + k * NB;
       const int jj = j < len ? j : 0;  // past the end: reload the first slot, dropped below
       v[k] = partials[base + jj];
       d[k] = (int)dest[base + jj];
     }
 #pragma unroll
-    for (int k = 0; k < kWinPer; ++k)
-      if (c0 + tid + k * kBlock < len && (unsigned)d[k] < (unsigned)win_cap) s_val[d[k]] = v[k];
+    for (int k = 0; k < kPer; ++k)
+      if (c0 + tid + k * NB < len && (unsigned)d[k] < (unsigned)win_cap) s_val[d[k]] = v[k];
   }
   __syncthreads();
 
@@ -552,7 +563,7 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   // so that a wave no longer runs each of its row loops as long as its longest row.
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    const int i = tid + m * kBlock;
+    const int i = tid + m * NB;
     if (i < nr) {
       if (re[m] - rs[m] > 2) {
         s_long[atomicAdd(&s_nlong, 1)] = (int16_t)i;
@@ -564,7 +575,7 @@ __global__ __launch_bounds__(kBlock) void xcs_window_combine_kernel(
   }
   __syncthreads();
   const int n_long = s_nlong;
-  for (int j = tid; j < n_long; j += kBlock) {
+  for (int j = tid; j < n_long; j += NB) {
     const int i = s_long[j];
     const int a = row_start[row0 + i];
     const int b = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
@@ -839,8 +850,8 @@ int launch_xcs(int item_format, const void* vals, const uint32_t* pidx, int col_
     if (rc) return rc;
   }
   if (n_windows == 0) return FSP_OK;
-  hipLaunchKernelGGL((xcs_window_combine_kernel<T, A>), dim3((unsigned)n_windows), dim3(kBlock),
-                     (size_t)window_slots * sizeof(A), st,
+hipLaunchKernelGGL((xcs_window_combine_kernel<T, A, kCombBlock>), dim3((unsigned)n_windows),
+                     dim3(kCombBlock), (size_t)window_slots * sizeof(A), st,
                      reinterpret_cast<const i32x4*>(windows), dest, row_start,
                      static_cast<const A*>(partials), static_cast<T*>(y), row_map,
                      (int)window_slots);

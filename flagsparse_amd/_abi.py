@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lib = None
 

@@ -86,6 +86,9 @@ FORCE_PANEL_ROW_MIN = None
 # (32 KiB of fp64 sums in LDS) and rows.
 WINDOW_SLOTS = 4096
 WINDOW_ROWS = 2048
+# Sums of one row in a combine window at most (the combine reads one byte per row); a row
+# with more is a window of its own.
+ROW_COUNT_MAX = 255
 # Stored runs of partial sums (one item's sums in one window) start on a multiple of this many
 # slots: 128 bytes of fp64 sums, a cache line.
 RUN_ALIGN = 16
@@ -489,19 +492,28 @@ class XcsLayout:
         partial sum ("pair"), in (item, row) order - the order in which an item produces them.
 
         Rows are grouped into windows of consecutive rows with at most WINDOW_SLOTS sums and
-        WINDOW_ROWS rows (a row with more sums is a window alone, "big").  The partials buffer
-        holds the windows one after the other, and inside a window one run per item with rows
-        in it (in item order), each run starting on a multiple of RUN_ALIGN slots: an item
-        writes whole lines of its own, and the combine reads a window as one contiguous range.
-        dest gives every stored slot its position in the window's (row, item) order (-1 for
-        the padding), row_start every row its first position."""
+        WINDOW_ROWS rows (a row with more sums, or more than ROW_COUNT_MAX, is a window alone,
+        "big").  The partials buffer holds the windows one after the other, and inside a
+        window one run per item with rows in it (in item order), each run starting on a
+        multiple of RUN_ALIGN slots: an item writes whole lines of its own, and the combine
+        reads a window as one contiguous range.  dest gives every stored slot its position in
+        the window's (row, item) order (-1 for the padding), row_count every row its number of
+        sums (one byte; a row's first position is the sum of the counts before it in its
+        window)."""
         dev = pair_row.device
         n_rows, n_pairs = self.n_rows, int(pair_row.numel())
         win_slots = min(WINDOW_SLOTS, caps["xcs_window_slots"])
         rows_cap = min(WINDOW_ROWS, caps["xcs_window_rows"])
         rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=dev)
         torch.cumsum(count, 0, out=rp[1:])
-        plan = build_row_block_plan_windows(rp, win_slots, rows_cap, win_slots, 1 << 30,
+        # the planner sees a row of more than ROW_COUNT_MAX sums as longer than a window, so
+        # that it becomes a window of its own
+        plan_rp = rp
+        if n_rows and int(count.max().item()) > ROW_COUNT_MAX:
+            plan_rp = torch.zeros_like(rp)
+            torch.cumsum(torch.where(count > ROW_COUNT_MAX, win_slots + 1, count), 0,
+                         out=plan_rp[1:])
+        plan = build_row_block_plan_windows(plan_rp, win_slots, rows_cap, win_slots, 1 << 30,
                                             PLAN_WINDOW_BLOCKS * rows_cap)
         wd = plan.desc.to(device=dev, dtype=torch.int64)
         n_win = int(wd.shape[0])
@@ -565,10 +577,9 @@ class XcsLayout:
         dest = torch.full((max(n_store, 1),), -1, dtype=torch.int64, device=dev)
         dest[stored] = pos
         self.dest = dest.to(torch.int16).contiguous()
-        row_start = rp[:-1] - first_pos[win_of_row]
-        row_start = torch.where(big[win_of_row], torch.zeros_like(row_start), row_start)
-        self.row_start = row_start.to(torch.int16).contiguous() if n_rows else \
-            torch.zeros(1, dtype=torch.int16, device=dev)
+        row_count = torch.where(big[win_of_row], torch.zeros_like(count), count)
+        self.row_count = row_count.to(torch.uint8).contiguous() if n_rows else \
+            torch.zeros(1, dtype=torch.uint8, device=dev)
         del by_row, rank, pos, dest, run_of, stored
         # per item: its runs (pair order = item order, then window order), each {stored slot
         # of its first sum, the item's index of that sum, sums, stored length}
@@ -594,7 +605,7 @@ class XcsLayout:
     def held_bytes(self, caller=()):
         """Device bytes of the layout's own arrays (the rewritten entries, tables, partials)."""
         return tensor_bytes(self.vals, self.pidx, self.items, self.item_runs, self.windows,
-                            self.dest, self.row_start, self.partials, self.panel_base)
+                            self.dest, self.row_count, self.partials, self.panel_base)
 
     def describe(self):
         return {"layout": self.kind, "panels": self.n_panels, "tiles": self.n_tiles,
@@ -616,7 +627,7 @@ class XcsLayout:
             args = [_abi.dtype_code(self.vals.dtype), int(acc_f64), p(self.vals), p(self.pidx),
                     self.n_entries, self.col_bits, None, None, None, 0, p(self.items),
                     self.n_slots, p(self.item_runs), p(self.partials), p(self.windows),
-                    self.n_windows, self.window_slots, p(self.dest), p(self.row_start),
+                    self.n_windows, self.window_slots, p(self.dest), p(self.row_count),
                     self.item_format, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
@@ -625,7 +636,7 @@ class XcsLayout:
         a[9] = n_out
         a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.items,
                                               self.item_runs, self.windows, self.dest,
-                                              self.row_start))
+                                              self.row_count))
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 

@@ -464,14 +464,17 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 //   1. streams the window's stored range with every load of a thread issued before the first
 //      is used, and scatters each sum to LDS position dest[slot] - the window's sums in
 //      (row, item) order; padding slots (dest -1) are dropped;
-//   2. gives row r the sum of LDS positions [row_start[r], row_start[r + 1]) (the window's
-//      number of sums for its last row), in order, and writes y in row order.  Rows of one or
-//      two sums are summed by the thread that holds them; rows with more are listed in LDS
-//      and shared out among all the threads (measured on MI355X, cfg3: 42.5 -> 40.8 us; each
-//      wave had run its row loops as long as its longest row).
-// A window of one row with more sums than LDS holds ({row, -1, ...}: a row longer than a
-// tile) is summed by the whole workgroup - thread t takes its slots t, t + NB, ... in order,
-// then the fixed workgroup tree.
+//   2. takes each row's number of sums (row_count, one byte per row; a row with more than 255
+//      sums is a window of its own) and their exclusive scan over the window - the row's first
+//      LDS position; thread t holds rows t, t + NB, ..., scanned block by block (a wave scan
+//      each), the wave totals of every block exchanged at the barrier of step 1;
+//   3. gives row r the sum of its positions, in order, and writes y.  Rows of one or two sums
+//      are summed by the thread that holds them; rows with more are listed in LDS and shared
+//      out among all the threads (measured on MI355X, cfg3: 42.5 -> 40.8 us; each wave had
+//      run its row loops as long as its longest row).
+// A window of one row with more sums than a window takes ({row, -1, ...}) is summed by the
+// whole workgroup - thread t takes its slots t, t + NB, ... in order, then the fixed workgroup
+// tree.
 // A separate launch: the kernel boundary makes the first pass's partials visible on every
 // XCD, so neither pass needs a device-scope fence.
 // Loads per thread and round of the stream step: a whole 4096-slot window in one round
@@ -482,33 +485,48 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 // MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024.
 constexpr int kCombBlock = 512;
 
+// Inclusive scan of c over the wave (DPP, as the count part of wave_seg_scan).
+__device__ __forceinline__ int wave_incl_scan(int c) {
+  c += dpp_mov<kDppRowShr1, 0xF>(0, c);
+  c += dpp_mov<kDppRowShr1 + 1, 0xF>(0, c);
+  c += dpp_mov<kDppRowShr1 + 3, 0xF>(0, c);
+  c += dpp_mov<kDppRowShr1 + 7, 0xF>(0, c);
+  c += dpp_mov<kDppRowBcast15, 0xA>(0, c);
+  c += dpp_mov<kDppRowBcast31, 0xC>(0, c);
+  return c;
+}
+
 template <typename T, typename A, int NB>
 __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
     const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
-    const int16_t* __restrict__ row_start, const A* __restrict__ partials, T* __restrict__ y,
+    const uint8_t* __restrict__ row_count, const A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int win_cap) {
+  constexpr int kWaves = NB / kWave;
+  constexpr int kPer = (int)kXcsWinSlotsCap / NB;  // loads per thread: a whole window at once
+  constexpr int kRound = kPer * NB;
+  constexpr int kRowsPer = (int)kXcsWinRowsCap / NB;  // rows per thread
   // win_cap sums of LDS (the layout's window size): smaller windows leave room for more
   // workgroups per CU, whose stream and sum phases then overlap.
   extern __shared__ __align__(16) unsigned char s_dyn[];
   A* const s_val = reinterpret_cast<A*>(s_dyn);
-  constexpr int kWaves = NB / kWave;
-  constexpr int kPer = (int)kXcsWinSlotsCap / NB;  // loads per thread: a whole window at once
-  constexpr int kRound = kPer * NB;
   __shared__ A s_red[kWaves];
-  // Rows with more than two sums, listed for a second pass (at most one per row).
+  __shared__ int s_wtot[kRowsPer][kWaves];
+  // Rows with more than two sums, listed for a second pass: (row in the window << 20) | (first
+  // position << 8) | sums.
   __shared__ int s_nlong;
-  __shared__ int16_t s_long[kXcsWinRowsCap];
+  __shared__ int s_long[kXcsWinRowsCap];
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
   if (tid == 0) s_nlong = 0;  // read after the barrier below
   const i32x4 w0 = windows[2 * blockIdx.x];
   const int total = windows[2 * blockIdx.x + 1].x;
   const int row0 = w0.x, nr = w0.y, base = w0.z, len = w0.w;
 
-  if (nr < 0) {  // one row with more sums than LDS holds: a workgroup sum in a fixed order
+  if (nr < 0) {  // one row with more sums than a window takes: a workgroup sum in fixed order
     A acc = A(0);
     for (int l = tid; l < len; l += NB) acc += partials[base + l];
     acc = wave_sum(acc);
-    if ((tid & (kWave - 1)) == 0) s_red[tid / kWave] = acc;
+    if (lane == 0) s_red[wid] = acc;
     __syncthreads();
     acc = s_red[0];
 #pragma unroll
@@ -518,15 +536,14 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
   }
   if (nr > (int)kXcsWinRowsCap || total > win_cap) return;  // not a layout window (uniform)
 
-  // Row starts of this thread's rows, requested first (they do not depend on LDS).
-  constexpr int kRowsPer = (int)(kXcsWinRowsCap / NB);
-  int rs[kRowsPer], re[kRowsPer];
+  // The sums of this thread's rows tid + m * NB, requested first (they do not depend on LDS).
+  // With rows strided so, every store of y covers consecutive rows (measured on MI355X, cfg3:
+  // 35.4 us, against 37.3 us with 4 consecutive rows per thread and one scan).
+  auto row_of = [&](int m) { return tid + m * NB; };
+  int cnt[kRowsPer];
 #pragma unroll
-  for (int m = 0; m < kRowsPer; ++m) {
-    const int i = tid + m * NB;
-    rs[m] = i < nr ? (int)row_start[row0 + i] : 0;
-    re[m] = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
-  }
+  for (int m = 0; m < kRowsPer; ++m)
+    cnt[m] = row_of(m) < nr ? (int)row_count[row0 + row_of(m)] : 0;
 
   // Every load of a thread is issued before the first is used.  (Measured on MI355X, cfg3:
   // reading 4 slots per load - 16-byte sums, 8-byte dest words - was slower, 52.1 / 53.0 us
@@ -546,27 +563,45 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
     for (int k = 0; k < kPer; ++k)
       if (c0 + tid + k * NB < len && (unsigned)d[k] < (unsigned)win_cap) s_val[d[k]] = v[k];
   }
+  // First positions: the exclusive scan of the row counts over the window, in row order.
+  int rs[kRowsPer];
+  int incl[kRowsPer];
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    incl[m] = wave_incl_scan(cnt[m]);
+    if (lane == kWave - 1) s_wtot[m][wid] = incl[m];
+  }
   __syncthreads();
+  int before = 0;  // rows of the blocks before block m, then of the waves before this one
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    int mine = 0, blk = 0;
+    for (int j = 0; j < kWaves; ++j) {
+      const int t = s_wtot[m][j];
+      blk += t;
+      if (j < wid) mine += t;
+    }
+    rs[m] = before + mine + incl[m] - cnt[m];
+    before += blk;
+  }
 
   // The first two sums of all the thread's rows are requested together (most rows have at
-  // most two); longer rows then take four at a time.  Added in order in every case.
+  // most two); rows with more are listed and summed afterwards by all threads, in order.
   A acc[kRowsPer];
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    const A t0 = rs[m] < re[m] ? s_val[rs[m]] : A(0);
-    const A t1 = rs[m] + 1 < re[m] ? s_val[rs[m] + 1] : A(0);
+    const A t0 = cnt[m] > 0 ? s_val[rs[m]] : A(0);
+    const A t1 = cnt[m] > 1 ? s_val[rs[m] + 1] : A(0);
     acc[m] = A(0);
-    if (rs[m] < re[m]) acc[m] += t0;
-    if (rs[m] + 1 < re[m]) acc[m] += t1;
+    if (cnt[m] > 0) acc[m] += t0;
+    if (cnt[m] > 1) acc[m] += t1;
   }
-  // Rows with at most two sums are done; the others go to a list that all threads then share,
-  // so that a wave no longer runs each of its row loops as long as its longest row.
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    const int i = tid + m * NB;
+    const int i = row_of(m);
     if (i < nr) {
-      if (re[m] - rs[m] > 2) {
-        s_long[atomicAdd(&s_nlong, 1)] = (int16_t)i;
+      if (cnt[m] > 2) {
+        s_long[atomicAdd(&s_nlong, 1)] = (i << 20) | (rs[m] << 8) | cnt[m];
       } else {
         const int row = row0 + i;
         y[row_map ? row_map[row] : row] = T(acc[m]);
@@ -576,9 +611,8 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
   __syncthreads();
   const int n_long = s_nlong;
   for (int j = tid; j < n_long; j += NB) {
-    const int i = s_long[j];
-    const int a = row_start[row0 + i];
-    const int b = i + 1 < nr ? (int)row_start[row0 + i + 1] : total;
+    const int e = s_long[j];
+    const int i = e >> 20, a = (e >> 8) & 0xfff, b = a + (e & 0xff);
     A r = A(0);  // the same order as above: 0 + s[a] + s[a + 1] + ...
     for (int k = a; k < b; k += 4) {
       A t[4];
@@ -831,7 +865,7 @@ int launch_xcs(int item_format, const void* vals, const uint32_t* pidx, int col_
                const void* x, void* y, const int32_t* row_map, const int32_t* items,
                int64_t n_slots, const int32_t* item_runs, void* partials,
                const int32_t* windows, int64_t n_windows, int64_t window_slots,
-               const int16_t* dest, const int16_t* row_start, hipStream_t st) {
+               const int16_t* dest, const uint8_t* row_count, hipStream_t st) {
   if (n_slots > 0 && item_format == 1) {
     hipLaunchKernelGGL((spmv_xcs_sorted_kernel<T, A>), dim3((unsigned)n_slots),
                        dim3(kSortedBlock), (xcs_sorted_lds_reserve<T, A>()), st,
@@ -850,9 +884,9 @@ int launch_xcs(int item_format, const void* vals, const uint32_t* pidx, int col_
     if (rc) return rc;
   }
   if (n_windows == 0) return FSP_OK;
-hipLaunchKernelGGL((xcs_window_combine_kernel<T, A, kCombBlock>), dim3((unsigned)n_windows),
+  hipLaunchKernelGGL((xcs_window_combine_kernel<T, A, kCombBlock>), dim3((unsigned)n_windows),
                      dim3(kCombBlock), (size_t)window_slots * sizeof(A), st,
-                     reinterpret_cast<const i32x4*>(windows), dest, row_start,
+                     reinterpret_cast<const i32x4*>(windows), dest, row_count,
                      static_cast<const A*>(partials), static_cast<T*>(y), row_map,
                      (int)window_slots);
   return check_hip(hipGetLastError(), "xcs_window_combine_kernel launch");
@@ -930,7 +964,7 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
                             const int32_t* row_map, int64_t n_out, const int32_t* items,
                             int64_t n_slots, const int32_t* item_runs, void* partials,
                             const int32_t* windows, int64_t n_windows, int64_t window_slots,
-                            const int16_t* dest, const int16_t* row_start, int item_format,
+                            const int16_t* dest, const uint8_t* row_count, int item_format,
                             void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64) return set_error(FSP_ENOTSUP, "fsp_spmv_xcs: dtype");
   if (item_format != 0 && item_format != 1)
@@ -950,7 +984,7 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
                                      std::to_string(kXcsWinSlotsCap) + "]");
   if (n_slots > 0 && (!vals || !pidx || !x || !items || !item_runs || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null pointer");
-  if (n_windows > 0 && (!y || !windows || !dest || !row_start || !partials))
+  if (n_windows > 0 && (!y || !windows || !dest || !row_count || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_xcs: null combine-table pointer");
   if (!aligned16(vals) || !aligned16(pidx) || !aligned16(items) || !aligned16(item_runs) ||
       !aligned16(windows))
@@ -964,7 +998,7 @@ extern "C" int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint
     if (rc) return rc;
   }
 #define FSP_XCS_ARGS item_format, vals, pidx, col_bits, x, y, row_map, items, n_slots, item_runs, \
-                     partials, windows, n_windows, window_slots, dest, row_start, st
+                     partials, windows, n_windows, window_slots, dest, row_count, st
   if (dtype == FSP_F32) {
     if (acc_f64) return launch_xcs<float, double>(FSP_XCS_ARGS);
     return launch_xcs<float, float>(FSP_XCS_ARGS);

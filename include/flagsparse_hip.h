@@ -217,25 +217,25 @@ int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals, const int32_t*
  *                run sums (in row order) [first sum, first sum + sums) go to partials[first
  *                slot ...], followed by zeros up to the stored length
  *   partials     the stored slots (8 bytes each with fp64 accumulation, else the value size)
- *   windows, dest, row_start
+ *   windows, dest, row_count
  *                the second launch (y written in row order), one workgroup per window:
  *                windows[w] = 8 int32 {row0, rows, first slot, stored length, sums, 0, 0, 0}:
  *                rows [row0, row0 + rows) (<= fsp_xcs_window_rows_cap()) take their sums from
  *                partials[first slot .. + stored length): slot s goes to position dest[s] of the
  *                window (its rank in (row, item) order; -1: padding, dropped; at most
  *                window_slots <= fsp_xcs_window_slots_cap() sums, the LDS each workgroup
- *                takes) and row r gets the sum, in that order, of
- *                positions [row_start[r], row_start[r + 1]) (the window's number of sums for its
- *                last row; int16, relative to the window).  rows = -1: one row given the sum of
- *                all the window's slots (more than fit one window).  Calls sharing partials
- *                must not overlap.
+ *                takes) and row r gets the sum, in that order, of its row_count[r] positions
+ *                (one byte per row, at most 255; a row's first position is the sum of the
+ *                counts of the window's rows before it).  rows = -1: one row given the sum of
+ *                all the window's slots (a row with more sums than a window takes, or more
+ *                than 255).  Calls sharing partials must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  int64_t n_entries, int col_bits, const void* x, void* y,
                  const int32_t* row_map, int64_t n_out, const int32_t* items, int64_t n_slots,
                  const int32_t* item_runs, void* partials, const int32_t* windows,
                  int64_t n_windows, int64_t window_slots, const int16_t* dest,
-                 const int16_t* row_start, int item_format, void* stream);
+                 const uint8_t* row_count, int item_format, void* stream);
 
 /*
  * y[rows[i]] (y[row_map[rows[i]]] when row_map != NULL) = row i of A @ x for the long rows of

@@ -182,6 +182,25 @@ def test_coo_runs(dev, force_xcs, dtype):
            oracle.spmv_coo(r2, c2, d2, x, shape[0]))
 
 
+@pytest.mark.parametrize("count_max", [3, 8])
+def test_rows_over_the_count_byte(dev, monkeypatch, count_max):
+    # rows with more sums than the combine's count byte holds (ROW_COUNT_MAX, lowered here)
+    # are windows of their own, summed by a whole workgroup; the others keep their windows
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-l2")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANELS_PER_XCD", 2)  # 16 panels: rows of 9+ sums
+    monkeypatch.setattr(_spmv_layouts, "ROW_COUNT_MAX", count_max)
+    lengths = [3, 0, 400, 1, 1, 2] + [0] * 90 + [170, 5, 0, 61, 7] + [1] * 3000 + [2] * 300
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, 300000, 24, torch.float32)
+    print(f"count byte {count_max}", flush=True)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    lay = p._kernel(False)
+    assert lay.kind == "xcs" and int((lay.windows.view(-1, 8)[:, 1] < 0).sum()) > 0
+    ref = oracle.spmv_csr(ptr, idx, data, x)
+    for use_opt in (False, True):
+        _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt), ref,
+               exact_fp32=not use_opt)
+
+
 def test_automatic_choice(dev):
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=5000)  # x: 8 MiB
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)

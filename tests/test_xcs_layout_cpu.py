@@ -54,13 +54,18 @@ def _sorted_item(layout, e0, ln):
     return vpos, col, flag
 
 
+def _window_row_starts(layout, row0, nr):
+    """First LDS position of each row of a window: the exclusive sum of the window's row counts
+    (row_count, one byte per row), as the combine scans them."""
+    cnt = layout.row_count.numpy().astype(np.int64)[row0:row0 + nr]
+    return np.concatenate([[0], np.cumsum(cnt)])
+
+
 def _combine_slot_rows(layout):
     """The row of every stored slot according to the combine tables (-1: padding or unused):
-    slot s of window w is at position dest[s], inside row r's positions [row_start[r],
-    row_start[r + 1])."""
+    slot s of window w is at position dest[s], inside row r's row_count[r] positions."""
     windows = layout.windows.numpy().reshape(-1, 8).astype(np.int64)
     dest = layout.dest.numpy().astype(np.int64)
-    row_start = layout.row_start.numpy().astype(np.int64)
     rows = np.full(layout.n_partials, -1, dtype=np.int64)
     for row0, nr, base, ln, total, _, _, _ in windows:
         sl = np.arange(base, base + ln)
@@ -69,7 +74,7 @@ def _combine_slot_rows(layout):
             continue
         d = dest[sl]
         ok = d >= 0
-        starts = row_start[row0:row0 + nr]
+        starts = _window_row_starts(layout, row0, nr)[:-1]
         rows[sl[ok]] = row0 + np.searchsorted(starts, d[ok], side="right") - 1
     return rows
 
@@ -91,9 +96,9 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
     item sums each row run it holds (in row order) and stores the sums through its runs
     (item_runs: {first slot, first sum, sums, stored length}, zeros after the sums); each combine
     window then places its stored slots at their dest positions (-1: padding) and row r gets
-    the sum of positions [row_start[r], row_start[r + 1]) in order - its sums in item order -,
-    0 without any, at y[row_map[r]] when a row map is given.  A big window (rows -1) is one row
-    given the sum of all its slots."""
+    the sum of its row_count[r] positions (from the sum of the window's counts before it) in
+    order - its sums in item order -, 0 without any, at y[row_map[r]] when a row map is given.
+    A big window (rows -1) is one row given the sum of all its slots."""
     caps = _spmv_layouts._abi.caps()
     items = layout.items.numpy().reshape(-1, 12).astype(np.int64)
     item_runs = layout.item_runs.numpy().astype(np.int64)
@@ -158,7 +163,7 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
     # and their dest is -1
     windows = layout.windows.numpy().reshape(-1, 8).astype(np.int64)
     dest = layout.dest.numpy().astype(np.int64)
-    row_start = layout.row_start.numpy().astype(np.int64)
+    row_count = layout.row_count.numpy().astype(np.int64)
     line = _spmv_layouts.WINDOW_ALIGN
     next_row, next_slot = 0, 0
     for row0, nr, base, ln, total, _, _, _ in windows:
@@ -169,8 +174,9 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
         next_slot = base + ln
         real = sl[slot_row[sl] >= 0] if ln else sl
         assert real.size == total
-        if nr < 0:  # one row with more sums than a window holds
-            assert total > layout.window_slots and ln == total
+        if nr < 0:  # one row with more sums than a window holds, or than a count byte
+            assert total > min(layout.window_slots, _spmv_layouts.ROW_COUNT_MAX) and ln == total
+            assert row_count[row0] == 0
             assert np.all(slot_row[sl] == row0)
             s = acc(0)
             for v in partials[sl]:
@@ -187,9 +193,10 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
         lds[d] = partials[real]
         lds_slot = np.full(total, -1, dtype=np.int64)
         lds_slot[d] = real
+        starts = _window_row_starts(layout, row0, nr)
+        assert starts[-1] == total and row_count[row0:row0 + nr].max() <= 255
         for i in range(nr):
-            a = row_start[row0 + i]
-            b = row_start[row0 + i + 1] if i + 1 < nr else total
+            a, b = starts[i], starts[i + 1]
             mine = lds_slot[a:b]
             # the row's own sums, all of them, in item order
             assert np.all(slot_row[mine] == row0 + i)
@@ -453,6 +460,23 @@ def test_xcs_combine_windows(win_slots, win_rows, monkeypatch):
     w = lay.windows.numpy().reshape(-1, 8)
     assert (w[:, 1] < 0).any() == (win_slots == 8)  # one-row windows only when rows exceed 8
     assert lay.n_windows > lay.n_tiles
+    y = _emulate(lay, x.numpy())
+    np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("count_max", [3, 8])
+def test_xcs_rows_over_the_count_byte(count_max, monkeypatch):
+    # the combine reads one byte of sum count per row: a row with more sums than
+    # ROW_COUNT_MAX (lowered here) is a window of its own, summed whole; the other rows keep
+    # their counts and windows
+    monkeypatch.setattr(_spmv_layouts, "ROW_COUNT_MAX", count_max)
+    lengths = [3, 0, 400, 1, 1, 2] + [0] * 90 + [170, 5, 0, 61, 7] + [1] * 3000 + [2] * 300
+    vals, cols, ip, x = _case(lengths, 300000, 6, unsorted=True)
+    lay = XcsLayout(vals, cols, ip, 300000, panels_per_xcd=2)
+    _check_structure(lay, vals, cols, ip)
+    w = lay.windows.numpy().reshape(-1, 8)
+    assert (w[:, 1] < 0).sum() > 0
+    assert lay.row_count.numpy().max() <= count_max
     y = _emulate(lay, x.numpy())
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
 

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lib = None
 
@@ -53,6 +53,8 @@ SIGNATURES = {
                             _p, _i64, _i64, _p, _p, _i32, _p]),
     "fsp_spmv_panels": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i64,
                                _p, _p, _i64, _p, _p, _p, _i64, _p]),
+    "fsp_spmv_hybrid_combine": (_i32, [_i32, _i32, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
+                                       _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
     "fsp_spmm_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
                             _i64, _i64, _i32, _i32, _p, _p, _p, _p, _i64, _i32, _p]),

@@ -79,6 +79,9 @@ BAND_MIN_SHARE = 0.2
 # >= 256 / 512 / 768 / 1024 / 2048 entries) 0.302 / 0.289 / 0.289 / 0.290 / 0.309 ms with
 # 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms.
 PANEL_JOB_CHUNKS = 1024
+# The XCS + panel hybrid launches the panel part's first pass before the XCS part's (False:
+# after it); both second passes then run in one launch.
+HYBRID_PANEL_FIRST = False
 PANEL_RUNS = 4
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
@@ -87,8 +90,10 @@ FORCE_PANEL_ROW_MIN = None
 WINDOW_SLOTS = 4096
 WINDOW_ROWS = 2048
 # Sums of one row in a combine window at most (the combine reads one byte per row); a row
-# with more is a window of its own.
-ROW_COUNT_MAX = 255
+# with more is a window of its own.  The byte value ROW_SKIP marks a row the window leaves
+# alone (the hybrid's long rows, written by the panel rows of the same launch).
+ROW_COUNT_MAX = 254
+ROW_SKIP = 255
 # Stored runs of partial sums (one item's sums in one window) start on a multiple of this many
 # slots: 128 bytes of fp64 sums, a cache line.
 RUN_ALIGN = 16
@@ -484,6 +489,9 @@ class XcsLayout:
         self.n_items = n_items
         self.max_items_per_panel = q
         self.partials = torch.empty(max(self.n_partials, 1), dtype=torch.float64, device=dev)
+        # every array a launch reads or writes (marked as used on a new caller stream)
+        self._keep = (self.partials, self.vals, self.pidx, self.items, self.item_runs,
+                      self.windows, self.dest, self.row_count)
         self._order = StreamOrder(dev)
 
     def _build_combine_windows(self, pair_item, pair_row, count, n_items, caps):
@@ -617,7 +625,9 @@ class XcsLayout:
                 "col_bits": self.col_bits, "padded_entries": self.n_entries,
                 "item_format": self.item_format}
 
-    def launch(self, x, y, acc_f64, row_map=None, n_out=0):
+    def launch(self, x, y, acc_f64, row_map=None, n_out=0, passes=3):
+        """Both passes (passes=3), or only the items (1: the partial sums; y zeroed first when
+        a row map is given) or only the combine windows (2)."""
         # static arguments converted once per accumulation mode (see RowBlockLayout.launch)
         args = self._args.get(bool(acc_f64)) if hasattr(self, "_args") else None
         if args is None:
@@ -634,9 +644,11 @@ class XcsLayout:
         a[6], a[7] = x.data_ptr(), y.data_ptr()
         a[8] = None if row_map is None else row_map.data_ptr()
         a[9] = n_out
-        a[20] = self._order.stream(y.device, (self.partials, self.vals, self.pidx, self.items,
-                                              self.item_runs, self.windows, self.dest,
-                                              self.row_count))
+        if not passes & 1:
+            a[11] = 0
+        if not passes & 2:
+            a[15] = 0
+        a[20] = self._order.stream(y.device, self._keep)
         _abi.check(_abi.lib().fsp_spmv_xcs(*a), "fsp_spmv_xcs")
         return y
 
@@ -859,7 +871,10 @@ class XcsHybridLayout:
     sees the long rows as rows without entries and writes them as 0; the panel part's combine,
     launched after it on the caller's stream, then writes their sums.
 
-    Both parts run one after the other on the caller's stream.  Measured on MI355X, cfg3: the
+    The first passes of both parts run one after the other on the caller's stream, then one
+    launch does both second passes (fsp_spmv_hybrid_combine): the XCS combine windows and the
+    panel part's rows, the long rows being marked ROW_SKIP in the XCS part's row counts.
+    Measured on MI355X, cfg3: the
     panel kernel on a second stream beside the XCS kernel (fork and join events around it)
     took 275.8 us per call against 279.2 us serial, 1.2 %: a CU that holds a panel workgroup
     (128 KiB of LDS) has no room for an XCS workgroup, so the two kernels take turns and only
@@ -884,6 +899,10 @@ class XcsHybridLayout:
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
         self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
+        # the long rows have no sums in the XCS part: its windows leave them to the panel rows
+        if long_rows.numel():
+            self.short.row_count[long_rows] = ROW_SKIP
+        self._args = {}
 
     def kernel_name(self):
         return "spmv_xcs_kernel+spmv_panel_kernel"
@@ -897,8 +916,28 @@ class XcsHybridLayout:
                 "panel_part": self.long.describe()}
 
     def launch(self, x, y, acc_f64, row_map=None, n_out=0):
-        self.short.launch(x, y, acc_f64, row_map, n_out)  # zeroes y[0..n_out) first
-        self.long.launch(x, y, acc_f64, row_map)
+        # each part's arrays ordered after their previous user and marked as used here
+        st = self.short._order.stream(y.device, self.short._keep)
+        self.long._order.stream(y.device, self.long._keep)
+        if HYBRID_PANEL_FIRST:
+            self.long.launch(x, y, acc_f64, row_map, passes=1, stream=st)
+            self.short.launch(x, y, acc_f64, row_map, n_out, passes=1)  # zeroes y[0..n_out)
+        else:
+            self.short.launch(x, y, acc_f64, row_map, n_out, passes=1)  # zeroes y[0..n_out)
+            self.long.launch(x, y, acc_f64, row_map, passes=1, stream=st)
+        args = self._args.get(bool(acc_f64))
+        if args is None:  # static arguments converted once per accumulation mode
+            p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
+            sh, lg = self.short, self.long
+            args = [_abi.dtype_code(sh.vals.dtype), int(acc_f64), None, None, p(sh.partials),
+                    p(sh.windows), sh.n_windows, sh.window_slots, p(sh.dest), p(sh.row_count),
+                    p(lg.partials), p(lg.rows), p(lg.row_ptr), p(lg.slots), lg.n_rows, None]
+            self._args[bool(acc_f64)] = args
+        a = list(args)
+        a[2] = y.data_ptr()
+        a[3] = None if row_map is None else row_map.data_ptr()
+        a[15] = st
+        _abi.check(_abi.lib().fsp_spmv_hybrid_combine(*a), "fsp_spmv_hybrid_combine")
         return y
 
 

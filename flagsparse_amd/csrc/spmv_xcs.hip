@@ -496,9 +496,14 @@ __device__ __forceinline__ int wave_incl_scan(int c) {
   return c;
 }
 
+// A row count that marks a row the window leaves alone (no sums here, and y written by the
+// panel rows of the same launch: the long rows of the hybrid).
+constexpr int kRowSkip = 255;
+
+// Window wi of the combine (the body of xcs_window_combine_kernel, NB threads).
 template <typename T, typename A, int NB>
-__global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
-    const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
+__device__ __forceinline__ void combine_window(
+    int wi, const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
     const uint8_t* __restrict__ row_count, const A* __restrict__ partials, T* __restrict__ y,
     const int* __restrict__ row_map, int win_cap) {
   constexpr int kWaves = NB / kWave;
@@ -518,8 +523,8 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
   if (tid == 0) s_nlong = 0;  // read after the barrier below
-  const i32x4 w0 = windows[2 * blockIdx.x];
-  const int total = windows[2 * blockIdx.x + 1].x;
+  const i32x4 w0 = windows[2 * wi];
+  const int total = windows[2 * wi + 1].x;
   const int row0 = w0.x, nr = w0.y, base = w0.z, len = w0.w;
 
   if (nr < 0) {  // one row with more sums than a window takes: a workgroup sum in fixed order
@@ -541,9 +546,13 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
   // 35.4 us, against 37.3 us with 4 consecutive rows per thread and one scan).
   auto row_of = [&](int m) { return tid + m * NB; };
   int cnt[kRowsPer];
+  bool skip[kRowsPer];
 #pragma unroll
-  for (int m = 0; m < kRowsPer; ++m)
-    cnt[m] = row_of(m) < nr ? (int)row_count[row0 + row_of(m)] : 0;
+  for (int m = 0; m < kRowsPer; ++m) {
+    const int c = row_of(m) < nr ? (int)row_count[row0 + row_of(m)] : 0;
+    skip[m] = c == kRowSkip;
+    cnt[m] = skip[m] ? 0 : c;
+  }
 
   // Every load of a thread is issued before the first is used.  (Measured on MI355X, cfg3:
   // reading 4 slots per load - 16-byte sums, 8-byte dest words - was slower, 52.1 / 53.0 us
@@ -599,7 +608,7 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
     const int i = row_of(m);
-    if (i < nr) {
+    if (i < nr && !skip[m]) {
       if (cnt[m] > 2) {
         s_long[atomicAdd(&s_nlong, 1)] = (i << 20) | (rs[m] << 8) | cnt[m];
       } else {
@@ -625,6 +634,15 @@ __global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
     const int row = row0 + i;
     y[row_map ? row_map[row] : row] = T(r);
   }
+}
+
+template <typename T, typename A, int NB>
+__global__ __launch_bounds__(NB) void xcs_window_combine_kernel(
+    const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
+    const uint8_t* __restrict__ row_count, const A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map, int win_cap) {
+  combine_window<T, A, NB>((int)blockIdx.x, windows, dest, row_count, partials, y, row_map,
+                           win_cap);
 }
 
 // Panel layout (see the file comment): one workgroup per job, waves independent after the
@@ -897,14 +915,12 @@ int launch_xcs(int item_format, const void* vals, const uint32_t* pidx, int col_
 // gives consecutive rows consecutive slots, so a line of partials serves 16 neighbouring rows:
 // workgroups are remapped so that each XCD takes one contiguous range of rows and fetches such
 // a line into its L2 once.
+// Panel row i by the calling wave (the body of panel_combine_kernel).
 template <typename T, typename A>
-__global__ __launch_bounds__(kBlock) void panel_combine_kernel(
-    const int* __restrict__ rows, const int* __restrict__ row_ptr, const int* __restrict__ slots,
-    const A* __restrict__ partials, T* __restrict__ y, const int* __restrict__ row_map,
-    int n_rows) {
-  const int blk = xcd_logical_block((int)blockIdx.x, (int)gridDim.x);
-  const int i = blk * kWavesPerBlock + (int)(threadIdx.x / kWave);
-  if (i >= n_rows) return;  // whole waves leave together
+__device__ __forceinline__ void combine_panel_row(
+    int i, const int* __restrict__ rows, const int* __restrict__ row_ptr,
+    const int* __restrict__ slots, const A* __restrict__ partials, T* __restrict__ y,
+    const int* __restrict__ row_map) {
   const int lane = threadIdx.x & (kWave - 1);
   const int a = row_ptr[i], b = row_ptr[i + 1];
   A acc = A(0);
@@ -929,6 +945,41 @@ __global__ __launch_bounds__(kBlock) void panel_combine_kernel(
 }
 
 template <typename T, typename A>
+__global__ __launch_bounds__(kBlock) void panel_combine_kernel(
+    const int* __restrict__ rows, const int* __restrict__ row_ptr, const int* __restrict__ slots,
+    const A* __restrict__ partials, T* __restrict__ y, const int* __restrict__ row_map,
+    int n_rows) {
+  const int blk = xcd_logical_block((int)blockIdx.x, (int)gridDim.x);
+  const int i = blk * kWavesPerBlock + (int)(threadIdx.x / kWave);
+  if (i >= n_rows) return;  // whole waves leave together
+  combine_panel_row<T, A>(i, rows, row_ptr, slots, partials, y, row_map);
+}
+
+// The second pass of the XCS + panel hybrid in one launch: workgroups [0, n_pblocks) take the
+// panel part's rows (a wave each, NB / 64 rows per workgroup, remapped so that each XCD takes
+// one contiguous range of rows), the rest the XCS part's combine windows, whose rows counted
+// kRowSkip (the long rows) are left to the panel rows.  The panel rows' loads are latency
+// bound (a slot index, then the partial it names); beside the windows' streams they cost
+// little.
+template <typename T, typename A, int NB>
+__global__ __launch_bounds__(NB) void hybrid_combine_kernel(
+    const i32x4* __restrict__ windows, const int16_t* __restrict__ dest,
+    const uint8_t* __restrict__ row_count, const A* __restrict__ xcs_partials,
+    int win_cap, const int* __restrict__ rows, const int* __restrict__ row_ptr,
+    const int* __restrict__ slots, const A* __restrict__ panel_partials, int n_rows,
+    int n_pblocks, T* __restrict__ y, const int* __restrict__ row_map) {
+  const int b = (int)blockIdx.x;
+  if (b < n_pblocks) {  // uniform
+    const int i = xcd_logical_block(b, n_pblocks) * (NB / kWave) + (int)(threadIdx.x / kWave);
+    if (i < n_rows)  // whole waves
+      combine_panel_row<T, A>(i, rows, row_ptr, slots, panel_partials, y, row_map);
+    return;
+  }
+  combine_window<T, A, NB>(b - n_pblocks, windows, dest, row_count, xcs_partials, y, row_map,
+                           win_cap);
+}
+
+template <typename T, typename A>
 int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const void* x,
                   int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
                   const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_info,
@@ -950,6 +1001,26 @@ int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const vo
                      rows, row_ptr, slots, static_cast<const A*>(partials), static_cast<T*>(y),
                      row_map, (int)n_rows);
   return check_hip(hipGetLastError(), "panel_combine_kernel launch");
+}
+
+template <typename T, typename A>
+int launch_hybrid_combine(void* y, const int32_t* row_map, const void* xcs_partials,
+                          const int32_t* windows, int64_t n_windows, int64_t window_slots,
+                          const int16_t* dest, const uint8_t* row_count,
+                          const void* panel_partials, const int32_t* rows,
+                          const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                          hipStream_t st) {
+  constexpr int kRowsPerBlock = kCombBlock / kWave;
+  const int64_t n_pblocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t grid = n_pblocks + n_windows;
+  if (grid == 0) return FSP_OK;
+  hipLaunchKernelGGL((hybrid_combine_kernel<T, A, kCombBlock>), dim3((unsigned)grid),
+                     dim3(kCombBlock), (size_t)window_slots * sizeof(A), st,
+                     reinterpret_cast<const i32x4*>(windows), dest, row_count,
+                     static_cast<const A*>(xcs_partials), (int)window_slots, rows, row_ptr,
+                     slots, static_cast<const A*>(panel_partials), (int)n_rows, (int)n_pblocks,
+                     static_cast<T*>(y), row_map);
+  return check_hip(hipGetLastError(), "hybrid_combine_kernel launch");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1051,4 +1122,38 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
   return launch_panels<double, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
                                        job_panel, n_jobs, chunk_info, partials, n_partials, rows,
                                        row_ptr, slots, n_rows, st);
+}
+
+extern "C" int fsp_spmv_hybrid_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
+                                       const void* xcs_partials, const int32_t* windows,
+                                       int64_t n_windows, int64_t window_slots,
+                                       const int16_t* dest, const uint8_t* row_count,
+                                       const void* panel_partials, const int32_t* rows,
+                                       const int32_t* row_ptr, const int32_t* slots,
+                                       int64_t n_rows, void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64)
+    return set_error(FSP_ENOTSUP, "fsp_spmv_hybrid_combine: dtype");
+  if (n_windows < 0 || n_rows < 0)
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: negative size");
+  if (n_windows > 0x3fffffffLL || n_rows > 0x3fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: too many windows or rows");
+  if (n_windows > 0 && (window_slots < 1 || window_slots > kXcsWinSlotsCap))
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: window_slots outside [1, " +
+                                     std::to_string(kXcsWinSlotsCap) + "]");
+  if (n_windows > 0 && (!y || !windows || !dest || !row_count || !xcs_partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: null combine-table pointer");
+  if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !panel_partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: null panel-row pointer");
+  if (!aligned16(windows))
+    return set_error(FSP_EINVAL, "fsp_spmv_hybrid_combine: windows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t slots_lds = n_windows > 0 ? window_slots : 1;
+#define FSP_HYB_ARGS y, row_map, xcs_partials, windows, n_windows, slots_lds, dest, row_count, \
+                     panel_partials, rows, row_ptr, slots, n_rows, st
+  if (dtype == FSP_F32) {
+    if (acc_f64) return launch_hybrid_combine<float, double>(FSP_HYB_ARGS);
+    return launch_hybrid_combine<float, float>(FSP_HYB_ARGS);
+  }
+  return launch_hybrid_combine<double, double>(FSP_HYB_ARGS);
+#undef FSP_HYB_ARGS
 }

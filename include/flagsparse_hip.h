@@ -28,6 +28,9 @@
  *                          step, flagsparse_amd/_spmv_layouts.py).
  *   fsp_spmv_panels      - the same launches, for the long rows of power-law matrices (x panels
  *                          copied to LDS); used together with fsp_spmv_xcs.
+ *   fsp_spmv_hybrid_combine
+ *                        - the second pass of the two above in one launch (same reference
+ *                          launches: the row sums of spmv_csr.py:329-376 and :510-536).
  *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
  *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
  *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
@@ -225,10 +228,12 @@ int fsp_spmv_csr_static(int dtype, int acc_f64, const void* vals, const int32_t*
  *                window (its rank in (row, item) order; -1: padding, dropped; at most
  *                window_slots <= fsp_xcs_window_slots_cap() sums, the LDS each workgroup
  *                takes) and row r gets the sum, in that order, of its row_count[r] positions
- *                (one byte per row, at most 255; a row's first position is the sum of the
- *                counts of the window's rows before it).  rows = -1: one row given the sum of
- *                all the window's slots (a row with more sums than a window takes, or more
- *                than 255).  Calls sharing partials must not overlap.
+ *                (one byte per row, at most 254; a row's first position is the sum of the
+ *                counts of the window's rows before it; a count of 255 marks a row without
+ *                sums that the window leaves alone - y written by fsp_spmv_hybrid_combine's
+ *                panel rows).  rows = -1: one row given the sum of all the window's slots (a
+ *                row with more sums than a window takes, or more than 254).  Calls sharing
+ *                partials must not overlap.
  */
 int fsp_spmv_xcs(int dtype, int acc_f64, const void* vals, const uint32_t* pidx,
                  int64_t n_entries, int col_bits, const void* x, void* y,
@@ -271,6 +276,21 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pc
                     int64_t n_jobs, const int32_t* chunk_info, void* partials,
                     int64_t n_partials, const int32_t* rows, const int32_t* row_ptr,
                     const int32_t* slots, int64_t n_rows, void* stream);
+
+/*
+ * The second passes of fsp_spmv_xcs (the combine windows: windows .. row_count, over
+ * xcs_partials) and of fsp_spmv_panels (its long rows: rows, row_ptr, slots, over
+ * panel_partials) in one launch, after both first passes (called with n_windows = 0 and
+ * n_rows = 0 respectively), on the same stream.  The windows' rows counted 255 are the long
+ * rows, whose y the panel rows write.  Same tables and semantics as the two calls' second
+ * passes; the panel rows' latency-bound loads run beside the windows' streams.
+ */
+int fsp_spmv_hybrid_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
+                            const void* xcs_partials, const int32_t* windows, int64_t n_windows,
+                            int64_t window_slots, const int16_t* dest, const uint8_t* row_count,
+                            const void* panel_partials, const int32_t* rows,
+                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                            void* stream);
 
 /*
  * y = A @ x for unsorted COO with atomics (reference sort_by_row=False route); y[0..n_rows)

@@ -56,8 +56,9 @@ def _sorted_item(layout, e0, ln):
 
 def _window_row_starts(layout, row0, nr):
     """First LDS position of each row of a window: the exclusive sum of the window's row counts
-    (row_count, one byte per row), as the combine scans them."""
+    (row_count, one byte per row; ROW_SKIP counts as none), as the combine scans them."""
     cnt = layout.row_count.numpy().astype(np.int64)[row0:row0 + nr]
+    cnt = np.where(cnt == _spmv_layouts.ROW_SKIP, 0, cnt)
     return np.concatenate([[0], np.cumsum(cnt)])
 
 
@@ -197,6 +198,9 @@ def _emulate(layout, x, acc=np.float64, y=None, row_map=None):
         assert starts[-1] == total and row_count[row0:row0 + nr].max() <= 255
         for i in range(nr):
             a, b = starts[i], starts[i + 1]
+            if row_count[row0 + i] == _spmv_layouts.ROW_SKIP:  # written by the panel rows
+                assert a == b
+                continue
             mine = lds_slot[a:b]
             # the row's own sums, all of them, in item order
             assert np.all(slot_row[mine] == row0 + i)
@@ -542,7 +546,8 @@ def test_xcs_hybrid(seed):
     assert h.short.nnz + h.long.nnz == vals.numel()
     _check_panels(h.long, *_long_part(vals, cols, ip, long_mask))
     y = _emulate(h.short, x.numpy())
-    assert np.all(y[long_mask.numpy()] == 0.0)  # long rows: no entries in the XCS part
+    assert np.all(np.isnan(y[long_mask.numpy()]))  # long rows: left to the panel rows
+    assert np.all(h.short.row_count.numpy()[long_mask.numpy()] == _spmv_layouts.ROW_SKIP)
     y = _emulate_panels(h.long, x.numpy(), y)
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
     # through a row map (COO row runs): layout row r is output row map[r]

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _lib = None
 
@@ -43,6 +43,7 @@ SIGNATURES = {
     "fsp_panel_chunk": (_i64, []),
     "fsp_panel_chunk_runs_cap": (_i64, []),
     "fsp_plan_panel_chunks": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p]),
+    "fsp_plan_panel_chunks_device": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _p]),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "fsp_spmv_csr": (_i32, [_i32, _i32, _p, _p, _p, _i32, _i64, _i64, _p, _p, _p, _i64, _p, _p,
                             _i64, _i64, _p, _p, _p, _p, _i64, _i32, _p]),

@@ -337,29 +337,37 @@ class XcsLayout:
         self.n_tiles = n_tiles
         self.n_long_tiles = n_long
         tile_of_row = torch.repeat_interleave(torch.arange(n_long, n_tiles, device=dev),
-                                              t_R_d[n_long:])
+                                              t_R_d[n_long:], output_size=n_rows)
         if n_long:
             tile_of_row[long_rows] = torch.arange(n_long, device=dev)
 
-        # 3. Entry -> (tile, panel); stable sort keeps row order (then original order).
-        entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths)
-        entry_tile = tile_of_row[entry_row]
+        # 3. Entry -> (tile, panel); stable sort keeps row order (then original order).  The
+        #    radix sort's key is 32 bits wide wherever (tile, panel) pairs fit.
+        entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev, dtype=torch.int32),
+                                            lengths, output_size=nnz)
+        key_type = torch.int32 if n_tiles * P < (1 << 31) else torch.int64
+        entry_tile = tile_of_row.to(key_type)[entry_row]
         bounds = torch.tensor(cb[1:P], dtype=torch.int32, device=dev)
-        panel = torch.bucketize(cols, bounds, right=True)
+        panel = torch.bucketize(cols, bounds, right=True, out_int32=True)
         key = entry_tile * P + panel
+        del entry_tile
         key_sorted, perm = torch.sort(key, stable=True)
+        key_sorted = key_sorted.to(torch.int64)
         del key
 
         # 4. Pieces (tile, panel) -> items of <= item_cap entries (equal split).
         n_pieces = n_tiles * P
-        cnt = torch.bincount(key_sorted, minlength=n_pieces) if nnz else \
-            torch.zeros(n_pieces, dtype=torch.int64, device=dev)
+        # entries per piece: the boundaries of equal keys in the sorted keys
+        bnd = torch.searchsorted(key_sorted, torch.arange(n_pieces + 1, device=dev))
+        cnt = bnd[1:] - bnd[:-1]
+        del bnd
         n_sub = (cnt + item_cap - 1) // item_cap
         n_items = int(n_sub.sum().item())
         piece_first_item = torch.cumsum(n_sub, 0) - n_sub
         base = torch.where(n_sub > 0, cnt // n_sub.clamp(min=1), torch.zeros_like(cnt))
         rem = torch.where(n_sub > 0, cnt % n_sub.clamp(min=1), torch.zeros_like(cnt))
-        item_piece = torch.repeat_interleave(torch.arange(n_pieces, device=dev), n_sub)
+        item_piece = torch.repeat_interleave(torch.arange(n_pieces, device=dev), n_sub,
+                                             output_size=n_items)
         item_j = torch.arange(n_items, device=dev) - piece_first_item[item_piece]
         item_len = base[item_piece] + (item_j < rem[item_piece]).to(base.dtype)
         item_off = item_j * base[item_piece] + torch.minimum(item_j, rem[item_piece])
@@ -528,7 +536,8 @@ class XcsLayout:
         big = wd[:, 2] != 0  # {row, 0, 1, -1}: one row with more sums than a window holds
         row0 = wd[:, 0]
         nr = torch.where(big, torch.ones_like(row0), wd[:, 1] - wd[:, 0])
-        win_of_row = torch.repeat_interleave(torch.arange(n_win, device=dev), nr)
+        win_of_row = torch.repeat_interleave(torch.arange(n_win, device=dev), nr,
+                                             output_size=n_rows)
         first_pos = rp[row0]  # a window's first sum in (row, item) order
         pair_win = win_of_row[pair_row] if n_pairs else torch.zeros(0, dtype=torch.int64,
                                                                     device=dev)
@@ -575,9 +584,10 @@ class XcsLayout:
             .to(torch.int32).contiguous()
         self.n_windows = n_win
         # every sum's stored slot, and its position in the window's (row, item) order
-        run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), run_len)
+        run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), run_len,
+                                         output_size=n_pairs)
         stored = run_base[run_of] + (torch.arange(n_pairs, device=dev) - run_first[run_of])
-        by_row = torch.sort(pair_row, stable=True)[1]
+        by_row = torch.sort(pair_row.to(torch.int32), stable=True)[1]  # a 32-bit radix key
         rank = torch.empty_like(by_row)
         rank[by_row] = torch.arange(n_pairs, device=dev)
         pos = rank - first_pos[pair_win]
@@ -668,27 +678,92 @@ def panel_row_min(n_cols, value_bytes):
     return PANEL_RUNS * max(1, n_panels)
 
 
-def plan_panel_chunks(panel_runs, run_len, chunk, runs_cap):
-    """(run_pos, panel_end) of fsp_plan_panel_chunks for device (or host) int64 tensors, on
-    the device of run_len: where each run's first entry is stored, and where each panel ends."""
+def plan_panel_chunks_prefix(panel_runs, run_len, chunk, runs_cap):
+    """fsp_plan_panel_chunks' plan as a prefix sum of the run lengths, on whatever device the
+    tensors live: (run_pos, panel_end), or None where that is not the plan.  Without the run
+    cap each panel's runs are packed back to back and only its last chunk is padded; the cap
+    changes nothing as long as no chunk would hold more than runs_cap pieces of runs (the runs
+    starting in it, plus one when its first entry continues a run), which is checked here -
+    the greedy planner closes a chunk early only at a run that would be its runs_cap + 1st."""
     dev = run_len.device
-    pr = panel_runs.to("cpu", torch.int64).contiguous()
-    rl = run_len.to("cpu", torch.int64).contiguous()
-    n_panels = int(pr.numel()) - 1
-    pos = torch.empty(max(int(rl.numel()), 1), dtype=torch.int64)
-    end = torch.empty(max(n_panels, 1), dtype=torch.int64)
-    _abi.check(_abi.lib().fsp_plan_panel_chunks(pr.data_ptr(), n_panels, rl.data_ptr(),
-                                                int(chunk), int(runs_cap), pos.data_ptr(),
-                                                end.data_ptr()), "fsp_plan_panel_chunks")
-    return pos[:rl.numel()].to(dev), end[:n_panels].to(dev)
+    n_panels = int(panel_runs.numel()) - 1
+    n_runs = int(run_len.numel())
+    pr = panel_runs.to(device=dev, dtype=torch.int64)
+    rl = run_len.to(torch.int64)
+    csum = torch.zeros(n_runs + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(rl, 0, out=csum[1:])
+    panel_len = (csum[pr[1:]] - csum[pr[:-1]] + chunk - 1) // chunk * chunk
+    panel_end = torch.cumsum(panel_len, 0)
+    if n_runs == 0:
+        return torch.zeros(0, dtype=torch.int64, device=dev), panel_end
+    panel_of = torch.repeat_interleave(torch.arange(n_panels, device=dev), pr[1:] - pr[:-1],
+                                       output_size=n_runs)
+    run_pos = (panel_end - panel_len)[panel_of] + csum[:-1] - csum[pr[:-1]][panel_of]
+    n_chunks = int(panel_end[-1].item()) // chunk
+    first_chunk = run_pos // chunk
+    pieces = torch.bincount(first_chunk, minlength=n_chunks)
+    at_start = torch.zeros(n_chunks, dtype=torch.int64, device=dev)
+    at_start[first_chunk[run_pos % chunk == 0]] = 1
+    pieces += 1 - at_start  # every chunk holds entries: a first entry that no run starts
+    if int(pieces.max().item()) > runs_cap:
+        return None
+    return run_pos, panel_end
+
+
+def plan_panel_chunks(panel_runs, run_len, chunk, runs_cap):
+    """(run_pos, panel_end) of fsp_plan_panel_chunks - where each run's first entry is stored,
+    and where each panel ends - on the device of run_len: the prefix-sum plan where it is the
+    plan, else fsp_plan_panel_chunks_device (one thread per panel, the greedy rule).  Host
+    tensors take the host planner."""
+    dev = run_len.device
+    n_panels = int(panel_runs.numel()) - 1
+    if not run_len.is_cuda:
+        pr = panel_runs.to("cpu", torch.int64).contiguous()
+        rl = run_len.to("cpu", torch.int64).contiguous()
+        pos = torch.empty(max(int(rl.numel()), 1), dtype=torch.int64)
+        end = torch.empty(max(n_panels, 1), dtype=torch.int64)
+        _abi.check(_abi.lib().fsp_plan_panel_chunks(pr.data_ptr(), n_panels, rl.data_ptr(),
+                                                    int(chunk), int(runs_cap), pos.data_ptr(),
+                                                    end.data_ptr()), "fsp_plan_panel_chunks")
+        return pos[:rl.numel()], end[:n_panels]
+    plan = plan_panel_chunks_prefix(panel_runs, run_len, chunk, runs_cap)
+    if plan is not None:
+        return plan
+    return plan_panel_chunks_kernel(panel_runs, run_len, chunk, runs_cap)
+
+
+def plan_panel_chunks_kernel(panel_runs, run_len, chunk, runs_cap):
+    """(run_pos, panel_end) of fsp_plan_panel_chunks from fsp_plan_panel_chunks_device (device
+    tensors)."""
+    dev = run_len.device
+    n_panels = int(panel_runs.numel()) - 1
+    if run_len.numel() == 0:  # no runs: every panel empty
+        return (torch.zeros(0, dtype=torch.int64, device=dev),
+                torch.zeros(max(n_panels, 0), dtype=torch.int64, device=dev))
+    pr = panel_runs.to(device=dev, dtype=torch.int64).contiguous()
+    rl = run_len.to(torch.int64).contiguous()
+    local = torch.empty(max(int(rl.numel()), 1), dtype=torch.int64, device=dev)
+    panel_len = torch.empty(max(n_panels, 1), dtype=torch.int64, device=dev)
+    _abi.check(_abi.lib().fsp_plan_panel_chunks_device(
+        pr.data_ptr(), n_panels, rl.data_ptr(), int(chunk), int(runs_cap), local.data_ptr(),
+        panel_len.data_ptr(), _abi.raw_stream(dev)), "fsp_plan_panel_chunks_device")
+    panel_len = panel_len[:n_panels]
+    panel_end = torch.cumsum(panel_len, 0)
+    panel_of = torch.repeat_interleave(torch.arange(n_panels, device=dev), pr[1:] - pr[:-1],
+                                       output_size=int(rl.numel()))
+    return local[:rl.numel()] + (panel_end - panel_len)[panel_of], panel_end
+
+
+def panel_storage_positions_of(p, chunk):
+    """Memory position of the logical entries p of the panel layout: inside a chunk, lane L's
+    h-th quad (logical quad 2L + h) is stored at quad 64h + L."""
+    lq = (p % chunk) // 4
+    return (p // chunk) * chunk + ((lq % 2) * (chunk // 8) + lq // 2) * 4 + p % 4
 
 
 def panel_storage_positions(n_entries, chunk, device):
-    """Memory position of each logical entry of the panel layout: inside a chunk, lane L's
-    h-th quad (logical quad 2L + h) is stored at quad 64h + L."""
-    p = torch.arange(n_entries, device=device)
-    lq = (p % chunk) // 4
-    return (p // chunk) * chunk + ((lq % 2) * (chunk // 8) + lq // 2) * 4 + p % 4
+    """panel_storage_positions_of for every logical entry 0 .. n_entries - 1."""
+    return panel_storage_positions_of(torch.arange(n_entries, device=device), chunk)
 
 
 class PanelLayout:
@@ -709,85 +784,70 @@ class PanelLayout:
         self.col_bits = cb
         self.rows = rows.to(torch.int32).contiguous()
         rp = rowptr.to(torch.int64)
-        row = torch.repeat_interleave(torch.arange(n_rows, device=dev), rp[1:] - rp[:-1])
-        c64 = cols.to(torch.int64)
-        # entries by (panel, row): a stable sort by panel keeps each row's entries in order
-        panel = c64 >> cb
+        nnz = self.nnz
         n_panels = max(1, -(-self.n_cols >> cb))
-        order = torch.sort(panel, stable=True)[1]
-        panel = panel[order]
+        cols32 = cols.to(torch.int32)
+        # entries by (panel, row): a stable sort by panel keeps each row's entries in order
+        # (radix-sorted on a key no wider than the panel count needs: one byte for cfg-sized x)
+        panel = cols32 >> cb
+        key = panel.to(torch.uint8 if n_panels <= 256 else
+                       torch.int16 if n_panels <= (1 << 15) else torch.int32)
+        order = torch.sort(key, stable=True)[1]
+        del key
+        row = torch.repeat_interleave(torch.arange(n_rows, device=dev, dtype=torch.int32),
+                                      rp[1:] - rp[:-1], output_size=nnz)
         row_s = row[order]
         del row
+        panel = panel[order]
         # runs: the entries of one row in one panel; chunks of at most `chunk` entries and
         # panel_chunk_runs runs (the kernel stages a chunk's run sums one per lane), planned on
-        # the host run by run (fsp_plan_panel_chunks); the rest of a chunk closed early, and of
-        # each panel's last chunk, is padding
-        brk = torch.ones(self.nnz, dtype=torch.bool, device=dev)
-        if self.nnz > 1:
+        # the device (plan_panel_chunks); the rest of a chunk closed early, and of each panel's
+        # last chunk, is padding
+        brk = torch.ones(nnz, dtype=torch.bool, device=dev)
+        if nnz > 1:
             brk[1:] = (panel[1:] != panel[:-1]) | (row_s[1:] != row_s[:-1])
         run_first = torch.nonzero(brk).flatten()
-        del brk
-        run_len = torch.diff(run_first, append=torch.tensor([self.nnz], device=dev))
+        n_runs = int(run_first.numel())
+        run_len = torch.diff(run_first, append=torch.tensor([nnz], device=dev))
+        run_panel = panel[run_first].to(torch.int64)
+        del panel
         panel_runs = torch.zeros(n_panels + 1, dtype=torch.int64, device=dev)
-        torch.cumsum(torch.bincount(panel[run_first], minlength=n_panels), 0,
-                     out=panel_runs[1:])
+        torch.cumsum(torch.bincount(run_panel, minlength=n_panels), 0, out=panel_runs[1:])
         run_pos, panel_end = plan_panel_chunks(panel_runs, run_len, chunk,
                                                caps["panel_chunk_runs"])
-        panel_start = torch.cat([panel_end.new_zeros(1), panel_end[:-1]])
         n_entries = int(panel_end[-1].item()) if n_panels else 0
-        n_runs = int(run_first.numel())
-        run_of = torch.repeat_interleave(torch.arange(n_runs, device=dev), run_len)
-        dest = run_pos[run_of] + (torch.arange(self.nnz, device=dev) - run_first[run_of])
-        del run_of
-        vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
-        vals[dest] = data[order]
-        # padding continues the run before it: the gap after run r (up to the next run of its
-        # panel, or the panel's end) takes run r's row, value 0
-        run_panel = panel[run_first]
-        run_row = row_s[run_first]
-        nxt = panel_end[run_panel].clone()
-        if n_runs > 1:
-            same = run_panel[1:] == run_panel[:-1]
-            nxt[:-1] = torch.where(same, run_pos[1:], nxt[:-1])
-        run_end = run_pos + run_len
-        gap = nxt - run_end
-        pidx = torch.empty(n_entries, dtype=torch.int64, device=dev)
-        n_gap = int(gap.sum().item()) if n_runs else 0
-        if n_gap:
-            g_run = torch.repeat_interleave(torch.arange(n_runs, device=dev), gap)
-            g_first = torch.cumsum(gap, 0) - gap
-            g_pos = run_end[g_run] + (torch.arange(n_gap, device=dev) - g_first[g_run])
-            pidx[g_pos] = run_row[g_run] << cb
-            del g_run, g_first, g_pos
-        pidx[dest] = (row_s << cb) | (c64[order] & ((1 << cb) - 1))
-        real = torch.zeros(n_entries, dtype=torch.bool, device=dev)
-        real[dest] = True
-        del order, row_s, c64, dest, panel, run_first, run_len, run_pos, run_panel, run_row
-        del nxt, run_end, gap
         self.n_entries = n_entries
-        # one partial slot per (chunk, run): runs start at a chunk start or a row change
         n_chunks = n_entries // chunk
-        rowpos = pidx >> cb
-        starts = torch.ones(n_entries, dtype=torch.bool, device=dev)
-        starts[1:] = rowpos[1:] != rowpos[:-1]
+        # logical position of every entry: its run's position plus its place in the run
+        run_id = torch.cumsum(brk, 0) - 1
+        del brk
+        dest = torch.arange(nnz, device=dev) + (run_pos - run_first)[run_id]
+        del run_id
+        # a chunk's runs start at the chunk's first entry and at every run's first entry (the
+        # padding closing a chunk continues the run before it, and no chunk opens with padding)
+        starts = torch.zeros(n_entries, dtype=torch.bool, device=dev)
         starts[::chunk] = True
+        starts[run_pos] = True
         runs = starts.view(n_chunks, chunk).sum(1)
         if n_chunks and int(runs.max().item()) > caps["panel_chunk_runs"]:
             raise AssertionError("panel chunk plan: a chunk holds more runs than the kernel "
                                  "stages")
         # per chunk {first slot, entries in use}: the padding (a chunk closed early, or a
         # panel's last chunk) is the chunk's tail, whose products the kernel takes as 0
-        used = real.view(n_chunks, chunk).sum(1)
-        if n_entries > 1:  # no entry in use after a padding entry of the same chunk
-            gap_then_use = ~real[:-1] & real[1:]
-            gap_then_use[chunk - 1::chunk] = False
-            if bool(gap_then_use.any()):
-                raise AssertionError("panel chunk plan: padding inside a chunk")
-            del gap_then_use
-        del real
+        real = torch.zeros(n_entries, dtype=torch.bool, device=dev)
+        real[dest] = True
+        rv = real.view(n_chunks, chunk)
+        used = rv.sum(1)
+        if n_chunks and bool((rv[:, 1:] & ~rv[:, :-1]).any()):
+            raise AssertionError("panel chunk plan: padding inside a chunk")
+        del real, rv
         self.chunk_info = torch.stack([torch.cumsum(runs, 0) - runs, used], 1) \
             .to(torch.int32).contiguous()
-        slot_row = rowpos[starts]
+        # one partial slot per (chunk, run), in slot order: the row at each run start
+        row_at = torch.zeros(n_entries, dtype=torch.int32, device=dev)
+        row_at[dest] = row_s
+        slot_row = row_at[torch.nonzero(starts).flatten()]
+        del row_at
         self.n_partials = int(slot_row.numel())
         if self.n_partials * 8 > _INDEX_LIMIT_INT32:
             raise ValueError("more panel partial sums than the kernel's store range holds")
@@ -799,14 +859,15 @@ class PanelLayout:
         # values: inside a chunk, logical quad 2L + h at quad 64h + L; 16-bit entries in logical
         # order, the column in the panel | 0x8000 at a run start (the kernel needs only where
         # runs start: a chunk's runs take consecutive slots)
-        mem = panel_storage_positions(n_entries, chunk, dev)
-        self.vals = torch.zeros_like(vals)
-        self.vals[mem] = vals[:n_entries]
-        pcol = (pidx & ((1 << cb) - 1)) | (starts.to(torch.int64) << 15)
+        self.vals = torch.zeros(max(n_entries, 4), dtype=data.dtype, device=dev)
+        self.vals[panel_storage_positions_of(dest, chunk)] = data[order]
+        pc = torch.zeros(n_entries, dtype=torch.int32, device=dev)
+        pc[dest] = cols32[order] & ((1 << cb) - 1)
+        pc |= starts.to(torch.int32) << 15
         self.pcol = torch.zeros(max(n_entries, 8), dtype=torch.int16, device=dev)
-        self.pcol[:n_entries] = torch.where(pcol >= (1 << 15), pcol - (1 << 16), pcol) \
-            .to(torch.int16)
-        del pidx, rowpos, starts, slot_row, vals, pcol, mem
+        self.pcol[:n_entries] = torch.where(pc >= (1 << 15), pc - (1 << 16), pc).to(torch.int16)
+        del pc, starts, slot_row, dest, order, row_s, cols32, run_first, run_len, run_pos
+        panel_start = torch.cat([panel_end.new_zeros(1), panel_end[:-1]])
         # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
         # sizes keep the rounds of workgroups even)
         per_panel = (panel_end - panel_start) // chunk
@@ -890,15 +951,18 @@ class XcsHybridLayout:
         rp = rowptr.to(torch.int64)
         lengths = rp[1:] - rp[:-1]
         self.n_rows, self.n_cols, self.nnz = int(lengths.numel()), int(n_cols), int(data.numel())
-        entry_long = torch.repeat_interleave(long_mask, lengths)
+        entry_long = torch.repeat_interleave(long_mask, lengths, output_size=self.nnz)
         short_ptr = torch.zeros_like(rp)
         torch.cumsum(torch.where(long_mask, 0, lengths), 0, out=short_ptr[1:])
-        self.short = xcs_layout(data[~entry_long], cols[~entry_long], short_ptr, n_cols,
-                                panels_per_xcd)
+        pick = torch.nonzero(~entry_long).flatten()
+        self.short = xcs_layout(data[pick], cols[pick], short_ptr, n_cols, panels_per_xcd)
+        pick = torch.nonzero(entry_long).flatten()
+        del entry_long
         long_rows = torch.nonzero(long_mask).flatten()
         long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
         torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
-        self.long = PanelLayout(data[entry_long], cols[entry_long], long_ptr, n_cols, long_rows)
+        self.long = PanelLayout(data[pick], cols[pick], long_ptr, n_cols, long_rows)
+        del pick
         # the long rows have no sums in the XCS part: its windows leave them to the panel rows
         if long_rows.numel():
             self.short.row_count[long_rows] = ROW_SKIP

@@ -145,10 +145,72 @@ int launch_plan(const void* rowptr, int64_t n_rows, int64_t window, int64_t nnz_
   return check_hip(hipGetLastError(), "plan_windows_kernel launch");
 }
 
+// The chunk plan of the panel layout on the device, one thread per panel: the greedy rule of
+// fsp_plan_panel_chunks (abi.cpp) over the panel's runs in order - a run starts where the
+// previous one ended, unless the open chunk already holds runs_cap runs (the rest of the
+// chunk is padding); a run longer than the chunk's free space continues in the next chunks
+// (each piece counts as a run of the chunk it lies in); the panel's last chunk is padded.
+// Writes each run's first position relative to its panel, and each panel's padded length.
+// The run lengths are read kPanelPlanBatch at a time, all requested before the first is used.
+constexpr int kPanelPlanBatch = 16;
+constexpr int kPanelPlanBlock = 64;
+
+__global__ __launch_bounds__(kPanelPlanBlock) void plan_panel_chunks_kernel(
+    const int64_t* __restrict__ panel_runs, int64_t n_panels,
+    const int64_t* __restrict__ run_len, int64_t chunk, int64_t runs_cap,
+    int64_t* __restrict__ run_pos, int64_t* __restrict__ panel_len) {
+  const int64_t p = (int64_t)blockIdx.x * kPanelPlanBlock + threadIdx.x;
+  if (p >= n_panels) return;
+  const int64_t r0 = panel_runs[p], r1 = panel_runs[p + 1];
+  int64_t pos = 0, used = 0, runs = 0;  // the open chunk's entries and runs
+  for (int64_t rb = r0; rb < r1; rb += kPanelPlanBatch) {
+    int64_t len[kPanelPlanBatch];
+#pragma unroll
+    for (int u = 0; u < kPanelPlanBatch; ++u) len[u] = rb + u < r1 ? run_len[rb + u] : 0;
+#pragma unroll
+    for (int u = 0; u < kPanelPlanBatch; ++u) {
+      if (rb + u >= r1) break;
+      int64_t left = len[u] > 0 ? len[u] : 1;  // runs are never empty (checked by the caller)
+      if (runs == runs_cap) {  // close the chunk: the rest is padding
+        pos += chunk - used;
+        used = runs = 0;
+      }
+      run_pos[rb + u] = pos;
+      while (left > 0) {
+        const int64_t piece = left < chunk - used ? left : chunk - used;
+        ++runs;
+        used += piece;
+        pos += piece;
+        left -= piece;
+        if (used == chunk) used = runs = 0;
+      }
+    }
+  }
+  if (used > 0) pos += chunk - used;  // the panel's last chunk
+  panel_len[p] = pos;
+}
+
 }  // namespace
 }  // namespace fsp
 
 using namespace fsp;
+
+extern "C" int fsp_plan_panel_chunks_device(const int64_t* panel_runs, int64_t n_panels,
+                                            const int64_t* run_len, int64_t chunk,
+                                            int64_t runs_cap, int64_t* run_pos,
+                                            int64_t* panel_len, void* stream) {
+  if (n_panels < 0 || chunk < 1 || runs_cap < 1)
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks_device: need n_panels >= 0, chunk >= 1, "
+                                 "runs_cap >= 1");
+  if (n_panels == 0) return FSP_OK;
+  if (!panel_runs || !panel_len || !run_len || !run_pos)
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks_device: null pointer");
+  const int64_t blocks = (n_panels + kPanelPlanBlock - 1) / kPanelPlanBlock;
+  hipLaunchKernelGGL(plan_panel_chunks_kernel, dim3((unsigned)blocks), dim3(kPanelPlanBlock), 0,
+                     static_cast<hipStream_t>(stream), panel_runs, n_panels, run_len, chunk,
+                     runs_cap, run_pos, panel_len);
+  return check_hip(hipGetLastError(), "plan_panel_chunks_kernel launch");
+}
 
 extern "C" int fsp_plan_windows_count(const void* rowptr, int rowptr_bits, int64_t n_rows,
                                       int64_t window_rows, int64_t nnz_cap, int64_t rows_cap,

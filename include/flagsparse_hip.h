@@ -116,6 +116,21 @@ int fsp_plan_panel_chunks(const int64_t* panel_runs, int64_t n_panels, const int
                           int64_t chunk, int64_t runs_cap, int64_t* run_pos, int64_t* panel_end);
 
 /*
+ * The same chunk plan on the device (no host copy, no host loop), one thread per panel; the
+ * prepare step takes it when a prefix sum of the run lengths does not already give the plan
+ * (a chunk of more than runs_cap runs).  panel_runs, run_len: device int64 as above (every
+ * run of at least one entry, not checked here); outputs, device int64: run_pos[r] = the
+ * position of run r's first entry counted from its panel's first position, panel_len[p] =
+ * panel p's padded length (a multiple of chunk), so that panel_end is their prefix sum.  Like
+ * fsp_plan_panel_chunks it has no reference counterpart (the reference has no panel layout);
+ * it keeps the prepare step on the device, as the planners below do for the reference's host
+ * loops (spmm_csr.py:417-441).
+ */
+int fsp_plan_panel_chunks_device(const int64_t* panel_runs, int64_t n_panels,
+                                 const int64_t* run_len, int64_t chunk, int64_t runs_cap,
+                                 int64_t* run_pos, int64_t* panel_len, void* stream);
+
+/*
  * The same plan built on the device in two passes (no host copy of rowptr, no host loop):
  * the rows are cut into windows of window_rows rows and each window is planned with the rules
  * of fsp_plan_row_blocks, except that no block crosses a window boundary.  Replaces the host

@@ -125,3 +125,31 @@ def test_device_plan_bisect_on_uniform_rows(dev):
     assert np.array_equal(whole.desc.cpu().numpy().astype(np.int64), want)
     wide = build_row_block_plan_device(rp_dev, *caps, window_rows=16 * 1024)
     assert wide.n_desc <= want.shape[0] + -(-n // (16 * 1024))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_device_panel_chunk_plan_matches_host(dev, seed):
+    # the panel layout's chunk plan on the device (fsp_plan_panel_chunks_device, one thread per
+    # panel) equals the host planner on random panels, with run caps that close chunks early
+    # and runs longer than a chunk; plan_panel_chunks on device tensors (its prefix route or
+    # the kernel) equals it too
+    from flagsparse_amd import _spmv_layouts
+
+    rng = np.random.default_rng(40 + seed)
+    for chunk in (8, 512):
+        for trial in range(12):
+            n_panels = int(rng.integers(1, 40))
+            counts = rng.integers(0, 300, n_panels)
+            counts[rng.integers(0, n_panels)] = 0  # an empty panel
+            lens = rng.integers(1, 3 * chunk, int(counts.sum()))
+            short = rng.random(lens.size) < rng.random()
+            lens[short] = rng.integers(1, 4, int(short.sum()))
+            cap = int(rng.integers(1, 70))
+            pr = torch.as_tensor(np.r_[0, np.cumsum(counts)])
+            rl = torch.as_tensor(lens)
+            print(f"panel plan seed {seed} chunk {chunk} trial {trial} cap {cap}", flush=True)
+            host = _spmv_layouts.plan_panel_chunks(pr, rl, chunk, cap)
+            kern = _spmv_layouts.plan_panel_chunks_kernel(pr.to(dev), rl.to(dev), chunk, cap)
+            auto = _spmv_layouts.plan_panel_chunks(pr.to(dev), rl.to(dev), chunk, cap)
+            for got in (kern, auto):
+                assert torch.equal(got[0].cpu(), host[0]) and torch.equal(got[1].cpu(), host[1])

@@ -687,6 +687,36 @@ def test_panel_chunk_plan_properties(seed):
         start = end[p]
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_panel_chunk_plan_prefix_matches_host(seed):
+    # the prefix-sum plan (the device path's fast route, device-agnostic torch) either equals
+    # the host greedy planner or declines, and it declines exactly when the host plan closes a
+    # chunk early at the run cap
+    rng = np.random.default_rng(100 + seed)
+    chunk = int(rng.choice([8, 16, 512]))
+    for trial in range(40):
+        n_panels = int(rng.integers(1, 9))
+        counts = rng.integers(0, 60, n_panels)
+        lens = rng.integers(1, 3 * chunk, int(counts.sum()))
+        short = rng.random(lens.size) < rng.random()
+        lens[short] = rng.integers(1, 4, int(short.sum()))
+        cap = int(rng.integers(2, 70))
+        pr = torch.as_tensor(np.r_[0, np.cumsum(counts)])
+        rl = torch.as_tensor(lens)
+        host_pos, host_end = _spmv_layouts.plan_panel_chunks(pr, rl, chunk, cap)
+        got = _spmv_layouts.plan_panel_chunks_prefix(pr, rl, chunk, cap)
+        packed = np.r_[0, np.cumsum(lens)][:-1] if lens.size else np.zeros(0, dtype=np.int64)
+        # host plan with no early close: every panel's runs back to back
+        starts = np.repeat(np.r_[0, host_end.numpy()[:-1]], counts)
+        firsts = np.repeat(np.r_[0, np.cumsum(lens)][pr.numpy()[:-1]], counts)
+        no_early = np.array_equal(host_pos.numpy(), starts + packed - firsts)
+        if got is None:
+            assert not no_early
+        else:
+            assert no_early
+            assert torch.equal(got[0], host_pos) and torch.equal(got[1], host_end)
+
+
 def test_panel_layout_short_runs():
     # rows with one or two entries in each of many panels: chunks close at the run cap, and
     # the sums still match the oracle

@@ -23,6 +23,11 @@ namespace fsp {
 namespace {
 
 constexpr int kSlots = (int)kSpmmSlots;
+// B rows requested together per lane of a short row.  Measured on MI355X, cfg5 (fp32 N=64):
+// 663.5 / 663.0 / 661.9 us with 4 / 6 / 8 (N=16: 324.7 / 325.3 / 326.0; fp64 N=16: 367.2 /
+// 368.4 / 366.5): the kernel is bound by the rate at which L2 misses are filled, not by the
+// loads a lane keeps in flight.
+constexpr int kRowsInFlight = 4;
 constexpr int kStageUPT = kSlots / (4 * kBlock);
 static_assert(kStageUPT * 4 * kBlock == kSlots, "staging slots must be whole quads per thread");
 
@@ -149,12 +154,13 @@ __global__ __launch_bounds__(kBlock) void spmm_rowblock_kernel(
       const int a = (int)(s_ptr[grp] - lo), e = (int)(s_ptr[grp + 1] - lo);
       const T* Bc = B + ncol;
       int i = a;
-      for (; i + 4 <= e; i += 4) {
-        T bv[4][VW];
+      for (; i + kRowsInFlight <= e; i += kRowsInFlight) {
+        T bv[kRowsInFlight][VW];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) load_vec<T, VW>(Bc + (int64_t)s_col[i + q] * ldb, bv[q]);
+        for (int q = 0; q < kRowsInFlight; ++q)
+          load_vec<T, VW>(Bc + (int64_t)s_col[i + q] * ldb, bv[q]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kRowsInFlight; ++q) {
           const A av = A(s_val[i + q]);
 #pragma unroll
           for (int j = 0; j < VW; ++j) acc[j] += av * A(bv[q][j]);

@@ -77,12 +77,16 @@ BAND_MIN_SHARE = 0.2
 # panel layout when they hold at least PANEL_MIN_SHARE of the entries.  Measured on MI355X
 # for cfg3 with 128 KiB panels (256 of them; whole path): PANEL_RUNS 1 / 2 / 3 / 4 / 8 (rows
 # >= 256 / 512 / 768 / 1024 / 2048 entries) 0.302 / 0.289 / 0.289 / 0.290 / 0.309 ms with
-# 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms.
+# 1024 chunks per job, 4 with 256 / 512 chunks per job 0.294 / 0.293 ms; with the current
+# kernels (both second passes in one launch) rows >= 512 / 640 / 768 / 1024 entries 267.6 /
+# 266.7 / 267.5 / 268.1 us: each row moved to the panels saves its gathers (the XCS kernel
+# 139.5 -> 128.1 us at 640) and adds a partial sum per panel (the panel kernel 88.7 -> 94.7
+# us, the combine +1.6 us).
 PANEL_JOB_CHUNKS = 1024
 # The XCS + panel hybrid launches the panel part's first pass before the XCS part's (False:
 # after it); both second passes then run in one launch.
 HYBRID_PANEL_FIRST = False
-PANEL_RUNS = 4
+PANEL_RUNS = 2.5
 PANEL_MIN_SHARE = 0.25
 FORCE_PANEL_ROW_MIN = None
 # Combine windows of the XCS layout: consecutive rows with at most this many partial slots
@@ -675,7 +679,7 @@ def panel_row_min(n_cols, value_bytes):
     if FORCE_PANEL_ROW_MIN is not None:
         return int(FORCE_PANEL_ROW_MIN)
     n_panels = -(-int(n_cols) >> _panel_col_bits(n_cols, value_bytes))
-    return PANEL_RUNS * max(1, n_panels)
+    return int(PANEL_RUNS * max(1, n_panels))
 
 
 def plan_panel_chunks_prefix(panel_runs, run_len, chunk, runs_cap):

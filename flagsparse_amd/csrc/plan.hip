@@ -145,49 +145,57 @@ int launch_plan(const void* rowptr, int64_t n_rows, int64_t window, int64_t nnz_
   return check_hip(hipGetLastError(), "plan_windows_kernel launch");
 }
 
-// The chunk plan of the panel layout on the device, one thread per panel: the greedy rule of
+// The chunk plan of the panel layout on the device, one wave per panel: the greedy rule of
 // fsp_plan_panel_chunks (abi.cpp) over the panel's runs in order - a run starts where the
 // previous one ended, unless the open chunk already holds runs_cap runs (the rest of the
 // chunk is padding); a run longer than the chunk's free space continues in the next chunks
 // (each piece counts as a run of the chunk it lies in); the panel's last chunk is padded.
 // Writes each run's first position relative to its panel, and each panel's padded length.
-// The run lengths are read kPanelPlanBatch at a time, all requested before the first is used.
-constexpr int kPanelPlanBatch = 16;
-constexpr int kPanelPlanBlock = 64;
+// The wave loads 64 run lengths at a time (one coalesced load), then steps through them with
+// the chunk state (position, entries and runs of the open chunk) the same in every lane; a
+// run's pieces are taken in closed form: the rest of the open chunk, whole chunks, a tail.
+constexpr int kPanelPlanBlock = kWave;
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+  const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffff), lane);
+  const int hi = __builtin_amdgcn_readlane((int)(v >> 32), lane);
+  return ((int64_t)hi << 32) | (uint32_t)lo;
+}
 
 __global__ __launch_bounds__(kPanelPlanBlock) void plan_panel_chunks_kernel(
-    const int64_t* __restrict__ panel_runs, int64_t n_panels,
-    const int64_t* __restrict__ run_len, int64_t chunk, int64_t runs_cap,
-    int64_t* __restrict__ run_pos, int64_t* __restrict__ panel_len) {
-  const int64_t p = (int64_t)blockIdx.x * kPanelPlanBlock + threadIdx.x;
-  if (p >= n_panels) return;
+    const int64_t* __restrict__ panel_runs, const int64_t* __restrict__ run_len, int64_t chunk,
+    int64_t runs_cap, int64_t* __restrict__ run_pos, int64_t* __restrict__ panel_len) {
+  const int64_t p = blockIdx.x;
+  const int lane = threadIdx.x;
   const int64_t r0 = panel_runs[p], r1 = panel_runs[p + 1];
-  int64_t pos = 0, used = 0, runs = 0;  // the open chunk's entries and runs
-  for (int64_t rb = r0; rb < r1; rb += kPanelPlanBatch) {
-    int64_t len[kPanelPlanBatch];
-#pragma unroll
-    for (int u = 0; u < kPanelPlanBatch; ++u) len[u] = rb + u < r1 ? run_len[rb + u] : 0;
-#pragma unroll
-    for (int u = 0; u < kPanelPlanBatch; ++u) {
-      if (rb + u >= r1) break;
-      int64_t left = len[u] > 0 ? len[u] : 1;  // runs are never empty (checked by the caller)
+  int64_t pos = 0, used = 0, runs = 0;  // the open chunk's entries and runs (wave-uniform)
+  for (int64_t rb = r0; rb < r1; rb += kWave) {
+    const int n = r1 - rb < kWave ? (int)(r1 - rb) : kWave;
+    const int64_t mine = lane < n ? run_len[rb + lane] : 0;
+    int64_t my_pos = 0;
+    for (int j = 0; j < n; ++j) {
+      int64_t len = readlane64(mine, j);
+      if (len < 1) len = 1;  // runs are never empty (checked by the caller)
       if (runs == runs_cap) {  // close the chunk: the rest is padding
         pos += chunk - used;
         used = runs = 0;
       }
-      run_pos[rb + u] = pos;
-      while (left > 0) {
-        const int64_t piece = left < chunk - used ? left : chunk - used;
+      if (lane == j) my_pos = pos;
+      const int64_t space = chunk - used;
+      pos += len;
+      if (len < space) {
+        used += len;
         ++runs;
-        used += piece;
-        pos += piece;
-        left -= piece;
-        if (used == chunk) used = runs = 0;
+      } else {  // fills the open chunk, then whole chunks, then a tail (a piece of its own)
+        const int64_t tail = (len - space) % chunk;
+        used = tail;
+        runs = tail ? 1 : 0;
       }
     }
+    if (lane < n) run_pos[rb + lane] = my_pos;
   }
   if (used > 0) pos += chunk - used;  // the panel's last chunk
-  panel_len[p] = pos;
+  if (lane == 0) panel_len[p] = pos;
 }
 
 }  // namespace
@@ -205,10 +213,11 @@ extern "C" int fsp_plan_panel_chunks_device(const int64_t* panel_runs, int64_t n
   if (n_panels == 0) return FSP_OK;
   if (!panel_runs || !panel_len || !run_len || !run_pos)
     return set_error(FSP_EINVAL, "fsp_plan_panel_chunks_device: null pointer");
-  const int64_t blocks = (n_panels + kPanelPlanBlock - 1) / kPanelPlanBlock;
-  hipLaunchKernelGGL(plan_panel_chunks_kernel, dim3((unsigned)blocks), dim3(kPanelPlanBlock), 0,
-                     static_cast<hipStream_t>(stream), panel_runs, n_panels, run_len, chunk,
-                     runs_cap, run_pos, panel_len);
+  if (n_panels > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_plan_panel_chunks_device: too many panels");
+  hipLaunchKernelGGL(plan_panel_chunks_kernel, dim3((unsigned)n_panels), dim3(kPanelPlanBlock), 0,
+                     static_cast<hipStream_t>(stream), panel_runs, run_len, chunk, runs_cap,
+                     run_pos, panel_len);
   return check_hip(hipGetLastError(), "plan_panel_chunks_kernel launch");
 }
 

@@ -116,7 +116,7 @@ int fsp_plan_panel_chunks(const int64_t* panel_runs, int64_t n_panels, const int
                           int64_t chunk, int64_t runs_cap, int64_t* run_pos, int64_t* panel_end);
 
 /*
- * The same chunk plan on the device (no host copy, no host loop), one thread per panel; the
+ * The same chunk plan on the device (no host copy, no host loop), one wave per panel; the
  * prepare step takes it when a prefix sum of the run lengths does not already give the plan
  * (a chunk of more than runs_cap runs).  panel_runs, run_len: device int64 as above (every
  * run of at least one entry, not checked here); outputs, device int64: run_pos[r] = the

@@ -468,10 +468,10 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 //      sums is a window of its own) and their exclusive scan over the window - the row's first
 //      LDS position; thread t holds rows t, t + NB, ..., scanned block by block (a wave scan
 //      each), the wave totals of every block exchanged at the barrier of step 1;
-//   3. gives row r the sum of its positions, in order, and writes y.  Rows of one or two sums
-//      are summed by the thread that holds them; rows with more are listed in LDS and shared
-//      out among all the threads (measured on MI355X, cfg3: 42.5 -> 40.8 us; each wave had
-//      run its row loops as long as its longest row).
+//   3. gives row r the sum of its positions, in order, and writes y.  Rows of at most kInline
+//      sums are summed by the thread that holds them; rows with more are listed in LDS and
+//      shared out among all the threads (measured on MI355X, cfg3: 42.5 -> 40.8 us; each wave
+//      had run its row loops as long as its longest row).
 // A window of one row with more sums than a window takes ({row, -1, ...}) is summed by the
 // whole workgroup - thread t takes its slots t, t + NB, ... in order, then the fixed workgroup
 // tree.
@@ -484,6 +484,10 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 // allows 4 workgroups per CU: with 512 threads that is every wave slot of the CU.  Measured on
 // MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024.
 constexpr int kCombBlock = 512;
+// Sums of a row added by the thread that holds it (rows with more go to the shared list).
+// Measured on MI355X: cfg3 36.2 / 36.5 / 36.4 us with 2 / 3 / 4, cfg4 (rows of about four
+// sums) 18.2 / 18.3 / 17.4 us.
+constexpr int kInline = 4;
 
 // Inclusive scan of c over the wave (DPP, as the count part of wave_seg_scan).
 __device__ __forceinline__ int wave_incl_scan(int c) {
@@ -594,22 +598,24 @@ __device__ __forceinline__ void combine_window(
     before += blk;
   }
 
-  // The first two sums of all the thread's rows are requested together (most rows have at
-  // most two); rows with more are listed and summed afterwards by all threads, in order.
+  // The first kInline sums of all the thread's rows are requested together (most rows have
+  // fewer); rows with more are listed and summed afterwards by all threads, in order.
   A acc[kRowsPer];
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    const A t0 = cnt[m] > 0 ? s_val[rs[m]] : A(0);
-    const A t1 = cnt[m] > 1 ? s_val[rs[m] + 1] : A(0);
+    A t[kInline];
+#pragma unroll
+    for (int u = 0; u < kInline; ++u) t[u] = cnt[m] > u ? s_val[rs[m] + u] : A(0);
     acc[m] = A(0);
-    if (cnt[m] > 0) acc[m] += t0;
-    if (cnt[m] > 1) acc[m] += t1;
+#pragma unroll
+    for (int u = 0; u < kInline; ++u)
+      if (cnt[m] > u) acc[m] += t[u];
   }
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
     const int i = row_of(m);
     if (i < nr && !skip[m]) {
-      if (cnt[m] > 2) {
+      if (cnt[m] > kInline) {
         s_long[atomicAdd(&s_nlong, 1)] = (i << 20) | (rs[m] << 8) | cnt[m];
       } else {
         const int row = row0 + i;

@@ -485,9 +485,9 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 // MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024.
 constexpr int kCombBlock = 512;
 // Sums of a row added by the thread that holds it (rows with more go to the shared list).
-// Measured on MI355X: cfg3 36.2 / 36.5 / 36.4 us with 2 / 3 / 4, cfg4 (rows of about four
-// sums) 18.2 / 18.3 / 17.4 us.
-constexpr int kInline = 4;
+// Measured on MI355X, whole call: cfg3 268.1 / 268.3 / 269.1 us with 2 / 3 / 4; the combine of
+// cfg4 (rows of about four sums) 18.2 / 18.3 / 17.4 us.
+constexpr int kInline = 2;
 
 // Inclusive scan of c over the wave (DPP, as the count part of wave_seg_scan).
 __device__ __forceinline__ int wave_incl_scan(int c) {

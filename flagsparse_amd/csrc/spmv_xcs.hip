@@ -482,7 +482,8 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
 // cfg4 14.7 / 14.4 / 13.8).
 // Threads per combine workgroup.  A window's LDS (its 4096 sums, 32 KiB, and the row list)
 // allows 4 workgroups per CU: with 512 threads that is every wave slot of the CU.  Measured on
-// MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024.
+// MI355X, cfg3: 41.1 us with 256 threads, 36.7 us with 512, 38.1 us with 1024 (then with 3
+// workgroups per CU, the row list taking more LDS than it can need).
 constexpr int kCombBlock = 512;
 // Sums of a row added by the thread that holds it (rows with more go to the shared list).
 // Measured on MI355X, whole call: cfg3 268.1 / 268.3 / 269.1 us with 2 / 3 / 4; the combine of
@@ -520,10 +521,14 @@ __device__ __forceinline__ void combine_window(
   A* const s_val = reinterpret_cast<A*>(s_dyn);
   __shared__ A s_red[kWaves];
   __shared__ int s_wtot[kRowsPer][kWaves];
-  // Rows with more than two sums, listed for a second pass: (row in the window << 20) | (first
-  // position << 8) | sums.
+  // Rows with more than kInline sums, listed for a second pass: (row in the window << 20) |
+  // (first position << 8) | sums.  A window holds at most kXcsWinSlotsCap sums, so at most
+  // kXcsWinSlotsCap / (kInline + 1) such rows; sized so, the list leaves the LDS of four
+  // workgroups per CU (a list of kXcsWinRowsCap entries put 40.2 KiB in each and allowed three:
+  // measured on MI355X, cfg3's combine 41.6 -> 40.8 us, the whole call 267.5 -> 265.4 us).
+  constexpr int kLongCap = (int)kXcsWinSlotsCap / (kInline + 1);
   __shared__ int s_nlong;
-  __shared__ int s_long[kXcsWinRowsCap];
+  __shared__ int s_long[kLongCap];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
   if (tid == 0) s_nlong = 0;  // read after the barrier below
@@ -616,7 +621,8 @@ __device__ __forceinline__ void combine_window(
     const int i = row_of(m);
     if (i < nr && !skip[m]) {
       if (cnt[m] > kInline) {
-        s_long[atomicAdd(&s_nlong, 1)] = (i << 20) | (rs[m] << 8) | cnt[m];
+        const int at = atomicAdd(&s_nlong, 1);
+        if (at < kLongCap) s_long[at] = (i << 20) | (rs[m] << 8) | cnt[m];  // always, in a layout
       } else {
         const int row = row0 + i;
         y[row_map ? row_map[row] : row] = T(acc[m]);
@@ -624,7 +630,7 @@ __device__ __forceinline__ void combine_window(
     }
   }
   __syncthreads();
-  const int n_long = s_nlong;
+  const int n_long = s_nlong < kLongCap ? s_nlong : kLongCap;
   for (int j = tid; j < n_long; j += NB) {
     const int e = s_long[j];
     const int i = e >> 20, a = (e >> 8) & 0xfff, b = a + (e & 0xff);

@@ -88,12 +88,13 @@ __device__ __forceinline__ void wave_seg_scan(int& h, A& v, int& c) {
   seg_scan_step<kDppRowBcast31, 0xC>(h, v, c);
 }
 
-// Occupancy cap.  The kernel needs at most 16 KiB of LDS (its partial-sum buffer) and 64
-// VGPRs, so up to 8 workgroups would share a CU; measured on MI355X, 5 per CU gathers fastest
-// (cfg3: 562 us at 5, 574 at 6 and 7, 646 at 8; cfg4: 234 vs 263 us) - more waves only queue
-// more x requests at the XCD's L2.  The launch adds unused dynamic LDS up to this many bytes
-// per workgroup, so that floor(160 KiB / kXcsLdsPerWorkgroup) = 5.
-constexpr unsigned kXcsLdsPerWorkgroup = 28u * 1024u;
+// Occupancy cap.  The kernel needs about 17 KiB of LDS (its partial-sum buffer, 16 KiB, and
+// the run table) and 50 VGPRs, so up to 8 workgroups would share a CU; more waves only queue
+// more x requests at the XCD's L2.  Measured on MI355X, cfg3's XCS kernel with 2 / 3 / 4 / 5 /
+// 6 / 7 / 8 workgroups per CU: 157.9 / 137.6 / 126.8 / 128.3 / 132.0 / 134.5 / 134.8 us (the
+// whole call 264.0 us at 4, 265.2 at 5).  The launch adds unused dynamic LDS up to this many
+// bytes per workgroup (with the static arrays, 39 KiB), so that four fit the CU's 160 KiB.
+constexpr unsigned kXcsLdsPerWorkgroup = 38u * 1024u;
 template <typename A>
 constexpr unsigned xcs_lds_reserve() {
   return kXcsLdsPerWorkgroup - (unsigned)(kItemCap * sizeof(A));

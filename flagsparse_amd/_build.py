@@ -6,6 +6,7 @@ compiled at run time.
 """
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -52,6 +53,20 @@ def _run(cmd):
     return proc.stdout
 
 
+def _scratch_kernels(log):
+    """Kernels whose resource-usage remarks report scratch memory per lane."""
+    found, name = set(), None
+    for line in log.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0:
+            found.add(name)
+    return found
+
+
 def build(verbose=False):
     """Compile every source for gfx950 and link the shared library.  Always recompiles."""
     hipcc = _hipcc()
@@ -61,15 +76,23 @@ def build(verbose=False):
 
     def compile_one(src):
         out = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
-        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        # device sources also report each kernel's resources (checked below)
+        lang = ["-x", "hip", "-Rpass-analysis=kernel-resource-usage"] if src.endswith(".hip") \
+            else []
         cmd = [hipcc, *HIP_FLAGS, *includes, *lang, "-c", os.path.join(CSRC, src), "-o", out]
         log = _run(cmd)
         if verbose and log.strip():
             print(log)
-        return out
+        return out, _scratch_kernels(log)
 
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+        done = list(ex.map(compile_one, SOURCES))
+    objs = [o for o, _ in done]
+    spills = sorted({k for _, ks in done for k in ks})
+    if spills:
+        # A kernel with per-lane scratch memory (spilled registers or a local array the compiler
+        # could not keep in registers) pays a memory round trip for what should be a register.
+        raise RuntimeError("kernels using scratch memory:\n  " + "\n  ".join(spills))
     tmp = LIB_PATH + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB_PATH)

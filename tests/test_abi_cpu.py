@@ -268,3 +268,19 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert L.fsp_spmv_panels(0, 0, fake, fake, 512, 10, fake, 1024, None, None, fake, fake, 1,
                              fake + 4, fake, 64, None, None, None, 0, None) == -1
     assert b"chunk_info" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
+
+
+def test_build_flags_kernels_with_scratch():
+    # the build reads each kernel's resource-usage remarks and refuses one that uses scratch
+    # memory per lane (registers spilled, or a local array kept in memory)
+    from flagsparse_amd import _build
+
+    log = "\n".join([
+        "a.hip:1:1: remark: Function Name: _Z4goodPf [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     VGPRs: 40 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark: Function Name: _Z3badPf [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 12 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert _build._scratch_kernels(log) == {"_Z3badPf"}
+    assert _build._scratch_kernels("") == set()

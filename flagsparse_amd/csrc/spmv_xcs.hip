@@ -76,6 +76,44 @@ __device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
   c += co;
 }
 
+// The same step without a branch: lanes without a source read 0 (bound_ctrl), which is the
+// identity of all three parts (no start, +0.0, 0), and the sum is selected rather than
+// branched to.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_bc(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_bc(double v) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = dpp_bc<CTRL, ROW_MASK>((int)(b & 0xffffffff));
+  const int hi = dpp_bc<CTRL, ROW_MASK>((int)(b >> 32));
+  return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_bc(float v) {
+  return __int_as_float(dpp_bc<CTRL, ROW_MASK>(__float_as_int(v)));
+}
+template <int CTRL, int ROW_MASK, typename A>
+__device__ __forceinline__ void seg_scan_step_bc(int& h, A& v, int& c) {
+  const int ho = dpp_bc<CTRL, ROW_MASK>(h);
+  const A vo = dpp_bc<CTRL, ROW_MASK>(v);
+  const int co = dpp_bc<CTRL, ROW_MASK>(c);
+  const A sum = vo + v;
+  v = h ? v : sum;
+  h |= ho;
+  c += co;
+}
+template <typename A>
+__device__ __forceinline__ void wave_seg_scan_bc(int& h, A& v, int& c) {
+  seg_scan_step_bc<kDppRowShr1, 0xF>(h, v, c);
+  seg_scan_step_bc<kDppRowShr1 + 1, 0xF>(h, v, c);
+  seg_scan_step_bc<kDppRowShr1 + 3, 0xF>(h, v, c);
+  seg_scan_step_bc<kDppRowShr1 + 7, 0xF>(h, v, c);
+  seg_scan_step_bc<kDppRowBcast15, 0xA>(h, v, c);
+  seg_scan_step_bc<kDppRowBcast31, 0xC>(h, v, c);
+}
+
 // Inclusive scans over the wave (seg_scan_step): shifts by 1, 2, 4 and 8 inside each 16-lane
 // row, then each row's last lane to the rows after it - a fixed order of additions.
 template <typename A>
@@ -707,8 +745,9 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const int* __restrict__ job_panel, const i32x2* __restrict__ chunk_info,
     A* __restrict__ partials, int64_t n_partials) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
-  // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule).
-  __shared__ A s_stage[kPanelBlock / kWave][kWave];
+  // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule),
+  // then one slot per lane for the stores of lanes where no run ends.
+  __shared__ A s_stage[kPanelBlock / kWave][2 * kWave];
   // The partial sums as a buffer resource of n_partials slots (< 2^32 bytes, checked by the
   // host): stores beyond it are dropped by the hardware.
   const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -748,7 +787,6 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
   // padding, whose products are 0 whatever x holds.
   auto reduce_chunk = [&](const T (&v)[kPanelPerLane], const i32x4& cq, const i32x2& info) {
     const int slot0 = info.x, used = info.y;
-    A prod[kPanelPerLane];
     bool start[kPanelPerLane];
     T xg[kPanelPerLane];
     const uint32_t cw[4] = {(uint32_t)cq.x, (uint32_t)cq.y, (uint32_t)cq.z, (uint32_t)cq.w};
@@ -767,56 +805,59 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       for (int q = 0; q < kPanelPerLane; ++q)
         if (q >= lim) xg[q] = T(0);
     }
-#pragma unroll
-    for (int q = 0; q < kPanelPerLane; ++q) prod[q] = A(v[q]) * A(xg[q]);
     constexpr int kLast = kPanelPerLane - 1;
     // a chunk starts a run whatever its first entry says, and ends one (lane 63 reads 1)
     const bool cont = lane > 0 && !start[0];
     const bool end_last = dpp_mov<kDppWaveShl1>(1, (int)start[0]) != 0;
-    // Running sums of the runs inside the lane (restarted where a run starts): the run that
-    // ends at q holds run[q]; the last one is the lane's piece of a run that may go on.
+    // Running sums of the runs inside the lane (restarted where a run starts).  With float32
+    // entries and fp64 sums a product is exact, so fma(v, x, s) is the sum s + v * x rounded
+    // once, as an add of the product would be.
     int has_head = cont ? 0 : 1;
     int n_end = end_last ? 1 : 0;
     A run[kPanelPerLane];
-    run[0] = prod[0];
+    run[0] = A(v[0]) * A(xg[0]);
 #pragma unroll
     for (int q = 1; q < kPanelPerLane; ++q) {
-      run[q] = start[q] ? prod[q] : run[q - 1] + prod[q];
-      if (start[q]) {
-        has_head = 1;
-        ++n_end;
+      if constexpr (sizeof(T) == 4 && sizeof(A) == 8) {
+        run[q] = __builtin_fma(A(v[q]), A(xg[q]), start[q] ? A(0) : run[q - 1]);
+      } else {
+        const A p = A(v[q]) * A(xg[q]);
+        run[q] = start[q] ? p : run[q - 1] + p;
       }
+      has_head |= (int)start[q];
+      n_end += (int)start[q];
     }
-    // segmented scan of (has_head, last piece) and a plain scan of n_end over the wave, all
-    // through DPP: shifts by 1, 2, 4 and 8 inside each 16-lane row, then each row's last lane
-    // to the rows after it; then each lane takes the scans of the lane before it
+    // Segmented scan of (has_head, last piece) and a plain scan of n_end over the wave, all
+    // through DPP; then each lane takes the scans of the lane before it: the carry into its
+    // first run and its first slot.  (Branch-free steps, fma products and the stores below
+    // took this kernel from 107 to 84 VGPRs and 878 to 729 VALU instructions; measured on
+    // MI355X, cfg3: 94.2 -> 93.1 us, the whole call 263.6 -> 262.0 us.)
     int h_in = has_head;
-    A v_in = run[kPanelPerLane - 1];
+    A v_in = run[kLast];
     int c_in = n_end;
-    wave_seg_scan(h_in, v_in, c_in);
-    const A carry = dpp_mov<kDppWaveShr1>(A(0), v_in);   // lane 0: 0
-    const int slot = dpp_mov<kDppWaveShr1>(0, c_in);
-    // The chunk's runs take slots slot0 .. slot0 + R - 1; the run ending at q in this lane is
-    // the lane's (j - slot)-th, j counting its ends.  The lane's first run, when it continues
-    // from the lanes before (cont), adds the carry.
-    const int n_runs = __builtin_amdgcn_readlane(c_in, kWave - 1);  // R, the same in all lanes
-    // The chunk's runs (at most kPanelChunkRunsCap = kWave, a layout rule) go to this wave's
-    // LDS row in slot order, and one store of 64 consecutive slots writes them in whole lines.
-    // Stored from the lanes where the runs end, eight stores per lane pieced the lines
-    // together: cfg3's panel kernel took 90 us that way, against 80 us with a single store.
-    // (Any store that only some paths issue also costs: the compiler then cannot count the
-    // memory operations in flight and waits for all of them, the prefetched chunks included.)
+    wave_seg_scan_bc(h_in, v_in, c_in);
+    const A carry = dpp_bc<kDppWaveShr1, 0xF>(v_in);   // lane 0: 0
+    const int slot = dpp_bc<kDppWaveShr1, 0xF>(c_in);
+    const int n_runs = __builtin_amdgcn_readlane(c_in, kWave - 1);
+    // The chunk's runs go to this wave's LDS row in slot order, and one store of 64
+    // consecutive slots writes them in whole lines (stored from the lanes where the runs end,
+    // eight stores per lane pieced the lines together: 90 against 80 us on cfg3; and any
+    // store that only some paths issue makes the compiler wait for every load in flight).
+    // Every lane writes each of its eight run sums: to the run's slot where a run ends there,
+    // else to a slot of its own past the chunk's.  Then the lane's first run, when it
+    // continues from the lanes before, gets the carry.
     A* const st = s_stage[wid];
     int j = slot;
-    bool first = cont;
 #pragma unroll
     for (int q = 0; q < kPanelPerLane; ++q) {
       const bool ends = q < kLast ? start[q + 1] : end_last;
-      if (ends && j < kWave) st[j] = first ? carry + run[q] : run[q];
-      if (ends) {
-        ++j;
-        first = false;
-      }
+      st[(ends && j < kWave) ? j : kWave + lane] = run[q];
+      j += (int)ends;
+    }
+    {
+      const bool fix = cont && j > slot && slot < kWave;
+      const int at = fix ? slot : kWave + lane;
+      st[at] = st[at] + (fix ? carry : A(0));
     }
     wave_sync();  // the row is written and read by this wave only
     const A staged = st[lane];

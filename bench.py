@@ -25,7 +25,9 @@ roofline     the same bytes / the path's kernel time (all the kernels of one lau
              ``gather_bound`` (cfg3, cfg5): the probe kernels timed in the same run on the
              workload's own gather count and pattern - the rate the gathers alone reach;
              ``kernel_ms_over_bound`` divides the whole path's kernel time by it, and for cfg3
-             ``part_ms_over_bound`` the XCS part's (its kernel and combine, ``parts_ms``)
+             ``part_ms_over_bound`` the XCS part's (its kernel and combine, ``parts_ms``).
+             ``stream_bound`` (cfg3): a plain read of the bytes the panel kernel reads
+             (fsp_probe_stream), and the panel kernel's time alone over it
 cpu_baseline the reference's own CPU path (its tests' torch comparison): torch.sparse.mm on
              CPU sparse tensors of the same matrix, on all of torch's host threads (``cores``,
              OMP_NUM_THREADS: the box's CPU share), ~10 s of full products, with the same byte
@@ -318,9 +320,21 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
             "inputs": {"data": data, "indices": idx, "indptr": ptr, "x": x}}
     acc_f64 = (not use_opt) or data.dtype == torch.float64
     parts = None
+    stream_bound = None
     if kc.kind == "xcs-hybrid":  # the two parts of the launch, each timed alone
+        from flagsparse_amd import _abi
+
         parts = {"xcs_part": lambda: kc.short.launch(x, y, acc_f64),
-                 "panel_part": lambda: kc.long.launch(x, y, acc_f64)}
+                 "panel_part": lambda: kc.long.launch(x, y, acc_f64),
+                 "panel_kernel": lambda: kc.long.launch(x, y, acc_f64, passes=1,
+                                                        stream=_abi.raw_stream(dev))}
+        # what the panel kernel reads: its entries (a value and 16 bits each), x once (the
+        # panels) and the chunk table - streamed alone by the probe
+        lg = kc.long
+        read = lg.n_entries * (v + 2) + shape[1] * v + int(lg.chunk_info.numel()) * 4
+        stream_bound = lambda: _stream_bound(read, dev, torch,  # noqa: E731
+                                             f"a plain read of {read} bytes (the panel "
+                                             f"kernel's entries, x and chunk table)")
 
     def cpu(seconds):
         from oracle import oracle
@@ -346,6 +360,7 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
         "step": lambda: fs.flagsparse_spmv_csr(x=x, prepared=prepared, use_opt=use_opt, out=y),
         "launch": lambda: mod._run_spmv_csr(prepared, x, use_opt, y),
         "parts": parts, "gather_bound": gather_bound, "bound_part": "xcs_part",
+        "stream_bound": stream_bound, "stream_part": "panel_kernel",
         "bytes_gather_inclusive": nnz * (v + 4 + v) + (shape[0] + 1) * p_k + shape[0] * v,
         "nbytes": nbytes, "flops": 2 * nnz, "info": info, "cpu": cpu,
         "cpu_lib": _cpu_lib("csr", (ptr, idx, data), x, shape, nbytes, 2 * nnz, torch),
@@ -630,6 +645,28 @@ def _bound(call, n, what, torch):
             "G_per_s": round(n / (ms * 1e-3) / 1e9, 2)}
 
 
+def _stream_bound(nbytes, dev, torch, what):
+    """A plain read of nbytes (fsp_probe_stream) timed as _bound times the gather probes."""
+    from flagsparse_amd import _abi
+
+    L = _abi.lib()
+    n16 = max(1, int(nbytes) // 16)
+    src = torch.empty(n16 * 16, dtype=torch.uint8, device=dev)
+    out = torch.empty(max(1, int(L.fsp_probe_stream_blocks(n16))), dtype=torch.float32,
+                      device=dev)
+
+    def call():
+        _abi.check(L.fsp_probe_stream(src.data_ptr(), n16, out.data_ptr(),
+                                      _abi.raw_stream(dev)), "fsp_probe_stream")
+
+    for _ in range(3):
+        call()
+    ms = sorted(_event_loop(call, 20, torch) for _ in range(5))[2]
+    del src, out
+    return {"pattern": what, "bytes": n16 * 16, "ms": round(ms, 6),
+            "GB_per_s": round(n16 * 16 / (ms * 1e-3) / 1e9, 1)}
+
+
 def _gather_bound(x_len, n, xcd, dev, torch, what):
     return _bound(_probe_gather_call(x_len, n, xcd, dev, torch), n, what, torch)
 
@@ -779,6 +816,13 @@ def _roofline(w, ms_kernel, kernel_runs, torch):
             gb["part"] = w["bound_part"]
             gb["part_ms_over_bound"] = round(out["parts_ms"][w["bound_part"]] / gb["ms"], 3)
         out["gather_bound"] = gb
+    if w.get("stream_bound"):
+        sb = w["stream_bound"]()
+        part = w.get("stream_part")
+        if part and part in out.get("parts_ms", {}):
+            sb["part"] = part
+            sb["part_ms_over_bound"] = round(out["parts_ms"][part] / sb["ms"], 3)
+        out["stream_bound"] = sb
     return out
 
 

@@ -73,6 +73,8 @@ SIGNATURES = {
     "fsp_probe_gather": (_i32, [_p, _i64, _p, _i64, _p, _p]),
     "fsp_probe_rows_blocks": (_i64, [_i64]),
     "fsp_probe_rows": (_i32, [_p, _i64, _i64, _p, _i64, _p, _p]),
+    "fsp_probe_stream_blocks": (_i64, [_i64]),
+    "fsp_probe_stream": (_i32, [_p, _i64, _p, _p]),
 }
 
 

@@ -8,6 +8,9 @@
 //   probe_rows_kernel    random row gathers from a row-major matrix: 16 lanes share one row of
 //                        row_bytes (16 bytes each), each lane has four rows in flight - the
 //                        pattern of the SpMM B-row gathers (spmm_rowblock_kernel, N = 64 fp32)
+//   probe_stream_kernel  a plain read of a contiguous range with non-temporal 16-byte loads,
+//                        eight in flight per thread - the entry stream of the panel kernel
+//                        (spmv_panel_kernel) without its LDS gathers, sums and stores
 //
 // Every workgroup writes the sum of what it loaded to out[blockIdx.x] (a fixed-order reduction),
 // so no load can be dropped by the compiler and the write traffic is one value per workgroup.
@@ -77,6 +80,27 @@ __global__ __launch_bounds__(kBlock) void probe_rows_kernel(const float* __restr
   if (threadIdx.x == 0) out[blockIdx.x] = acc;
 }
 
+constexpr int kStreamPer = 8;  // 16-byte loads per thread
+
+__global__ __launch_bounds__(kBlock) void probe_stream_kernel(const i32x4* __restrict__ src,
+                                                              int64_t n16,
+                                                              float* __restrict__ out) {
+  __shared__ float red[kWavesPerBlock];
+  const int64_t v0 = (int64_t)blockIdx.x * kBlock * kStreamPer + threadIdx.x;
+  i32x4 v[kStreamPer];
+#pragma unroll
+  for (int u = 0; u < kStreamPer; ++u) {
+    const int64_t i = v0 + (int64_t)u * kBlock;
+    v[u] = ld_stream<true>(src + (i < n16 ? i : n16 - 1));  // the tail reloads the last one
+  }
+  int acc = 0;
+#pragma unroll
+  for (int u = 0; u < kStreamPer; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  float f = (float)(acc & 1);
+  f = block_sum(f, red);
+  if (threadIdx.x == 0) out[blockIdx.x] = f;
+}
+
 }  // namespace
 }  // namespace fsp
 
@@ -124,4 +148,22 @@ extern "C" int fsp_probe_rows(const float* b, int64_t n_rows, int64_t row_floats
                      static_cast<hipStream_t>(stream), b, (unsigned)(n_rows - 1), row_floats, rows,
                      n, out);
   return check_hip(hipGetLastError(), "probe_rows_kernel launch");
+}
+
+extern "C" int64_t fsp_probe_stream_blocks(int64_t n16) {
+  const int64_t per_block = (int64_t)kBlock * kStreamPer;
+  return n16 <= 0 ? 0 : (n16 + per_block - 1) / per_block;
+}
+
+extern "C" int fsp_probe_stream(const void* src, int64_t n16, float* out, void* stream) {
+  if (n16 < 0) return set_error(FSP_EINVAL, "fsp_probe_stream: negative size");
+  if (n16 == 0) return FSP_OK;
+  if (!src || !out) return set_error(FSP_EINVAL, "fsp_probe_stream: null");
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) != 0)
+    return set_error(FSP_EINVAL, "fsp_probe_stream: src must be 16-byte aligned");
+  const int64_t blocks = fsp_probe_stream_blocks(n16);
+  if (blocks > 0x7fffffffLL) return set_error(FSP_EINVAL, "fsp_probe_stream: n16 too large");
+  hipLaunchKernelGGL(probe_stream_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const i32x4*>(src), n16, out);
+  return check_hip(hipGetLastError(), "probe_stream_kernel launch");
 }

@@ -406,6 +406,9 @@ int fsp_mtx_read(const char* path, int64_t* info, int64_t* rows, int64_t* cols, 
  *   fsp_probe_rows    n random gathers of whole 256-byte rows b[rows[i]][0..64) from a
  *                     row-major fp32 b[n_rows][64], 16 lanes per row, 4 rows per lane in
  *                     flight (row indices clamped into b)
+ *   fsp_probe_stream  a read of n16 consecutive 16-byte vectors from src (16-byte aligned),
+ *                     non-temporal loads, 8 per thread in flight (the value written is a parity
+ *                     bit count, only there so that no load can be dropped)
  */
 int64_t fsp_probe_gather_blocks(int64_t n);
 int fsp_probe_gather(const float* x, int64_t x_len, const int32_t* idx, int64_t n, float* out,
@@ -413,6 +416,8 @@ int fsp_probe_gather(const float* x, int64_t x_len, const int32_t* idx, int64_t 
 int64_t fsp_probe_rows_blocks(int64_t n);
 int fsp_probe_rows(const float* b, int64_t n_rows, int64_t row_floats, const int32_t* rows,
                    int64_t n, float* out, void* stream);
+int64_t fsp_probe_stream_blocks(int64_t n16);
+int fsp_probe_stream(const void* src, int64_t n16, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -107,3 +107,38 @@ def test_comprehensive_spmm_test(dev):
     _check_schema(r, SPMM_KEYS)
     assert r["parameters"]["value_dtype"] == str(torch.float64)
     assert r["verification"]["triton_match_reference"]
+
+
+def test_measurement_probes(dev):
+    # bench.py's probes: the gather probe sums what it gathered (x of ones: one per gather), the
+    # row probe likewise (rows of ones: 64 per row), the stream probe counts per workgroup the
+    # parity of what it read (a buffer of zeros: 0), over every workgroup's share
+    from flagsparse_amd import _abi
+
+    L = _abi.lib()
+    s = _abi.raw_stream(dev)
+    n = 4096 * 3 + 8
+    x = torch.ones(1000, dtype=torch.float32, device=dev)
+    idx = torch.randint(0, 1000, (n,), dtype=torch.int32, device=dev)
+    out = torch.zeros(int(L.fsp_probe_gather_blocks(n)), dtype=torch.float32, device=dev)
+    print("probe gather", flush=True)
+    _abi.check(L.fsp_probe_gather(x.data_ptr(), 1000, idx.data_ptr(), n, out.data_ptr(), s), "g")
+    torch.cuda.synchronize()
+    assert float(out.sum()) == n
+    b = torch.ones((300, 64), dtype=torch.float32, device=dev)
+    rows = torch.randint(0, 300, (777,), dtype=torch.int32, device=dev)
+    out = torch.zeros(int(L.fsp_probe_rows_blocks(777)), dtype=torch.float32, device=dev)
+    print("probe rows", flush=True)
+    _abi.check(L.fsp_probe_rows(b.data_ptr(), 300, 64, rows.data_ptr(), 777, out.data_ptr(), s),
+               "r")
+    torch.cuda.synchronize()
+    assert float(out.sum()) == 777 * 64
+    n16 = 2048 * 5 + 3
+    src = torch.zeros(n16 * 16, dtype=torch.uint8, device=dev)
+    out = torch.full((int(L.fsp_probe_stream_blocks(n16)),), -1.0, device=dev)
+    assert out.numel() == 6
+    print("probe stream", flush=True)
+    _abi.check(L.fsp_probe_stream(src.data_ptr(), n16, out.data_ptr(), s), "s")
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.zeros_like(out))
+    assert L.fsp_probe_stream(src.data_ptr() + 4, n16, out.data_ptr(), s) == -1  # misaligned

@@ -62,23 +62,8 @@ constexpr int kRowsCap = (int)kXcsRowsCap;
 constexpr int kItemRuns = (int)kXcsItemRunsCap;
 static_assert(kItemRuns <= kBlock, "an item's runs are loaded one per thread");
 
-// One step of the wave scans of the XCS and panel kernels: (h, v) a segmented inclusive scan
-// (h: a run starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c
-// a plain one, with the source lane that the DPP control CTRL selects.  Lanes without a source
-// take the identity (no start, -0.0, 0): -0.0 + v is v for every v.
-template <int CTRL, int ROW_MASK, typename A>
-__device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
-  const int ho = dpp_mov<CTRL, ROW_MASK>(0, h);
-  const A vo = dpp_mov<CTRL, ROW_MASK>(A(-0.0), v);
-  const int co = dpp_mov<CTRL, ROW_MASK>(0, c);
-  if (!h) v = vo + v;
-  h |= ho;
-  c += co;
-}
-
-// The same step without a branch: lanes without a source read 0 (bound_ctrl), which is the
-// identity of all three parts (no start, +0.0, 0), and the sum is selected rather than
-// branched to.
+// DPP move with bound_ctrl: the value of the lane that CTRL selects, 0 where that lane lies
+// outside the control's range or ROW_MASK leaves the lane's row out.
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ int dpp_bc(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
@@ -94,8 +79,14 @@ template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ float dpp_bc(float v) {
   return __int_as_float(dpp_bc<CTRL, ROW_MASK>(__float_as_int(v)));
 }
+
+// One step of the wave scans of the XCS and panel kernels: (h, v) a segmented inclusive scan
+// (h: a run starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c
+// a plain one, with the source lane that the DPP control CTRL selects.  Lanes without a source
+// read 0, the identity of all three parts (no start, +0.0, 0), and the sum is selected rather
+// than branched to (a branch per step cost the panel kernel a third of its scan instructions).
 template <int CTRL, int ROW_MASK, typename A>
-__device__ __forceinline__ void seg_scan_step_bc(int& h, A& v, int& c) {
+__device__ __forceinline__ void seg_scan_step(int& h, A& v, int& c) {
   const int ho = dpp_bc<CTRL, ROW_MASK>(h);
   const A vo = dpp_bc<CTRL, ROW_MASK>(v);
   const int co = dpp_bc<CTRL, ROW_MASK>(c);
@@ -103,15 +94,6 @@ __device__ __forceinline__ void seg_scan_step_bc(int& h, A& v, int& c) {
   v = h ? v : sum;
   h |= ho;
   c += co;
-}
-template <typename A>
-__device__ __forceinline__ void wave_seg_scan_bc(int& h, A& v, int& c) {
-  seg_scan_step_bc<kDppRowShr1, 0xF>(h, v, c);
-  seg_scan_step_bc<kDppRowShr1 + 1, 0xF>(h, v, c);
-  seg_scan_step_bc<kDppRowShr1 + 3, 0xF>(h, v, c);
-  seg_scan_step_bc<kDppRowShr1 + 7, 0xF>(h, v, c);
-  seg_scan_step_bc<kDppRowBcast15, 0xA>(h, v, c);
-  seg_scan_step_bc<kDppRowBcast31, 0xC>(h, v, c);
 }
 
 // Inclusive scans over the wave (seg_scan_step): shifts by 1, 2, 4 and 8 inside each 16-lane
@@ -835,7 +817,7 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     int h_in = has_head;
     A v_in = run[kLast];
     int c_in = n_end;
-    wave_seg_scan_bc(h_in, v_in, c_in);
+    wave_seg_scan(h_in, v_in, c_in);
     const A carry = dpp_bc<kDppWaveShr1, 0xF>(v_in);   // lane 0: 0
     const int slot = dpp_bc<kDppWaveShr1, 0xF>(c_in);
     const int n_runs = __builtin_amdgcn_readlane(c_in, kWave - 1);

@@ -118,7 +118,10 @@ SORTED_TILE_ITEMS = 8
 # reach.  Measured on MI355X: cfg4 (rows of 21 entries over 4 panels, 5.3 per panel) 193 ->
 # 186 us in the XCS kernel; cfg3's short rows (2.0 per panel: most rows put one entry into
 # each panel they reach, so most entries are row runs of their own) 142 us with row-order
-# items, 144-155 us with sorted ones for tiles of 6144 to 16384 rows.
+# items, 144-155 us with sorted ones for tiles of 6144 to 16384 rows; with sorted items of
+# 2048 entries in workgroups of 256 (the row-order items' tiles and sizes, results
+# bit-identical) 130.5 us against 126.7 us - the LDS permutation back to row order costs more
+# than the sorted gathers save.
 SORTED_MIN_RUN = 3.0
 
 

@@ -317,6 +317,7 @@ constexpr int kSortedWaves = kSortedBlock / kWave;
 constexpr int kSortedCap = (int)kXcsSortedItemCap;
 constexpr int kSortedPer = kSortedCap / kSortedBlock;
 static_assert(kSortedPer == 8, "eight entries per thread");
+constexpr int kSortedWaveEntries = kWave * kSortedPer;  // 512: a wave's share of an item
 constexpr unsigned kSortedColBits = (unsigned)kXcsSortedColBits;
 constexpr unsigned kSortedColMask = (1u << kSortedColBits) - 1u;
 constexpr unsigned kSortedPosShift = kSortedColBits + 1u;
@@ -362,7 +363,7 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
   if (tid < n_ir) my_run = item_runs[run0 + tid];
 
   // Threads [0, P/8) hold entries; the others re-read thread 0's quads and drop them.
-  const int n_thr = (len + kSortedBlock - 1) / kSortedBlock * (kSortedBlock / kPer);
+  const int n_thr = (len + kSortedWaveEntries - 1) / kSortedWaveEntries * kWave;
   const int tt = tid < n_thr ? tid : 0;
   T v[kPer];
   uint32_t g[kPer];
@@ -386,12 +387,12 @@ __global__ __launch_bounds__(kSortedBlock) void spmv_xcs_sorted_kernel(
   T xv[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const bool ok = tid < n_thr && wid * kSortedBlock + k * kWave + lane < len;
+    const bool ok = tid < n_thr && wid * kSortedWaveEntries + k * kWave + lane < len;
     xv[k] = x[cbase + (ok ? (int)(g[k] & kSortedColMask) : 0)];
   }
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    if (tid < n_thr && wid * kSortedBlock + k * kWave + lane < len) {
+    if (tid < n_thr && wid * kSortedWaveEntries + k * kWave + lane < len) {
       const int p = (int)(g[k] >> kSortedPosShift);
       s_x[p] = xv[k];
       s_fl[p] = (unsigned char)((g[k] >> kSortedColBits) & 1u);

@@ -22,12 +22,14 @@ roofline     the same bytes / the path's kernel time (all the kernels of one lau
              which the kernel moves the bytes it does move).  ``bytes_gather_inclusive``
              counts x (SpMV) or B (SpMM) once per entry instead of once, and
              ``frac_gather_inclusive`` is that count over the same time against the peak.
-             ``gather_bound`` (cfg3, cfg5): the probe kernels timed in the same run on the
-             workload's own gather count and pattern - the rate the gathers alone reach;
+             ``gather_bound`` (cfg5; cfg3 with the XCS layouts): the probe kernels timed in
+             the same run on the workload's own gather count and pattern - the rate the
+             gathers alone reach;
              ``kernel_ms_over_bound`` divides the whole path's kernel time by it, and for cfg3
              ``part_ms_over_bound`` the XCS part's (its kernel and combine, ``parts_ms``).
              ``stream_bound`` (cfg3): a plain read of the bytes the panel kernel reads
-             (fsp_probe_stream), and the panel kernel's time alone over it
+             (fsp_probe_stream), and the panel kernel's time alone over it (with the
+             staged-x layout the panel kernel also writes the staged x values)
 cpu_baseline the reference's own CPU path (its tests' torch comparison): torch.sparse.mm on
              CPU sparse tensors of the same matrix, on all of torch's host threads (``cores``,
              OMP_NUM_THREADS: the box's CPU share), ~10 s of full products, with the same byte
@@ -321,6 +323,21 @@ def _spmv_csr_workload(name, dev, opt, torch, fs, synthetic):
     acc_f64 = (not use_opt) or data.dtype == torch.float64
     parts = None
     stream_bound = None
+    if kc.kind == "xstage":  # the two launches, each timed alone
+        # the first launch reads the long rows' entries (a value and 16 bits each), x once (the
+        # panels), the chunk table and the staged entries' 16-bit columns, and writes the
+        # staged x values and the long rows' partial sums; the probe streams its reads alone
+        lg = kc.long
+        read = shape[1] * v + kc.n_staged * 2
+        if lg is not None:
+            read += lg.n_entries * (v + 2) + int(lg.chunk_info.numel()) * 4
+        parts = {"panel_kernel": lambda: kc.launch(x, y, acc_f64, passes=1),
+                 "combine": lambda: kc.launch(x, y, acc_f64, passes=2)}
+        stream_bound = lambda: _stream_bound(read, dev, torch,  # noqa: E731
+                                             f"a plain read of {read} bytes (what the panel "
+                                             f"kernel reads: entries, staged columns, x and "
+                                             f"chunk table; not its {kc.n_staged * v} bytes of "
+                                             f"staged x written)")
     if kc.kind == "xcs-hybrid":  # the two parts of the launch, each timed alone
         from flagsparse_amd import _abi
 

@@ -26,6 +26,14 @@ The layouts below, chosen once per matrix at prepare time:
     ``PanelLayout`` for the rows long enough to put several entries in every panel,
     ``XcsLayout`` for the others; both parts run one after the other on the caller's stream.
 
+``XstageLayout`` (csrc/spmv_xcs.hip: ``spmv_panel_kernel`` + ``stage_combine_kernel``)
+    The default where columns are spread over an x larger than an L2: the long rows as in
+    ``PanelLayout``, and for the other rows the panel jobs also *stage* x - entry e of panel p
+    gets xs[e] = x[its column], read from the same LDS copy of the panel - so no entry gathers
+    from L2.  A second launch takes windows of consecutive rows: each entry's value times its
+    staged x, placed in LDS in (row, panel) order, and each row's products summed in that
+    fixed order (deterministic), beside the long rows' partial sums.
+
 Both replace the reference's per-bucket launches (spmv_csr.py:281-376) and produce the same
 row sums up to floating-point summation order.
 """
@@ -51,10 +59,14 @@ MIN_PANELS = 4
 NEAR_COLUMNS = 1 << 16
 SAMPLE = 1 << 20
 
-# Test hooks: layout (None: choose per matrix, "rowblock", "xcs" - hybrid when the long rows
-# qualify -, "xcs-l2" - never hybrid - or "xcs-hybrid" - hybrid whenever there is a long row);
-# panels per XCD (None: from the size of x).
+# Test hooks: layout (None: choose per matrix, "rowblock", "xstage", "xcs" - hybrid when the
+# long rows qualify -, "xcs-l2" - never hybrid - or "xcs-hybrid" - hybrid whenever there is a
+# long row); panels per XCD (None: from the size of x).
 FORCE = None
+# Matrices whose columns are spread over an x larger than an L2 take the staged-x layout
+# (False: the XCS layouts).  Measured on MI355X, cfg3's short rows (26.4M entries, both passes):
+# 123 us staged against 161 us as XCS items and their combine.
+STAGED = True
 # Row-block SpMV launches in hardware order (workgroup i on XCD i % 8): on MI355X this streamed
 # faster than one contiguous descriptor range per XCD (cfg2 60.5 vs 64.7 us, cfg1 9.7 vs 12.0
 # us; banded and power-law matrices within 1%).
@@ -875,6 +887,7 @@ class PanelLayout:
         self.pcol[:n_entries] = torch.where(pc >= (1 << 15), pc - (1 << 16), pc).to(torch.int16)
         del pc, starts, slot_row, dest, order, row_s, cols32, run_first, run_len, run_pos
         panel_start = torch.cat([panel_end.new_zeros(1), panel_end[:-1]])
+        self.panel_chunk0 = panel_start // chunk  # each panel's first chunk
         # jobs: a panel's chunks cut evenly into the fewest jobs of <= PANEL_JOB_CHUNKS (equal
         # sizes keep the rounds of workgroups even)
         per_panel = (panel_end - panel_start) // chunk
@@ -920,7 +933,7 @@ class PanelLayout:
                     self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
                     p(self.job_panel), self.n_jobs, p(self.chunk_info), p(self.partials),
                     int(self.partials.numel()), p(self.rows), p(self.row_ptr), p(self.slots),
-                    self.n_rows, None]
+                    self.n_rows, None, None, None, 0, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
@@ -929,7 +942,7 @@ class PanelLayout:
             a[12] = 0
         if not passes & 2:
             a[19] = 0
-        a[20] = stream if stream is not None else self._order.stream(y.device, self._keep)
+        a[24] = stream if stream is not None else self._order.stream(y.device, self._keep)
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 
@@ -1012,6 +1025,228 @@ class XcsHybridLayout:
         return y
 
 
+class XstageLayout:
+    """Long rows in a PanelLayout (``self.long``, None when there are none), the other rows
+    staged (module docstring).  Built on the device.  ValueError when x needs more panels than
+    the combine takes (fsp_stage_panels_cap())."""
+
+    kind = "xstage"
+
+    def __init__(self, data, cols, rowptr, n_cols, long_mask):
+        dev = data.device
+        caps = _abi.caps()
+        rp = rowptr.to(torch.int64)
+        lengths = rp[1:] - rp[:-1]
+        n_rows = int(lengths.numel())
+        self.n_rows, self.n_cols, self.nnz = n_rows, int(n_cols), int(data.numel())
+        cb = _panel_col_bits(n_cols, data.element_size())
+        P = max(1, -(-self.n_cols >> cb))
+        if P > caps["stage_panels"]:
+            raise ValueError("x needs more panels than the staged-x combine takes")
+        self.col_bits, self.n_panels = cb, P
+        win_cap, win_rows = caps["stage_window"], caps["stage_window_rows"]
+        # A window holds every entry of its rows: rows longer than a quarter window go to the
+        # panel part whatever their length per panel, so that windows stay nearly full.
+        long_mask = long_mask | (lengths > win_cap // 4)
+        short_len = torch.where(long_mask, 0, lengths)
+        entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths,
+                                            output_size=self.nnz)
+        entry_long = long_mask[entry_row]
+
+        # 1. Windows: consecutive rows whose short entries start in [kC, (k + 1) C), so that
+        #    a window holds at most C - 1 + (the longest short row) <= win_cap entries, cut
+        #    again wherever a window would pass win_rows rows.
+        maxlen = int(short_len.max().item()) if n_rows else 0
+        C = win_cap - maxlen + 1 if maxlen > 0 else win_cap
+        start = torch.cumsum(short_len, 0) - short_len
+        w0 = start // C
+        n_w0 = int(w0[-1].item()) + 1 if n_rows else 0
+        w0_first = torch.searchsorted(w0, torch.arange(n_w0, device=dev))
+        sub = (torch.arange(n_rows, device=dev) - w0_first[w0]) // win_rows
+        key = w0 * (n_rows // win_rows + 2) + sub
+        _, win_of_row = torch.unique_consecutive(key, return_inverse=True)
+        del key, sub, w0, w0_first, start
+        W = int(win_of_row[-1].item()) + 1 if n_rows else 0
+        win_row0 = torch.searchsorted(win_of_row, torch.arange(W, device=dev))
+        win_rows_n = torch.bincount(win_of_row, minlength=W)
+        win_len = torch.zeros(W, dtype=torch.int64, device=dev).index_add_(0, win_of_row,
+                                                                           short_len)
+        win_first = torch.cumsum(win_len, 0) - win_len
+        if W and (int(win_len.max().item()) > win_cap or int(win_rows_n.max().item()) > win_rows):
+            raise AssertionError("staged-x windows: a window past its caps")
+        self.n_windows = W
+
+        # 2. Short entries (CSR order) and their panels; staged order (panel, window, row),
+        #    each panel's run padded to a multiple of 8.
+        pick = torch.nonzero(~entry_long).flatten()
+        er = entry_row[pick]
+        del entry_row, entry_long
+        ec = cols[pick].to(torch.int64)
+        n_short = int(pick.numel())
+        self.n_entries = n_short
+        pan = ec >> cb
+        ew = win_of_row[er]
+        key = pan * max(W, 1) + ew
+        ks, perm = torch.sort(key, stable=True)  # stable: row order inside a segment
+        cnt_pw = torch.bincount(key, minlength=P * W) if n_short else \
+            torch.zeros(P * W, dtype=torch.int64, device=dev)
+        del key
+        cnt_p = cnt_pw.view(P, W).sum(1)
+        padded_p = (cnt_p + 7) // 8 * 8
+        pstart = torch.cumsum(padded_p, 0) - padded_p
+        n_staged = int(padded_p.sum().item())
+        if n_staged > _INDEX_LIMIT_INT32 - (1 << 16):
+            raise ValueError("too many entries for the staged-x layout")
+        self.n_staged = n_staged
+        pfirst = torch.cumsum(cnt_p, 0) - cnt_p  # each panel's first sorted entry
+        kstart = torch.cumsum(cnt_pw, 0) - cnt_pw  # each (panel, window) segment's
+        sp = ks // max(W, 1)
+        spos = pstart[sp] + torch.arange(n_short, device=dev) - pfirst[sp]
+        sc = torch.zeros(n_staged + 8, dtype=torch.int32, device=dev)
+        sc[spos] = (ec[perm] & ((1 << cb) - 1)).to(torch.int32)
+        self.scol = torch.where(sc >= (1 << 15), sc - (1 << 16), sc).to(torch.int16)
+        del sc, spos
+        self.xs = torch.zeros(n_staged + 8, dtype=data.dtype, device=dev)
+        # segments: seg[w][p] = the staged position of panel p's entries of window w
+        seg = torch.empty((W + 1, P), dtype=torch.int64, device=dev)
+        seg[:W] = (pstart.view(P, 1) + kstart.view(P, W) - pfirst.view(P, 1)).t()
+        seg[W] = pstart + cnt_p
+        self.seg = seg.to(torch.int32).contiguous()
+        del seg
+
+        # 3. Window order (window, panel, row) for the values and LDS positions; the position
+        #    of an entry is its rank in the window's (row, panel) order.
+        seglen = cnt_pw.view(P, W).t()
+        lsw = torch.cumsum(seglen, 1) - seglen  # each segment's start in its window
+        sw = ks % max(W, 1)
+        wpos = win_first[sw] + lsw[sw, sp] + torch.arange(n_short, device=dev) - kstart[ks]
+        del seglen, lsw, sw, sp, ks
+        rank_key = er * P + pan  # CSR order is row order: a stable sort by (row, panel)
+        order2 = torch.sort(rank_key, stable=True)[1]
+        del rank_key
+        rank = torch.empty_like(order2)
+        rank[order2] = torch.arange(n_short, device=dev)
+        del order2
+        slot = rank - win_first[ew]
+        del rank
+        self.vals = torch.zeros(n_short + 8, dtype=data.dtype, device=dev)
+        self.vals[wpos] = data[pick][perm]
+        dest = torch.zeros(n_short + 8, dtype=torch.int32, device=dev)
+        dest[wpos] = slot[perm].to(torch.int32)
+        self.dest = dest.to(torch.int16)
+        del dest, slot, wpos, perm, pick, ec, pan, ew, er
+        rc = torch.where(long_mask, 0xFFFF, short_len).to(torch.int32)
+        self.row_count = torch.where(rc >= (1 << 15), rc - (1 << 16), rc).to(torch.int16)
+        del rc
+        self.windows = torch.stack([win_row0, win_rows_n, win_len, win_first], 1).to(
+            torch.int32).contiguous()
+
+        # 4. The long rows, and the jobs of the first launch: every panel has at least one
+        #    job (the panel part's jobs, or one without chunks); a panel's staged entries are
+        #    split evenly over its jobs, in groups of 8.
+        long_rows = torch.nonzero(long_mask).flatten()
+        self.long = None
+        if long_rows.numel():
+            pick = torch.nonzero(long_mask[torch.repeat_interleave(
+                torch.arange(n_rows, device=dev), lengths, output_size=self.nnz)]).flatten()
+            long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
+            torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
+            self.long = PanelLayout(data[pick], cols[pick], long_ptr, n_cols, long_rows)
+            del pick
+            lg = self.long
+            if lg.col_bits != cb or lg.n_panels != P:
+                raise AssertionError("staged-x layout: the panel parts disagree on the panels")
+            njp = torch.bincount(lg.job_panel.to(torch.int64), minlength=P)
+            old_first = torch.cumsum(njp, 0) - njp
+            old_jobs = lg.jobs.to(torch.int64)
+            n_chunks = int(old_jobs[-1].item())
+            chunk0 = lg.panel_chunk0.to(torch.int64)
+        else:
+            njp = torch.zeros(P, dtype=torch.int64, device=dev)
+            old_first = njp
+            old_jobs = torch.zeros(1, dtype=torch.int64, device=dev)
+            n_chunks = 0
+            chunk0 = torch.zeros(P, dtype=torch.int64, device=dev)
+        added = njp == 0
+        nj = torch.where(added, 1, njp)
+        job_panel = torch.repeat_interleave(torch.arange(P, device=dev), nj)
+        n_jobs = int(job_panel.numel())
+        jfirst = torch.cumsum(nj, 0) - nj
+        k = torch.arange(n_jobs, device=dev) - jfirst[job_panel]
+        old = (old_first[job_panel] + k).clamp(max=max(int(old_jobs.numel()) - 2, 0))
+        starts = torch.where(added[job_panel], chunk0[job_panel], old_jobs[old])
+        self.jobs = torch.cat([starts, torch.tensor([n_chunks], device=dev)]).to(
+            torch.int32).contiguous()
+        self.job_panel = job_panel.to(torch.int32).contiguous()
+        self.n_jobs = n_jobs
+        units = padded_p // 8
+        s_lo = pstart[job_panel] + (k * units[job_panel] // nj[job_panel]) * 8
+        self.stage_jobs = torch.cat([s_lo, torch.tensor([n_staged], device=dev)]).to(
+            torch.int32).contiguous()
+        del k, old, starts, s_lo, job_panel
+        self._keep = (self.scol, self.xs, self.seg, self.vals, self.dest, self.row_count,
+                      self.windows, self.jobs, self.job_panel, self.stage_jobs)
+        if self.long is not None:
+            self._keep = self._keep + self.long._keep
+        self._args = {}
+        self._order = StreamOrder(dev)
+
+    def kernel_name(self):
+        return "spmv_panel_kernel+stage_combine_kernel"
+
+    def held_bytes(self, caller=()):
+        own = tensor_bytes(self.scol, self.xs, self.seg, self.vals, self.dest, self.row_count,
+                           self.windows, self.jobs, self.job_panel, self.stage_jobs)
+        return own + (self.long.held_bytes(caller) if self.long is not None else 0)
+
+    def describe(self):
+        d = {"layout": self.kind, "panels": self.n_panels, "col_bits": self.col_bits,
+             "staged_entries": self.n_entries, "windows": self.n_windows, "jobs": self.n_jobs,
+             "long_rows": 0 if self.long is None else self.long.n_rows,
+             "long_entries": 0 if self.long is None else self.long.nnz}
+        if self.long is not None:
+            d["panel_part"] = self.long.describe()
+        return d
+
+    def launch(self, x, y, acc_f64, row_map=None, n_out=0, passes=3):
+        """Both launches (passes=3), or only the panel jobs (1: long-row partial sums and the
+        staged x) or only the row sums (2), on the caller's stream."""
+        args = self._args.get(bool(acc_f64))
+        if args is None:  # static arguments converted once per accumulation mode
+            p = lambda t: t.data_ptr() if t is not None and t.numel() else None  # noqa: E731
+            lg = self.long
+            dt = _abi.dtype_code(self.vals.dtype)
+            first = [dt, int(acc_f64), p(lg.vals) if lg else None,
+                     p(lg.pcol) if lg else None, lg.n_entries if lg else 0, self.col_bits, None,
+                     self.n_cols, None, None, p(self.jobs), p(self.job_panel), self.n_jobs,
+                     p(lg.chunk_info) if lg else None, p(lg.partials) if lg else None,
+                     int(lg.partials.numel()) if lg else 0, None, None, None, 0, p(self.scol),
+                     p(self.stage_jobs), p(self.xs), self.n_staged, None]
+            second = [dt, int(acc_f64), None, None, 0, p(self.windows), self.n_windows,
+                      p(self.seg), self.n_panels, p(self.vals), p(self.dest), self.n_entries,
+                      p(self.xs), self.n_staged + 8, p(self.row_count),
+                      p(lg.partials) if lg else None, p(lg.rows) if lg else None,
+                      p(lg.row_ptr) if lg else None, p(lg.slots) if lg else None,
+                      lg.n_rows if lg else 0, None]
+            args = (first, second)
+            self._args[bool(acc_f64)] = args
+        st = self._order.stream(y.device, self._keep)
+        L = _abi.lib()
+        if passes & 1:
+            a = list(args[0])
+            a[6], a[8] = x.data_ptr(), y.data_ptr()
+            a[24] = st
+            _abi.check(L.fsp_spmv_panels(*a), "fsp_spmv_panels")
+        if passes & 2:
+            a = list(args[1])
+            a[2] = y.data_ptr()
+            a[3] = None if row_map is None else row_map.data_ptr()
+            a[4] = n_out
+            a[20] = st
+            _abi.check(L.fsp_spmv_stage_combine(*a), "fsp_spmv_stage_combine")
+        return y
+
+
 def sample_indices(n, k, device):
     """min(n, k) indices spread evenly over [0, n), computed in exact int64 arithmetic."""
     if n <= k:
@@ -1064,7 +1299,16 @@ def build_layout(data, cols, rowptr, n_cols, one_shot=False):
     if mode is None and one_shot:
         mode = "rowblock"
     if mode is None:
-        mode = "xcs" if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
+        mode = ("xstage" if STAGED else "xcs") \
+            if prefers_xcs(cols, rowptr, n_cols, data.element_size()) else "rowblock"
+    if mode == "xstage" and nnz <= _INDEX_LIMIT_INT32 // 2 and int(rowptr.numel()) > 1:
+        rp = rowptr.to(torch.int64)
+        lengths = rp[1:] - rp[:-1]
+        try:
+            return XstageLayout(data, cols, rowptr, n_cols,
+                                lengths >= panel_row_min(n_cols, data.element_size()))
+        except ValueError:
+            mode = "xcs"  # x too wide for the staged-x combine: the XCS layouts
     if mode in ("xcs", "xcs-l2", "xcs-hybrid") and nnz <= _INDEX_LIMIT_INT32 // 2 and \
             int(n_cols) <= (1 << 27) and int(rowptr.numel()) > 1:
         if mode != "xcs-l2":
@@ -1085,6 +1329,7 @@ def build_layout(data, cols, rowptr, n_cols, one_shot=False):
     return RowBlockLayout(data, cols, rowptr)
 
 
-__all__ = ["RowBlockLayout", "XcsLayout", "PanelLayout", "XcsHybridLayout", "build_layout",
+__all__ = ["RowBlockLayout", "XcsLayout", "PanelLayout", "XcsHybridLayout", "XstageLayout",
+           "build_layout",
            "xcs_layout",
            "prefers_xcs", "sample_indices", "FORCE"]

@@ -721,12 +721,66 @@ static_assert(kPanelChunkRunsCap == kWave, "a chunk's runs are staged one per la
 
 constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
 
+// Rounds of 8-entry groups a thread of spmv_panel_kernel has in flight while staging.
+constexpr int kStageRounds = 4;
+
+// The staged-x pass of a job (see the file comment): xs[e] = sx[scol[e]] for e in [s0, s1)
+// (multiples of 8), 8 consecutive entries per thread per group, the next round's column
+// loads issued before this round's values are stored.
+template <typename T>
+__device__ __forceinline__ void stage_panel_entries(const T* sx, uint32_t cmask,
+                                                    const uint16_t* __restrict__ scol, int s0,
+                                                    int s1, T* __restrict__ xs) {
+  constexpr int kRound = 8 * kPanelBlock;
+  constexpr int U = kStageRounds;
+  int e = s0 + 8 * (int)threadIdx.x;
+  i32x4 c[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int ee = e + u * kRound;
+    c[u] = ee < s1 ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(scol + ee))
+                   : i32x4{0, 0, 0, 0};
+  }
+  for (; e < s1; e += U * kRound) {
+    T v[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t w[4] = {(uint32_t)c[u].x, (uint32_t)c[u].y, (uint32_t)c[u].z,
+                             (uint32_t)c[u].w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        v[u][q] = sx[((q & 1) ? (w[q >> 1] >> 16) : w[q >> 1]) & cmask];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int ee = e + (U + u) * kRound;
+      c[u] = ee < s1 ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(scol + ee))
+                     : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int ee = e + u * kRound;
+      if (ee < s1) {
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<f32x4*>(xs + ee) = f32x4{v[u][0], v[u][1], v[u][2], v[u][3]};
+          *reinterpret_cast<f32x4*>(xs + ee + 4) = f32x4{v[u][4], v[u][5], v[u][6], v[u][7]};
+        } else {
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            *reinterpret_cast<f64x2*>(xs + ee + 2 * h) = f64x2{v[u][2 * h], v[u][2 * h + 1]};
+        }
+      }
+    }
+  }
+}
+
 template <typename T, typename A>
 __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const T* __restrict__ vals, const uint16_t* __restrict__ pcol, int col_bits,
     const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
     const int* __restrict__ job_panel, const i32x2* __restrict__ chunk_info,
-    A* __restrict__ partials, int64_t n_partials) {
+    A* __restrict__ partials, int64_t n_partials, const uint16_t* __restrict__ scol,
+    const int* __restrict__ stage_jobs, T* __restrict__ xs) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
   // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule),
   // then one slot per lane for the stores of lanes where no run ends.
@@ -905,6 +959,8 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
       reduce_chunk(v[b], c[b], sl[b]);
     }
   }
+  // the staged-x entries of the job, from the same LDS panel
+  if (scol != nullptr) stage_panel_entries<T>(sx, cmask, scol, stage_jobs[job], stage_jobs[job + 1], xs);
 }
 
 template <typename T, typename A>
@@ -1016,19 +1072,224 @@ __global__ __launch_bounds__(NB) void hybrid_combine_kernel(
                            win_cap);
 }
 
+// Staged-x windows (see the file comment).  Entries of a row summed inline by the thread that
+// holds the row; rows of more than kStageMed entries take a wave each.
+constexpr int kStageInline = 4;
+constexpr int kStageMed = 16;
+constexpr uint16_t kStageSkip = 0xFFFFu;  // row_count: a row the window leaves alone
+
+// Window w of the staged-x layout, NB threads: the window's entries f < L are, in order, the
+// segments of panels 0, 1, ... (panel p's staged entries of the window's rows, in row order):
+// vals / dest at first + f (window-major), the staged x value at seg[w][p] + f - (the
+// segment's start in the window).  Products go to LDS position dest (the entry's rank in
+// (row, panel) order), then row r of the window gets the sum of its row_count[r] positions in
+// that order.
+template <typename T, typename A, int NB>
+__device__ __forceinline__ void stage_combine_window(
+    int w, const i32x4* __restrict__ windows, const int* __restrict__ seg, int n_panels,
+    const T* __restrict__ vals, const int16_t* __restrict__ dest, const T* __restrict__ xs,
+    unsigned n_xs, const uint16_t* __restrict__ row_count, T* __restrict__ y,
+    const int* __restrict__ row_map) {
+  constexpr int kWaves = NB / kWave;
+  constexpr int kCap = (int)kStageWinCap;
+  constexpr int kPer = kCap / NB;                   // entries per thread
+  constexpr int kRowsPer = (int)kStageWinRows / NB;  // rows per thread
+  constexpr int kPanelsPer = (int)kStagePanelsCap / NB;
+  constexpr int kLongCap = kCap / (kStageInline + 1);
+  constexpr int kHugeCap = kCap / (kStageMed + 1);
+  static_assert(kRowsPer * kWaves <= kWave, "one lane per wave total of the row counts");
+  static_assert(kCap * 2 + (int)kStagePanelsCap * 4 <= kCap * (int)sizeof(A),
+                "the panel map and the segment offsets fit the product slots");
+  static_assert(kStageMed < 32 && kCap <= 8192 && kStageWinRows <= 8192, "row list packing");
+  // The products; before them (the same LDS) the panel of every window entry and the offset
+  // from window entry to staged entry of every panel.
+  __shared__ A s_val[kCap];
+  uint16_t* const s_map = reinterpret_cast<uint16_t*>(s_val);
+  int* const s_delta = reinterpret_cast<int*>(s_map + kCap);
+  __shared__ int s_wt[kWaves];
+  __shared__ int s_wtot[kRowsPer][kWaves];
+  __shared__ int s_nlong, s_nhuge;
+  // rows of kStageInline + 1 .. kStageMed entries: (row << 18) | (first position << 5) | count
+  __shared__ int s_long[kLongCap];
+  // rows of more: (row << 13) | first position, and the count
+  __shared__ int s_huge[kHugeCap];
+  __shared__ uint16_t s_hcnt[kHugeCap];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  if (tid == 0) s_nlong = 0, s_nhuge = 0;  // read after the barriers below
+  const i32x4 win = windows[w];
+  const int row0 = win.x, nr = win.y, L = win.z, first = win.w;
+  if (nr > (int)kStageWinRows || L > kCap) return;  // not a layout window (uniform)
+  // the window's segments (thread t: panels kPanelsPer t ..): their lengths and starts
+  int gs[kPanelsPer], len[kPanelsPer], own = 0;
+#pragma unroll
+  for (int u = 0; u < kPanelsPer; ++u) {
+    const int p = kPanelsPer * tid + u;
+    gs[u] = p < n_panels ? seg[(int64_t)w * n_panels + p] : 0;
+    len[u] = p < n_panels ? seg[(int64_t)(w + 1) * n_panels + p] - gs[u] : 0;
+    own += len[u];
+  }
+  // values and positions: window-major, contiguous
+  T v[kPer];
+  int d[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int f = tid + k * NB;
+    const int ff = f < L ? f : 0;  // past the end: the first entry again, dropped below
+    v[k] = vals[first + ff];
+    d[k] = dest[first + ff];
+  }
+  int craw[kRowsPer];  // row counts, used after the products are in place
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    const int r = tid + m * NB;
+    craw[m] = r < nr ? (int)row_count[row0 + r] : 0;
+  }
+  // segment starts in the window (a block scan of the lengths in panel order), the map of
+  // window entries to panels, and every panel's offset
+  const int incl = wave_incl_scan(own);
+  if (lane == kWave - 1) s_wt[wid] = incl;
+  __syncthreads();
+  int ls = incl - own;
+  for (int j = 0; j < wid; ++j) ls += s_wt[j];
+#pragma unroll
+  for (int u = 0; u < kPanelsPer; ++u) {
+    const int p = kPanelsPer * tid + u;
+    if (p < n_panels) {
+      s_delta[p] = gs[u] - ls;
+      for (int j = 0; j < len[u]; ++j) s_map[ls + j] = (uint16_t)p;
+    }
+    ls += len[u];
+  }
+  __syncthreads();
+  T xv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int f = tid + k * NB;
+    // past the end: staged entry 0, dropped below; an index outside the staged entries (a
+    // table that breaks the layout's rules) is clamped into them
+    const unsigned g = f < L ? (unsigned)(s_delta[s_map[f]] + f) : 0u;
+    xv[k] = xs[g < n_xs ? g : n_xs - 1u];
+  }
+  __syncthreads();  // every map read done: the products overwrite it
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int f = tid + k * NB;
+    if (f < L && (unsigned)d[k] < (unsigned)kCap) s_val[d[k]] = A(v[k]) * A(xv[k]);
+  }
+  // first positions: an exclusive scan of the row counts in row order (thread t holds rows
+  // t, t + NB, ...; the wave totals scanned by wave 0)
+  int cnt[kRowsPer], rs[kRowsPer];
+  bool skip[kRowsPer];
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    skip[m] = craw[m] == (int)kStageSkip;
+    cnt[m] = skip[m] ? 0 : craw[m];
+    rs[m] = wave_incl_scan(cnt[m]);
+    if (lane == kWave - 1) s_wtot[m][wid] = rs[m];
+    rs[m] -= cnt[m];
+  }
+  __syncthreads();
+  if (wid == 0) {
+    const bool in = lane < kRowsPer * kWaves;
+    const int t = in ? s_wtot[lane / kWaves][lane % kWaves] : 0;
+    const int ex = wave_incl_scan(t) - t;
+    if (in) s_wtot[lane / kWaves][lane % kWaves] = ex;
+  }
+  __syncthreads();  // products and wave offsets in place
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) rs[m] += s_wtot[m][wid];
+  // rows of up to kStageInline entries here; longer ones listed
+#pragma unroll
+  for (int m = 0; m < kRowsPer; ++m) {
+    const int i = tid + m * NB;
+    if (i >= nr || skip[m]) continue;
+    if (cnt[m] > kStageMed) {
+      const int at = atomicAdd(&s_nhuge, 1);
+      if (at < kHugeCap) {  // always, in a layout window
+        s_huge[at] = (i << 13) | rs[m];
+        s_hcnt[at] = (uint16_t)cnt[m];
+      }
+    } else if (cnt[m] > kStageInline) {
+      const int at = atomicAdd(&s_nlong, 1);
+      if (at < kLongCap) s_long[at] = (i << 18) | (rs[m] << 5) | cnt[m];
+    } else {
+      A t[kStageInline];
+#pragma unroll
+      for (int u = 0; u < kStageInline; ++u) t[u] = cnt[m] > u ? s_val[rs[m] + u] : A(0);
+      A acc = A(0);
+#pragma unroll
+      for (int u = 0; u < kStageInline; ++u)
+        if (cnt[m] > u) acc += t[u];
+      const int row = row0 + i;
+      y[row_map ? row_map[row] : row] = T(acc);
+    }
+  }
+  __syncthreads();
+  const int n_long = s_nlong < kLongCap ? s_nlong : kLongCap;
+  for (int j = tid; j < n_long; j += NB) {
+    const unsigned e = (unsigned)s_long[j];
+    const int i = (int)(e >> 18), a = (int)((e >> 5) & 0x1fffu), b = a + (int)(e & 0x1fu);
+    A r = A(0);  // 0 + s[a] + s[a + 1] + ..., in order
+    for (int k = a; k < b; k += 4) {
+      A t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t[u] = k + u < b ? s_val[k + u] : A(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (k + u < b) r += t[u];
+    }
+    const int row = row0 + i;
+    y[row_map ? row_map[row] : row] = T(r);
+  }
+  const int n_huge = s_nhuge < kHugeCap ? s_nhuge : kHugeCap;
+  for (int j = wid; j < n_huge; j += kWaves) {  // a wave per row: strided lanes, fixed tree
+    const int e = s_huge[j];
+    const int i = e >> 13, a = e & 0x1fff, b = a + (int)s_hcnt[j];
+    A r = A(0);
+    for (int k = a + lane; k < b; k += kWave) r += s_val[k];
+    r = wave_sum(r);
+    if (lane == 0) {
+      const int row = row0 + i;
+      y[row_map ? row_map[row] : row] = T(r);
+    }
+  }
+}
+
+// The second pass of the staged-x layout: workgroups [0, n_pblocks) take the panel part's
+// long rows (as in hybrid_combine_kernel), the rest the windows.
+template <typename T, typename A, int NB>
+__global__ __launch_bounds__(NB) void stage_combine_kernel(
+    const i32x4* __restrict__ windows, const int* __restrict__ seg, int n_panels,
+    const T* __restrict__ vals, const int16_t* __restrict__ dest, const T* __restrict__ xs,
+    unsigned n_xs, const uint16_t* __restrict__ row_count, const int* __restrict__ rows,
+    const int* __restrict__ row_ptr, const int* __restrict__ slots,
+    const A* __restrict__ panel_partials, int n_rows, int n_pblocks, T* __restrict__ y,
+    const int* __restrict__ row_map) {
+  const int b = (int)blockIdx.x;
+  if (b < n_pblocks) {  // uniform
+    const int i = xcd_logical_block(b, n_pblocks) * (NB / kWave) + (int)(threadIdx.x / kWave);
+    if (i < n_rows)  // whole waves
+      combine_panel_row<T, A>(i, rows, row_ptr, slots, panel_partials, y, row_map);
+    return;
+  }
+  const int nw = (int)gridDim.x - n_pblocks;
+  stage_combine_window<T, A, NB>(xcd_logical_block(b - n_pblocks, nw), windows, seg, n_panels,
+                                 vals, dest, xs, n_xs, row_count, y, row_map);
+}
+
 template <typename T, typename A>
 int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const void* x,
                   int64_t x_len, void* y, const int32_t* row_map, const int32_t* jobs,
                   const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_info,
                   void* partials, int64_t n_partials, const int32_t* rows,
                   const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
-                  hipStream_t st) {
+                  const uint16_t* scol, const int32_t* stage_jobs, void* xs, hipStream_t st) {
   if (n_jobs > 0) {
     hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
                        ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
                        pcol, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
                        reinterpret_cast<const i32x2*>(chunk_info), static_cast<A*>(partials),
-                       n_partials);
+                       n_partials, scol, stage_jobs, static_cast<T*>(xs));
     int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
     if (rc) return rc;
   }
@@ -1058,6 +1319,26 @@ int launch_hybrid_combine(void* y, const int32_t* row_map, const void* xcs_parti
                      slots, static_cast<const A*>(panel_partials), (int)n_rows, (int)n_pblocks,
                      static_cast<T*>(y), row_map);
   return check_hip(hipGetLastError(), "hybrid_combine_kernel launch");
+}
+
+template <typename T, typename A>
+int launch_stage_combine(void* y, const int32_t* row_map, const int32_t* windows,
+                         int64_t n_windows, const int32_t* seg, int64_t n_panels,
+                         const void* vals, const int16_t* dest, const void* xs, int64_t n_xs,
+                         const uint16_t* row_count, const void* panel_partials,
+                         const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
+                         int64_t n_rows, hipStream_t st) {
+  constexpr int kRowsPerBlock = kCombBlock / kWave;
+  const int64_t n_pblocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int64_t grid = n_pblocks + n_windows;
+  if (grid == 0) return FSP_OK;
+  hipLaunchKernelGGL((stage_combine_kernel<T, A, kCombBlock>), dim3((unsigned)grid),
+                     dim3(kCombBlock), 0, st, reinterpret_cast<const i32x4*>(windows), seg,
+                     (int)n_panels, static_cast<const T*>(vals), dest,
+                     static_cast<const T*>(xs), (unsigned)n_xs, row_count, rows, row_ptr,
+                     slots, static_cast<const A*>(panel_partials), (int)n_rows,
+                     (int)n_pblocks, static_cast<T*>(y), row_map);
+  return check_hip(hipGetLastError(), "stage_combine_kernel launch");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1121,11 +1402,13 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
                                const int32_t* job_panel, int64_t n_jobs,
                                const int32_t* chunk_info, void* partials, int64_t n_partials,
                                const int32_t* rows, const int32_t* row_ptr,
-                               const int32_t* slots, int64_t n_rows, void* stream) {
+                               const int32_t* slots, int64_t n_rows, const uint16_t* scol,
+                               const int32_t* stage_jobs, void* xs, int64_t n_staged,
+                               void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
     return set_error(FSP_ENOTSUP, "fsp_spmv_panels: dtype");
   const int64_t vsize = dtype == FSP_F32 ? 4 : 8;
-  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0 || n_partials < 0)
+  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0 || n_partials < 0 || n_staged < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: negative size");
   if (n_partials * 8 > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: more partial slots than 2^31 bytes hold");
@@ -1133,32 +1416,78 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
       n_jobs > 0x7fffffffLL || n_rows > 0x7fffffffLL - kBlock)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: n_entries must be a multiple of " +
                                      std::to_string(kPanelChunk) + " and sizes within int32");
+  if (n_staged % 8 != 0 || n_staged > 0x7fffffffLL - 8 * kPanelBlock * kStageRounds)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: n_staged must be a multiple of 8 below 2^31");
   if (col_bits < 1 || col_bits > 15 || (vsize << col_bits) > kPanelBytes)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: col_bits must be <= 15 and a panel of "
                                  "2^col_bits values must fit " +
                                      std::to_string(kPanelBytes) + " bytes of LDS");
-  if (n_jobs > 0 && (!vals || !pcol || !x || !jobs || !job_panel || !chunk_info || !partials))
+  if (n_jobs > 0 && (!x || !jobs || !job_panel))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null pointer");
+  if (n_jobs > 0 && n_entries > 0 && (!vals || !pcol || !chunk_info || !partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: null entry pointer");
+  if (n_jobs > 0 && n_staged > 0 && (!scol || !stage_jobs || !xs))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: null staging pointer");
   if ((reinterpret_cast<uintptr_t>(chunk_info) & 7u) != 0)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: chunk_info must be 8-byte aligned");
   if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null row pointer");
-  if (!aligned16(vals) || !aligned16(pcol))
-    return set_error(FSP_EINVAL, "fsp_spmv_panels: vals and pcol must be 16-byte aligned");
+  if (!aligned16(vals) || !aligned16(pcol) || !aligned16(scol) || !aligned16(xs))
+    return set_error(FSP_EINVAL,
+                     "fsp_spmv_panels: vals, pcol, scol and xs must be 16-byte aligned");
   if (n_jobs == 0 && n_rows == 0) return FSP_OK;
+  if (n_staged == 0) scol = nullptr;  // the kernel stages nothing
   hipStream_t st = static_cast<hipStream_t>(stream);
+#define FSP_PANEL_ARGS vals, pcol, col_bits, x, x_len, y, row_map, jobs, job_panel, n_jobs, \
+                       chunk_info, partials, n_partials, rows, row_ptr, slots, n_rows, scol, \
+                       stage_jobs, xs, st
   if (dtype == FSP_F32) {
-    if (acc_f64)
-      return launch_panels<float, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                          job_panel, n_jobs, chunk_info, partials, n_partials, rows,
-                                          row_ptr, slots, n_rows, st);
-    return launch_panels<float, float>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_info, partials, n_partials, rows,
-                                       row_ptr, slots, n_rows, st);
+    if (acc_f64) return launch_panels<float, double>(FSP_PANEL_ARGS);
+    return launch_panels<float, float>(FSP_PANEL_ARGS);
   }
-  return launch_panels<double, double>(vals, pcol, col_bits, x, x_len, y, row_map, jobs,
-                                       job_panel, n_jobs, chunk_info, partials, n_partials, rows,
-                                       row_ptr, slots, n_rows, st);
+  return launch_panels<double, double>(FSP_PANEL_ARGS);
+#undef FSP_PANEL_ARGS
+}
+
+extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
+                                      int64_t n_out, const int32_t* windows, int64_t n_windows,
+                                      const int32_t* seg, int64_t n_panels, const void* vals,
+                                      const int16_t* dest, int64_t n_entries, const void* xs,
+                                      int64_t n_staged, const uint16_t* row_count,
+                                      const void* panel_partials, const int32_t* rows,
+                                      const int32_t* row_ptr, const int32_t* slots,
+                                      int64_t n_rows, void* stream) {
+  if (dtype != FSP_F32 && dtype != FSP_F64)
+    return set_error(FSP_ENOTSUP, "fsp_spmv_stage_combine: dtype");
+  if (n_windows < 0 || n_rows < 0 || n_panels < 0 || n_entries < 0 || n_staged < 0 || n_out < 0)
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: negative size");
+  if (n_windows > 0x3fffffffLL || n_rows > 0x3fffffffLL || n_entries > 0x7fffffffLL ||
+      n_staged > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: sizes beyond int32");
+  if (n_windows > 0 && (n_panels < 1 || n_panels > kStagePanelsCap))
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: n_panels outside [1, " +
+                                     std::to_string(kStagePanelsCap) + "]");
+  if (n_windows > 0 && (!y || !windows || !seg || !vals || !dest || !xs || !row_count ||
+                        n_staged < 1))
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null window-table pointer");
+  if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !panel_partials))
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null panel-row pointer");
+  if (!aligned16(windows))
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: windows must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (row_map && n_out > 0) {
+    int rc = (dtype == FSP_F32) ? fill_zero<float>(static_cast<float*>(y), n_out, st)
+                                : fill_zero<double>(static_cast<double*>(y), n_out, st);
+    if (rc) return rc;
+  }
+#define FSP_STAGE_ARGS y, row_map, windows, n_windows, seg, n_panels, vals, dest, xs, n_staged, \
+                       row_count, panel_partials, rows, row_ptr, slots, n_rows, st
+  if (dtype == FSP_F32) {
+    if (acc_f64) return launch_stage_combine<float, double>(FSP_STAGE_ARGS);
+    return launch_stage_combine<float, float>(FSP_STAGE_ARGS);
+  }
+  return launch_stage_combine<double, double>(FSP_STAGE_ARGS);
+#undef FSP_STAGE_ARGS
 }
 
 extern "C" int fsp_spmv_hybrid_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,

@@ -27,10 +27,15 @@
  *                          columns split into one panel per XCD (layout built by the prepare
  *                          step, flagsparse_amd/_spmv_layouts.py).
  *   fsp_spmv_panels      - the same launches, for the long rows of power-law matrices (x panels
- *                          copied to LDS); used together with fsp_spmv_xcs.
+ *                          copied to LDS), which also stage x for the short rows of the
+ *                          staged-x layout; used with fsp_spmv_xcs or fsp_spmv_stage_combine.
  *   fsp_spmv_hybrid_combine
- *                        - the second pass of the two above in one launch (same reference
- *                          launches: the row sums of spmv_csr.py:329-376 and :510-536).
+ *                        - the second pass of fsp_spmv_xcs and fsp_spmv_panels in one launch
+ *                          (same reference launches: the row sums of spmv_csr.py:329-376 and
+ *                          :510-536).
+ *   fsp_spmv_stage_combine
+ *                        - the second pass of the staged-x layout (its row sums) with that of
+ *                          fsp_spmv_panels, in one launch (the same reference launches).
  *   fsp_spmv_coo_atomic  - spmv_coo.py:269-280 (_spmv_coo_atomic_*, sort_by_row=False).
  *   fsp_spmm_csr         - spmm_csr.py:525-574 (_triton_spmm_csr_impl, base path) and
  *                          spmm_csr.py:922-1055 (bucketed opt path incl. the two-pass
@@ -85,6 +90,9 @@ int64_t fsp_xcs_sorted_col_bits(void);   /* max col_bits of sorted-gather XCS it
 int64_t fsp_panel_bytes_cap(void);       /* max bytes of one x panel (panel SpMV)     */
 int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)            */
 int64_t fsp_panel_chunk_runs_cap(void);  /* runs (rows) per chunk, at most (panel SpMV) */
+int64_t fsp_stage_window_cap(void);      /* max entries of one staged-x window          */
+int64_t fsp_stage_window_rows_cap(void); /* max rows of one staged-x window             */
+int64_t fsp_stage_panels_cap(void);      /* max x panels of the staged-x layout         */
 
 /*
  * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
@@ -290,7 +298,43 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pc
                     const int32_t* row_map, const int32_t* jobs, const int32_t* job_panel,
                     int64_t n_jobs, const int32_t* chunk_info, void* partials,
                     int64_t n_partials, const int32_t* rows, const int32_t* row_ptr,
-                    const int32_t* slots, int64_t n_rows, void* stream);
+                    const int32_t* slots, int64_t n_rows, const uint16_t* scol,
+                    const int32_t* stage_jobs, void* xs, int64_t n_staged, void* stream);
+
+/*
+ * The second pass of the staged-x layout (the short rows of power-law and uniform-random
+ * matrices whose x exceeds an L2): fsp_spmv_panels' jobs stage x for them, xs[e] = the x value
+ * at column (panel << col_bits) + scol[e] of their panel (scol, stage_jobs, xs, n_staged
+ * above: job j stages entries [stage_jobs[j], stage_jobs[j+1]) of its panel, multiples of 8,
+ * 16-byte aligned arrays; n_staged = 0 stages nothing), and this launch sums the rows, one
+ * workgroup per window, beside the panel part's long rows (rows .. n_rows, over
+ * panel_partials, as fsp_spmv_panels' second pass; n_rows may be 0).  Same reference launches
+ * as fsp_spmv_csr.
+ *   windows      n_windows int32 quadruples {row0, rows, entries L, first}: rows [row0, row0 +
+ *                rows) (<= fsp_stage_window_rows_cap()), L <= fsp_stage_window_cap() entries
+ *                vals[first .. first + L), dest[...] in window order: panel 0's staged entries
+ *                of the window's rows (in row order), then panel 1's, ...
+ *   seg          (n_windows + 1) x n_panels int32 (n_panels <= fsp_stage_panels_cap()):
+ *                panel p's staged entries of window w are xs[seg[w][p] .. seg[w+1][p]), the
+ *                lengths summing to L
+ *   dest         int16 per entry: its rank in the window's (row, panel) order; entry f adds
+ *                vals[first + f] * xs[...] (in the accumulation type) at that position
+ *   row_count    uint16 per row: the row's entries in its window (0xFFFF: a row the window
+ *                leaves alone - y written by the panel rows); row r gets the sum of its
+ *                positions in order (a fixed order for up to 16 entries, then lanes of a wave
+ *                in order and a fixed tree)
+ *   row_map      NULL: layout row r is y[r]; else y[row_map[r]], and y[0..n_out) is zeroed
+ *                first
+ * Calls sharing xs or panel_partials must not overlap.
+ */
+int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
+                           int64_t n_out, const int32_t* windows, int64_t n_windows,
+                           const int32_t* seg, int64_t n_panels, const void* vals,
+                           const int16_t* dest, int64_t n_entries, const void* xs,
+                           int64_t n_staged, const uint16_t* row_count,
+                           const void* panel_partials, const int32_t* rows,
+                           const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                           void* stream);
 
 /*
  * The second passes of fsp_spmv_xcs (the combine windows: windows .. row_count, over

@@ -245,10 +245,11 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert xcs(col_bits=19, item_format=1) == 0
     assert L.fsp_spmv_coo_atomic(0, None, None, None, -1, None, None, 0, 1, None) == -1
 
-    def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0, n_partials=0):
+    def panels(dtype=0, n_entries=0, col_bits=10, n_jobs=0, n_rows=0, n_partials=0,
+               n_staged=0):
         return L.fsp_spmv_panels(dtype, 0, None, None, n_entries, col_bits, None, 1, None, None,
                                  None, None, n_jobs, None, None, n_partials, None, None, None,
-                                 n_rows, None)
+                                 n_rows, None, None, None, n_staged, None)
 
     assert panels() == 0                          # nothing to run
     assert panels(dtype=5) == -3
@@ -266,8 +267,37 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     # launch (the other pointers are never dereferenced on the host)
     fake = 1 << 20
     assert L.fsp_spmv_panels(0, 0, fake, fake, 512, 10, fake, 1024, None, None, fake, fake, 1,
-                             fake + 4, fake, 64, None, None, None, 0, None) == -1
+                             fake + 4, fake, 64, None, None, None, 0, None, None, None, 0,
+                             None) == -1
     assert b"chunk_info" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
+    # staging (the staged-x layout's first pass): whole groups of 8, arrays given
+    assert panels(n_staged=12) == -1
+    assert b"multiple of 8" in L.fsp_last_error()
+    assert L.fsp_spmv_panels(0, 0, None, None, 0, 10, fake, 1024, None, None, fake, fake, 1,
+                             None, None, 0, None, None, None, 0, None, None, None, 64,
+                             None) == -1
+    assert b"staging" in L.fsp_last_error()
+    assert L.fsp_spmv_panels(0, 0, None, None, 0, 10, fake, 1024, None, None, fake, fake, 1,
+                             None, None, 0, None, None, None, 0, fake + 8, fake, fake, 64,
+                             None) == -1
+    assert b"aligned" in L.fsp_last_error()
+
+    def stage(dtype=0, n_windows=0, n_panels=1, n_rows=0, n_staged=8, tables=False):
+        t = fake if tables else None
+        return L.fsp_spmv_stage_combine(dtype, 1, t, None, 0, t, n_windows, t, n_panels, t, t,
+                                        64, t, n_staged, t, None, None, None, None, n_rows,
+                                        None)
+
+    assert stage() == 0                           # nothing to run
+    assert stage(dtype=7) == -3
+    assert stage(n_windows=2) == -1               # windows without their tables
+    assert b"null" in L.fsp_last_error()
+    assert stage(n_windows=2, n_panels=L.fsp_stage_panels_cap() + 1, tables=True) == -1
+    assert b"n_panels" in L.fsp_last_error()
+    assert stage(n_windows=2, n_staged=0, tables=True) == -1  # nothing staged to read
+    assert stage(n_rows=4) == -1                  # panel rows without their arrays
+    assert b"panel-row" in L.fsp_last_error()
+    assert L.fsp_stage_window_cap() == 4096 and L.fsp_stage_window_rows_cap() == 2048
 
 
 def test_build_flags_kernels_with_scratch():

@@ -4,8 +4,9 @@ size-independent properties that hold exactly:
 
   cfg2  Poisson 2048^2 fp64: A * 1 = 4 - (number of neighbours) for every row, exactly;
         random x against the oracle (both paths); linearity A(2x - z) = 2Ax - Az
-  cfg3  8M power-law fp32, int64 indices (XCS + panel hybrid): oracle bars incl. <= 1 ulp from
-        float32(fp64 oracle) on the default path; two calls bit-identical
+  cfg3  8M power-law fp32, int64 indices (the default staged-x layout, and the XCS + panel
+        hybrid): oracle bars incl. <= 1 ulp from float32(fp64 oracle) on the default path; two
+        calls bit-identical
   cfg4  COO 2M, 41.9M entries: oracle bars; A * 0 = 0
   cfg5  SpMM N=64 fp32 (opt), N=16 fp32 (base and opt) and N=16 fp64 (base): oracle bars;
         column j of A B = A B[:, j] (the SpMV of the same matrix), within 1 ulp where both
@@ -23,7 +24,7 @@ import pytest
 import torch
 
 import flagsparse_amd as fs
-from flagsparse_amd import synthetic
+from flagsparse_amd import _spmv_layouts, synthetic
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -64,12 +65,14 @@ def test_cfg2_full(dev):
     assert oracle.rel_l2(lhs, rhs) <= 1e-12
 
 
-def test_cfg3_full(dev):
-    print("full size cfg3", flush=True)
+@pytest.mark.parametrize("mode", [None, "xcs"])
+def test_cfg3_full(dev, monkeypatch, mode):
+    print(f"full size cfg3 {mode or 'default'}", flush=True)
+    monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(device=dev)
     assert idx.dtype == torch.int64 and data.numel() == 100663296
     p = fs.prepare_spmv_csr(data, idx, ptr, shape)
-    assert p._kernel(False).kind == "xcs-hybrid"
+    assert p._kernel(False).kind == ("xstage" if mode is None else "xcs-hybrid")
     ref = oracle.spmv_csr(ptr.cpu(), idx.cpu(), data.cpu(), x.cpu())
     y = fs.flagsparse_spmv_csr(x=x, prepared=p)
     _bars(y, ref, torch.float32)

@@ -84,7 +84,7 @@ def _force(monkeypatch, layout):
     return mode
 
 
-LAYOUTS = ["rowblock", "xcs-l2", "xcs-l2-sorted", "xcs-hybrid", "xcs-hybrid-sorted"]
+LAYOUTS = ["rowblock", "xcs-l2", "xcs-l2-sorted", "xcs-hybrid", "xcs-hybrid-sorted", "xstage"]
 
 
 @pytest.mark.parametrize("seed", range(len(CASES)))
@@ -104,7 +104,7 @@ def test_fuzz_spmv(dev, monkeypatch, seed, layout):
     print(f"  layout built: {built} item format {getattr(xcs, 'item_format', '-')}", flush=True)
     # the forced layout is the one tested (the hybrid needs a row of FORCE_PANEL_ROW_MIN entries)
     has_long = bool(((ptr[1:] - ptr[:-1]) >= _spmv_layouts.FORCE_PANEL_ROW_MIN).any())
-    expect = {"rowblock": "rowblock", "xcs-l2": "xcs",
+    expect = {"rowblock": "rowblock", "xcs-l2": "xcs", "xstage": "xstage",
               "xcs-hybrid": "xcs-hybrid" if has_long else "xcs"}[layout]
     assert built == expect
     for use_opt in (False, True):

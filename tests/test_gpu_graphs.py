@@ -60,7 +60,9 @@ def _replay_and_check(dev, g, src, out, inputs, eager, ref_fn, dtype):
                                           ("rowblock", torch.float64),
                                           ("xcs-l2", torch.float32),
                                           ("xcs-hybrid", torch.float32),
-                                          ("xcs-hybrid", torch.float64)])
+                                          ("xcs-hybrid", torch.float64),
+                                          ("xstage", torch.float32),
+                                          ("xstage", torch.float64)])
 @pytest.mark.parametrize("use_opt", [False, True])
 def test_spmv_csr_graph_replay(dev, monkeypatch, layout, dtype, use_opt):
     monkeypatch.setattr(_spmv_layouts, "FORCE", layout)

@@ -1,7 +1,8 @@
-"""SpMV through the XCD column-split layout on the GPU (spmv_xcs_kernel), forced for every
-matrix here - alone, and as the hybrid with the long rows in the panel layout - against the fp64
-CPU oracle; the automatic choice is checked to pick it for random-column matrices (the hybrid
-for a power law) and to keep row blocks for banded ones.
+"""SpMV through the layouts for columns spread over a large x on the GPU, forced for every matrix
+here: the XCD column-split layout (spmv_xcs_kernel) alone and as the hybrid with the long rows
+in the panel layout, and the staged-x layout (spmv_panel_kernel staging x for the short rows,
+stage_combine_kernel) - against the fp64 CPU oracle; the automatic choice is checked to pick
+the staged-x layout for random-column matrices and to keep row blocks for banded ones.
 
 Bars as for the row-block kernel: relative L2 error <= 1e-5 / 1e-12, the reference scripts'
 allclose ratio, and for the default float32 path at most 1 ulp from float32(fp64 oracle).
@@ -18,8 +19,9 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[("xcs-l2", 0), ("xcs-l2", 1), ("xcs-hybrid", 0), ("xcs-hybrid", 1)],
-                ids=["xcs-rows", "xcs-sorted", "hybrid-rows", "hybrid-sorted"])
+@pytest.fixture(params=[("xcs-l2", 0), ("xcs-l2", 1), ("xcs-hybrid", 0), ("xcs-hybrid", 1),
+                        ("xstage", 0)],
+                ids=["xcs-rows", "xcs-sorted", "hybrid-rows", "hybrid-sorted", "xstage"])
 def force_xcs(request, monkeypatch):
     # the hybrid with rows of >= 32 entries in the panel part, so that these small matrices
     # have long rows in every case that checks the layout kind; the XCS items in row order
@@ -28,13 +30,13 @@ def force_xcs(request, monkeypatch):
     monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
     monkeypatch.setattr(_spmv_layouts, "SORTED_ITEMS", fmt == 1)
     monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 0.0)
-    if mode == "xcs-hybrid":
+    if mode in ("xcs-hybrid", "xstage"):
         monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
     return mode
 
 
 def _kind(mode):
-    return "xcs" if mode == "xcs-l2" else "xcs-hybrid"
+    return {"xcs-l2": "xcs"}.get(mode, mode)
 
 
 def _ulp(a, b):
@@ -102,13 +104,14 @@ HYBRID_EDGES = [
 
 @pytest.mark.parametrize("lengths,n_cols", HYBRID_EDGES)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype):
-    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+@pytest.mark.parametrize("mode", ["xcs-hybrid", "xstage"])
+def test_hybrid_edges(dev, monkeypatch, lengths, n_cols, dtype, mode):
+    monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
     data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 21, dtype)
-    print(f"hybrid edges rows={len(lengths)} n_cols={n_cols} {dtype}", flush=True)
+    print(f"hybrid edges {mode} rows={len(lengths)} n_cols={n_cols} {dtype}", flush=True)
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
-    assert p._kernel(False).kind == "xcs-hybrid"
+    assert p._kernel(False).kind == mode
     ref = oracle.spmv_csr(ptr, idx, data, x)
     for use_opt in (False, True):
         y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p, use_opt=use_opt)
@@ -149,6 +152,40 @@ def test_hybrid_marks_every_panel_array(dev, monkeypatch):
     assert got, "the panel part's stream order was not consulted"
     for t in wanted:
         assert any(any(u is t for u in ts) for ts in got), "a panel array was not marked"
+    _check(y, oracle.spmv_csr(ptr, idx, data, x), exact_fp32=True)
+
+
+def test_xstage_marks_every_array(dev, monkeypatch):
+    # As above for the staged-x layout: one stream order for both launches, and every array
+    # they read or write (the staged part's and the panel part's) marked on the caller's stream.
+    monkeypatch.setattr(_spmv_layouts, "FORCE", "xstage")
+    monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    lengths, n_cols = HYBRID_EDGES[3]
+    data, idx, ptr, x, shape = _csr_from_lengths(lengths, n_cols, 23, torch.float32)
+    p = fs.prepare_spmv_csr(data.to(dev), idx.to(torch.int32).to(dev), ptr.to(dev), shape)
+    layout = p._kernel(False)
+    assert layout.kind == "xstage" and layout.long is not None
+    seen = []
+    real = _spmv_layouts.StreamOrder.stream
+
+    def spy(self, device, tensors=()):
+        seen.append((self, tuple(tensors)))
+        return real(self, device, tensors)
+
+    monkeypatch.setattr(_spmv_layouts.StreamOrder, "stream", spy)
+    side = torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p)
+    torch.cuda.synchronize()
+    lg = layout.long
+    wanted = (layout.scol, layout.xs, layout.seg, layout.vals, layout.dest, layout.row_count,
+              layout.windows, layout.jobs, layout.job_panel, layout.stage_jobs, lg.partials,
+              lg.vals, lg.pcol, lg.chunk_info, lg.rows, lg.row_ptr, lg.slots)
+    got = [ts for order, ts in seen if order is layout._order]
+    assert got, "the layout's stream order was not consulted"
+    for t in wanted:
+        assert any(any(u is t for u in ts) for ts in got), "an array was not marked"
     _check(y, oracle.spmv_csr(ptr, idx, data, x), exact_fp32=True)
 
 
@@ -204,7 +241,7 @@ def test_rows_over_the_count_byte(dev, monkeypatch, count_max):
 def test_automatic_choice(dev):
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=5000)  # x: 8 MiB
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
-    assert p._kernel(False).kind in ("xcs", "xcs-hybrid")
+    assert p._kernel(False).kind == "xstage"
     ref = oracle.spmv_csr(ptr, idx, data, x)
     _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), ref, exact_fp32=True)
     # a call without a prepared object takes the row-block layout (fastest to build)
@@ -214,14 +251,14 @@ def test_automatic_choice(dev):
     _check(fs.flagsparse_spmv_coo(data.to(dev), rows.to(dev), idx.to(dev), x.to(dev), shape),
            oracle.spmv_coo(rows, idx, data, x, shape[0]))
     po = fs.prepare_spmv_coo(data.to(dev), rows.to(dev), idx.to(dev), shape)
-    assert po._run_layout().kind in ("xcs", "xcs-hybrid")
+    assert po._run_layout().kind == "xstage"
     d, i, pp, xx, sh = synthetic.csr_poisson2d(1024)
     p = fs.prepare_spmv_csr(d.to(dev), i.to(dev), pp.to(dev), sh)
     assert p._kernel(False).kind == "rowblock"
-    # a heavier tail (cap 200000 as cfg3): most entries in long rows -> the hybrid
+    # a heavier tail (cap 200000 as cfg3): the long rows in the staged-x layout's panel part
     data, idx, ptr, x, shape = synthetic.csr_powerlaw(1 << 21, cap=200000)
     p = fs.prepare_spmv_csr(data.to(dev), idx.to(dev), ptr.to(dev), shape)
-    assert p._kernel(False).kind == "xcs-hybrid"
+    assert p._kernel(False).kind == "xstage" and p._kernel(False).long is not None
     _check(fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p), oracle.spmv_csr(ptr, idx, data, x),
            exact_fp32=True)
 
@@ -252,7 +289,7 @@ def test_combine_unaligned_windows(dev, monkeypatch, dtype):
         _check(y, ref, exact_fp32=(dtype == torch.float32 and not use_opt))
 
 
-@pytest.mark.parametrize("layout", ["rowblock", "xcs-l2", "xcs-hybrid"])
+@pytest.mark.parametrize("layout", ["rowblock", "xcs-l2", "xcs-hybrid", "xstage"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 def test_unaligned_x_and_out(dev, monkeypatch, layout, dtype):
     # x and out as views one element into their buffers (not 16-byte aligned): the panel
@@ -284,12 +321,15 @@ def test_unaligned_x_and_out(dev, monkeypatch, layout, dtype):
 
 @pytest.mark.parametrize("bad", [float("inf"), float("nan")])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype):
+@pytest.mark.parametrize("mode", ["xcs-hybrid", "xstage"])
+def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype, mode):
     # x infinite or NaN in every panel's first column: the panel layout's padding entries point
     # there with value 0 and must add exactly 0 (0 * inf would be NaN).  Without entries in
     # those columns every row is finite; with them, the rows holding one are inf / NaN exactly
-    # as in the oracle (inf or NaN of a row does not depend on the summation order).
-    monkeypatch.setattr(_spmv_layouts, "FORCE", "xcs-hybrid")
+    # as in the oracle (inf or NaN of a row does not depend on the summation order).  In the
+    # staged-x layout the staged part's padding (up to 7 entries per panel) stages that x too,
+    # and must never be read.
+    monkeypatch.setattr(_spmv_layouts, "FORCE", mode)
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
     rng = np.random.default_rng(17)
     lengths = np.concatenate([rng.integers(0, 30, 4000), rng.integers(32, 3000, 400)])
@@ -310,7 +350,7 @@ def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype):
             d, i, p = data, idx, ptr
         prep = fs.prepare_spmv_csr(d.to(dev), i.to(torch.int32).to(dev), p.to(dev), shape)
         lay = prep._kernel(False)
-        assert lay.kind == "xcs-hybrid"
+        assert lay.kind == mode
         assert int(lay.long.chunk_info[:, 1].min()) < 512  # padding present
         ref = oracle.spmv_csr(p, i, d, x)
         for use_opt in (False, True):
@@ -330,7 +370,7 @@ def test_panel_padding_with_nonfinite_x(dev, monkeypatch, bad, dtype):
     (5, 3, [0, 3, 0, 0, 3]),
     (2, 100000, [0, 0]),            # wide, empty
 ])
-@pytest.mark.parametrize("layout", ["xcs-l2", "xcs-hybrid"])
+@pytest.mark.parametrize("layout", ["xcs-l2", "xcs-hybrid", "xstage"])
 def test_degenerate_shapes(dev, monkeypatch, n_rows, n_cols, lengths, layout):
     monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
     monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 2)

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _lib = None
 
@@ -44,7 +44,7 @@ SIGNATURES = {
     "fsp_panel_chunk_runs_cap": (_i64, []),
     "fsp_stage_window_cap": (_i64, []),
     "fsp_stage_window_rows_cap": (_i64, []),
-    "fsp_stage_panels_cap": (_i64, []),
+    "fsp_stage_chunk": (_i64, []),
     "fsp_plan_panel_chunks": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p]),
     "fsp_plan_panel_chunks_device": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _p]),
     "fsp_plan_row_blocks": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
@@ -56,9 +56,10 @@ SIGNATURES = {
     "fsp_spmv_xcs": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64, _p, _p,
                             _p, _i64, _i64, _p, _p, _i32, _p]),
     "fsp_spmv_panels": (_i32, [_i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _i64,
-                               _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _p, _i64, _p]),
-    "fsp_spmv_stage_combine": (_i32, [_i32, _i32, _p, _p, _i64, _p, _i64, _p, _i64, _p, _p,
-                                      _i64, _p, _i64, _p, _p, _p, _p, _p, _i64, _p]),
+                               _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64,
+                               _p]),
+    "fsp_spmv_stage_combine": (_i32, [_i32, _i32, _p, _p, _i64, _p, _i64, _i64, _p, _p, _p,
+                                      _i64, _p, _p, _p, _p, _p, _i64, _p]),
     "fsp_spmv_hybrid_combine": (_i32, [_i32, _i32, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
                                        _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),
@@ -163,5 +164,5 @@ def caps():
         "panel_chunk_runs": int(L.fsp_panel_chunk_runs_cap()),
         "stage_window": int(L.fsp_stage_window_cap()),
         "stage_window_rows": int(L.fsp_stage_window_rows_cap()),
-        "stage_panels": int(L.fsp_stage_panels_cap()),
+        "stage_chunk": int(L.fsp_stage_chunk()),
     }

@@ -67,6 +67,16 @@ FORCE = None
 # (False: the XCS layouts).  Measured on MI355X, cfg3's short rows (26.4M entries, both passes):
 # 123 us staged against 161 us as XCS items and their combine.
 STAGED = True
+# Jobs the staged entries of a matrix are cut into, about (one per CU of the MI355X: a job
+# copies its x panel into LDS once, so more jobs copy more), of at least STAGE_JOB_MIN entries
+# (whose columns and staged values are about as many bytes as the panel copy).
+STAGE_JOBS = 256
+STAGE_JOB_MIN = 16384
+# Segments of a window in the order of the XCDs whose jobs stage them (test hook: False = panel
+# order): measured on MI355X, cfg3's panel kernel 128.4 against 135.6 us in panel order.
+STAGE_XCD_ORDER = True
+STAGE_SEGMENT_MIN = 32
+FORCE_STAGE_WINDOW = None  # test hook: the staged-x window size
 # Row-block SpMV launches in hardware order (workgroup i on XCD i % 8): on MI355X this streamed
 # faster than one contiguous descriptor range per XCD (cfg2 60.5 vs 64.7 us, cfg1 9.7 vs 12.0
 # us; banded and power-law matrices within 1%).
@@ -933,7 +943,7 @@ class PanelLayout:
                     self.n_entries, self.col_bits, None, self.n_cols, None, None, p(self.jobs),
                     p(self.job_panel), self.n_jobs, p(self.chunk_info), p(self.partials),
                     int(self.partials.numel()), p(self.rows), p(self.row_ptr), p(self.slots),
-                    self.n_rows, None, None, None, 0, None]
+                    self.n_rows, None, 0, None, None, None, None, 0, None]
             self._args[bool(acc_f64)] = args
         a = list(args)
         a[6], a[8] = x.data_ptr(), y.data_ptr()
@@ -942,7 +952,7 @@ class PanelLayout:
             a[12] = 0
         if not passes & 2:
             a[19] = 0
-        a[24] = stream if stream is not None else self._order.stream(y.device, self._keep)
+        a[27] = stream if stream is not None else self._order.stream(y.device, self._keep)
         _abi.check(_abi.lib().fsp_spmv_panels(*a), "fsp_spmv_panels")
         return y
 
@@ -1041,13 +1051,23 @@ class XstageLayout:
         self.n_rows, self.n_cols, self.nnz = n_rows, int(n_cols), int(data.numel())
         cb = _panel_col_bits(n_cols, data.element_size())
         P = max(1, -(-self.n_cols >> cb))
-        if P > caps["stage_panels"]:
-            raise ValueError("x needs more panels than the staged-x combine takes")
         self.col_bits, self.n_panels = cb, P
+        chunk = caps["stage_chunk"]
+        # Windows of the larger size where the smaller would leave each panel's segment of a
+        # window under STAGE_SEGMENT_MIN entries: the panel jobs write the segments of a window
+        # from many CUs, and short segments share more lines (measured on MI355X, cfg3 - 256
+        # panels -: 8192 against 4096 entries 205 against 214 us a call; cfg4 - 64 panels -:
+        # 142 against 137 us).
         win_cap, win_rows = caps["stage_window"], caps["stage_window_rows"]
+        if FORCE_STAGE_WINDOW:
+            win_cap = int(FORCE_STAGE_WINDOW)
+        elif (win_cap // 2) // P >= STAGE_SEGMENT_MIN:
+            win_cap //= 2
+        win_rows = win_rows * win_cap // caps["stage_window"]
+        self.window_cap = win_cap
         # A window holds every entry of its rows: rows longer than a quarter window go to the
         # panel part whatever their length per panel, so that windows stay nearly full.
-        long_mask = long_mask | (lengths > win_cap // 4)
+        long_mask = long_mask | (lengths > caps["stage_window"] // 8)
         short_len = torch.where(long_mask, 0, lengths)
         entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths,
                                             output_size=self.nnz)
@@ -1076,8 +1096,11 @@ class XstageLayout:
             raise AssertionError("staged-x windows: a window past its caps")
         self.n_windows = W
 
-        # 2. Short entries (CSR order) and their panels; staged order (panel, window, row),
-        #    each panel's run padded to a multiple of 8.
+        # 2. Short entries (CSR order) and their panels.  Staged order (panel, window, row); a
+        #    segment is one (panel, window) pair's entries, its first marked in the 16-bit
+        #    column.  Each panel's segments fill chunks of `chunk` entries, a chunk closing
+        #    early rather than hold more than 64 segments (the kernel's offsets per chunk, the
+        #    panel layout's chunk planner with segments for runs); the rest is padding.
         pick = torch.nonzero(~entry_long).flatten()
         er = entry_row[pick]
         del entry_row, entry_long
@@ -1086,47 +1109,114 @@ class XstageLayout:
         self.n_entries = n_short
         pan = ec >> cb
         ew = win_of_row[er]
-        key = pan * max(W, 1) + ew
+        Wk = max(W, 1)
+        key = pan * Wk + ew
         ks, perm = torch.sort(key, stable=True)  # stable: row order inside a segment
-        cnt_pw = torch.bincount(key, minlength=P * W) if n_short else \
-            torch.zeros(P * W, dtype=torch.int64, device=dev)
         del key
-        cnt_p = cnt_pw.view(P, W).sum(1)
-        padded_p = (cnt_p + 7) // 8 * 8
-        pstart = torch.cumsum(padded_p, 0) - padded_p
-        n_staged = int(padded_p.sum().item())
-        if n_staged > _INDEX_LIMIT_INT32 - (1 << 16):
+        ar = torch.arange(n_short, device=dev)
+        seg_start = torch.ones(n_short, dtype=torch.bool, device=dev)
+        if n_short > 1:
+            seg_start[1:] = ks[1:] != ks[:-1]
+        seg_id = torch.cumsum(seg_start, 0) - 1  # segments numbered in staged order
+        first_e = torch.nonzero(seg_start).flatten()  # each segment's first sorted entry
+        n_seg = int(first_e.numel())
+        self.n_segments = n_seg
+        seg_len = torch.diff(first_e, append=torch.tensor([n_short], device=dev))
+        seg_panel = ks[first_e] // Wk
+        panel_segs = torch.zeros(P + 1, dtype=torch.int64, device=dev)
+        torch.cumsum(torch.bincount(seg_panel, minlength=P), 0, out=panel_segs[1:])
+        seg_pos, panel_end = plan_panel_chunks(panel_segs, seg_len, chunk, 64)
+        seg_pos = seg_pos.to(device=dev, dtype=torch.int64)
+        panel_end = panel_end.to(device=dev, dtype=torch.int64)
+        n_staged = int(panel_end[-1].item()) if P else 0
+        if n_staged > (1 << 30) or n_short > _INDEX_LIMIT_INT32 - 64:
             raise ValueError("too many entries for the staged-x layout")
         self.n_staged = n_staged
-        pfirst = torch.cumsum(cnt_p, 0) - cnt_p  # each panel's first sorted entry
-        kstart = torch.cumsum(cnt_pw, 0) - cnt_pw  # each (panel, window) segment's
-        sp = ks // max(W, 1)
-        spos = pstart[sp] + torch.arange(n_short, device=dev) - pfirst[sp]
-        sc = torch.zeros(n_staged + 8, dtype=torch.int32, device=dev)
-        sc[spos] = (ec[perm] & ((1 << cb) - 1)).to(torch.int32)
+        panel_len = torch.diff(panel_end, prepend=panel_end.new_zeros(1))
+        pstart = panel_end - panel_len
+        spos = seg_pos[seg_id] + ar - first_e[seg_id]  # staged position of every sorted entry
+        sc = torch.zeros(n_staged + chunk, dtype=torch.int32, device=dev)
+        sc[spos] = (ec[perm] & ((1 << cb) - 1)).to(torch.int32) | \
+            (seg_start.to(torch.int32) << 15)
         self.scol = torch.where(sc >= (1 << 15), sc - (1 << 16), sc).to(torch.int16)
-        del sc, spos
-        self.xs = torch.zeros(n_staged + 8, dtype=data.dtype, device=dev)
-        # segments: seg[w][p] = the staged position of panel p's entries of window w
-        seg = torch.empty((W + 1, P), dtype=torch.int64, device=dev)
-        seg[:W] = (pstart.view(P, 1) + kstart.view(P, W) - pfirst.view(P, 1)).t()
-        seg[W] = pstart + cnt_p
-        self.seg = seg.to(torch.int32).contiguous()
-        del seg
+        del sc
+        # per chunk: the segment of its first entry (always a real one) and its entries in use
+        n_chunks = n_staged // chunk
+        self.stage_info = torch.zeros((max(n_chunks, 1), 2), dtype=torch.int32, device=dev)
+        if n_chunks:
+            real = torch.zeros(n_staged, dtype=torch.bool, device=dev)
+            real[spos] = True
+            seg_at = torch.zeros(n_staged, dtype=torch.int64, device=dev)
+            seg_at[spos] = seg_id
+            rv = real.view(n_chunks, chunk)
+            if not bool(rv[:, 0].all()) or bool((rv[:, 1:] & ~rv[:, :-1]).any()):
+                raise AssertionError("staged-x chunks: padding before an entry")
+            self.stage_info[:, 0] = seg_at[::chunk].to(torch.int32)
+            self.stage_info[:, 1] = rv.sum(1).to(torch.int32)
+            del real, seg_at, rv
 
-        # 3. Window order (window, panel, row) for the values and LDS positions; the position
-        #    of an entry is its rank in the window's (row, panel) order.
-        seglen = cnt_pw.view(P, W).t()
-        lsw = torch.cumsum(seglen, 1) - seglen  # each segment's start in its window
-        sw = ks % max(W, 1)
-        wpos = win_first[sw] + lsw[sw, sp] + torch.arange(n_short, device=dev) - kstart[ks]
-        del seglen, lsw, sw, sp, ks
+        # 3. The jobs of the first launch: panel p's chunks of long rows (if any) and its
+        #    staged chunks are split evenly over n_p >= 1 jobs, n_p the most of what its long
+        #    chunks need (PANEL_JOB_CHUNKS each) and its share of about STAGE_JOBS jobs for all
+        #    the staged chunks (rounded: panels of about the average share keep one job), so
+        #    that a matrix without long rows still fills the GPU.
+        long_rows = torch.nonzero(long_mask).flatten()
+        self.long = None
+        chunk0 = torch.zeros(P + 1, dtype=torch.int64, device=dev)
+        if long_rows.numel():
+            lpick = torch.nonzero(long_mask[torch.repeat_interleave(
+                torch.arange(n_rows, device=dev), lengths, output_size=self.nnz)]).flatten()
+            long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
+            torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
+            self.long = PanelLayout(data[lpick], cols[lpick], long_ptr, n_cols, long_rows)
+            del lpick
+            lg = self.long
+            if lg.col_bits != cb or lg.n_panels != P:
+                raise AssertionError("staged-x layout: the panel parts disagree on the panels")
+            chunk0[:P] = lg.panel_chunk0.to(torch.int64)
+            chunk0[P] = int(lg.jobs[-1].item())
+        per_panel = chunk0[1:] - chunk0[:-1]
+        sch = panel_len // chunk  # staged chunks per panel
+        per_job = max(-(-STAGE_JOB_MIN // chunk), -(-n_chunks // STAGE_JOBS))
+        nj = torch.maximum((per_panel + PANEL_JOB_CHUNKS - 1) // PANEL_JOB_CHUNKS,
+                           (2 * sch + per_job) // (2 * per_job)).clamp(min=1)
+        job_panel = torch.repeat_interleave(torch.arange(P, device=dev), nj)
+        n_jobs = int(job_panel.numel())
+        k = torch.arange(n_jobs, device=dev) - (torch.cumsum(nj, 0) - nj)[job_panel]
+        starts = chunk0[job_panel] + k * per_panel[job_panel] // nj[job_panel]
+        self.jobs = torch.cat([starts, chunk0[P:]]).to(torch.int32).contiguous()
+        self.job_panel = job_panel.to(torch.int32).contiguous()
+        self.n_jobs = n_jobs
+        s_lo = pstart[job_panel] // chunk + k * sch[job_panel] // nj[job_panel]
+        self.stage_jobs = torch.cat([s_lo, torch.tensor([n_chunks], device=dev)]).to(
+            torch.int32).contiguous()
+        del k, starts
+
+        # 4. Window order: in each window its segments by (XCD of the job that stages it -
+        #    workgroup j runs on XCD j mod 8 -, panel), so that the XCD's jobs write the lines
+        #    of their segments together; every entry's values, LDS position (its rank in the
+        #    window's (row, panel) order) and staged x there; seg_delta takes a segment's staged
+        #    positions to its window positions.
+        seg_chunk = seg_pos // chunk
+        seg_job = torch.searchsorted(s_lo, seg_chunk, right=True) - 1
+        seg_key = (ks[first_e] % Wk) * (XCD_COUNT * P) + \
+            (seg_job % XCD_COUNT) * P * int(STAGE_XCD_ORDER) + ks[first_e] // Wk
+        seg_order = torch.sort(seg_key)[1]
+        ordered_len = seg_len[seg_order]
+        seg_wpos = torch.empty_like(seg_len)
+        seg_wpos[seg_order] = torch.cumsum(ordered_len, 0) - ordered_len  # window-major start
+        del seg_key, seg_order, ordered_len, seg_chunk, seg_job, s_lo
+        sdelta = torch.zeros(n_seg + 64, dtype=torch.int64, device=dev)
+        sdelta[:n_seg] = seg_wpos - seg_pos
+        self.seg_delta = sdelta.to(torch.int32).contiguous()
+        wpos = seg_wpos[seg_id] + ar - first_e[seg_id]
+        del seg_len, seg_wpos, first_e, seg_start, seg_id, spos, seg_pos
         rank_key = er * P + pan  # CSR order is row order: a stable sort by (row, panel)
         order2 = torch.sort(rank_key, stable=True)[1]
         del rank_key
         rank = torch.empty_like(order2)
-        rank[order2] = torch.arange(n_short, device=dev)
-        del order2
+        rank[order2] = ar
+        del order2, ar
         slot = rank - win_first[ew]
         del rank
         self.vals = torch.zeros(n_short + 8, dtype=data.dtype, device=dev)
@@ -1134,58 +1224,15 @@ class XstageLayout:
         dest = torch.zeros(n_short + 8, dtype=torch.int32, device=dev)
         dest[wpos] = slot[perm].to(torch.int32)
         self.dest = dest.to(torch.int16)
-        del dest, slot, wpos, perm, pick, ec, pan, ew, er
+        self.xs = torch.zeros(n_short + 8, dtype=data.dtype, device=dev)
+        del dest, slot, wpos, perm, pick, ec, pan, ew, er, ks
         rc = torch.where(long_mask, 0xFFFF, short_len).to(torch.int32)
         self.row_count = torch.where(rc >= (1 << 15), rc - (1 << 16), rc).to(torch.int16)
         del rc
         self.windows = torch.stack([win_row0, win_rows_n, win_len, win_first], 1).to(
             torch.int32).contiguous()
-
-        # 4. The long rows, and the jobs of the first launch: every panel has at least one
-        #    job (the panel part's jobs, or one without chunks); a panel's staged entries are
-        #    split evenly over its jobs, in groups of 8.
-        long_rows = torch.nonzero(long_mask).flatten()
-        self.long = None
-        if long_rows.numel():
-            pick = torch.nonzero(long_mask[torch.repeat_interleave(
-                torch.arange(n_rows, device=dev), lengths, output_size=self.nnz)]).flatten()
-            long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
-            torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
-            self.long = PanelLayout(data[pick], cols[pick], long_ptr, n_cols, long_rows)
-            del pick
-            lg = self.long
-            if lg.col_bits != cb or lg.n_panels != P:
-                raise AssertionError("staged-x layout: the panel parts disagree on the panels")
-            njp = torch.bincount(lg.job_panel.to(torch.int64), minlength=P)
-            old_first = torch.cumsum(njp, 0) - njp
-            old_jobs = lg.jobs.to(torch.int64)
-            n_chunks = int(old_jobs[-1].item())
-            chunk0 = lg.panel_chunk0.to(torch.int64)
-        else:
-            njp = torch.zeros(P, dtype=torch.int64, device=dev)
-            old_first = njp
-            old_jobs = torch.zeros(1, dtype=torch.int64, device=dev)
-            n_chunks = 0
-            chunk0 = torch.zeros(P, dtype=torch.int64, device=dev)
-        added = njp == 0
-        nj = torch.where(added, 1, njp)
-        job_panel = torch.repeat_interleave(torch.arange(P, device=dev), nj)
-        n_jobs = int(job_panel.numel())
-        jfirst = torch.cumsum(nj, 0) - nj
-        k = torch.arange(n_jobs, device=dev) - jfirst[job_panel]
-        old = (old_first[job_panel] + k).clamp(max=max(int(old_jobs.numel()) - 2, 0))
-        starts = torch.where(added[job_panel], chunk0[job_panel], old_jobs[old])
-        self.jobs = torch.cat([starts, torch.tensor([n_chunks], device=dev)]).to(
-            torch.int32).contiguous()
-        self.job_panel = job_panel.to(torch.int32).contiguous()
-        self.n_jobs = n_jobs
-        units = padded_p // 8
-        s_lo = pstart[job_panel] + (k * units[job_panel] // nj[job_panel]) * 8
-        self.stage_jobs = torch.cat([s_lo, torch.tensor([n_staged], device=dev)]).to(
-            torch.int32).contiguous()
-        del k, old, starts, s_lo, job_panel
-        self._keep = (self.scol, self.xs, self.seg, self.vals, self.dest, self.row_count,
-                      self.windows, self.jobs, self.job_panel, self.stage_jobs)
+        self._keep = (self.scol, self.stage_info, self.seg_delta, self.xs, self.vals, self.dest,
+                      self.row_count, self.windows, self.jobs, self.job_panel, self.stage_jobs)
         if self.long is not None:
             self._keep = self._keep + self.long._keep
         self._args = {}
@@ -1195,13 +1242,14 @@ class XstageLayout:
         return "spmv_panel_kernel+stage_combine_kernel"
 
     def held_bytes(self, caller=()):
-        own = tensor_bytes(self.scol, self.xs, self.seg, self.vals, self.dest, self.row_count,
-                           self.windows, self.jobs, self.job_panel, self.stage_jobs)
+        own = tensor_bytes(*self._keep[:11])
         return own + (self.long.held_bytes(caller) if self.long is not None else 0)
 
     def describe(self):
         d = {"layout": self.kind, "panels": self.n_panels, "col_bits": self.col_bits,
-             "staged_entries": self.n_entries, "windows": self.n_windows, "jobs": self.n_jobs,
+             "window_cap": self.window_cap,
+             "staged_entries": self.n_entries, "segments": self.n_segments,
+             "windows": self.n_windows, "jobs": self.n_jobs,
              "long_rows": 0 if self.long is None else self.long.n_rows,
              "long_entries": 0 if self.long is None else self.long.nnz}
         if self.long is not None:
@@ -1221,13 +1269,13 @@ class XstageLayout:
                      self.n_cols, None, None, p(self.jobs), p(self.job_panel), self.n_jobs,
                      p(lg.chunk_info) if lg else None, p(lg.partials) if lg else None,
                      int(lg.partials.numel()) if lg else 0, None, None, None, 0, p(self.scol),
-                     p(self.stage_jobs), p(self.xs), self.n_staged, None]
+                     self.n_staged, p(self.stage_jobs), p(self.stage_info), p(self.seg_delta),
+                     p(self.xs), int(self.xs.numel()), None]
             second = [dt, int(acc_f64), None, None, 0, p(self.windows), self.n_windows,
-                      p(self.seg), self.n_panels, p(self.vals), p(self.dest), self.n_entries,
-                      p(self.xs), self.n_staged + 8, p(self.row_count),
-                      p(lg.partials) if lg else None, p(lg.rows) if lg else None,
-                      p(lg.row_ptr) if lg else None, p(lg.slots) if lg else None,
-                      lg.n_rows if lg else 0, None]
+                      self.window_cap, p(self.vals), p(self.dest), p(self.xs), self.n_entries,
+                      p(self.row_count), p(lg.partials) if lg else None,
+                      p(lg.rows) if lg else None, p(lg.row_ptr) if lg else None,
+                      p(lg.slots) if lg else None, lg.n_rows if lg else 0, None]
             args = (first, second)
             self._args[bool(acc_f64)] = args
         st = self._order.stream(y.device, self._keep)
@@ -1235,14 +1283,14 @@ class XstageLayout:
         if passes & 1:
             a = list(args[0])
             a[6], a[8] = x.data_ptr(), y.data_ptr()
-            a[24] = st
+            a[27] = st
             _abi.check(L.fsp_spmv_panels(*a), "fsp_spmv_panels")
         if passes & 2:
             a = list(args[1])
             a[2] = y.data_ptr()
             a[3] = None if row_map is None else row_map.data_ptr()
             a[4] = n_out
-            a[20] = st
+            a[18] = st
             _abi.check(L.fsp_spmv_stage_combine(*a), "fsp_spmv_stage_combine")
         return y
 

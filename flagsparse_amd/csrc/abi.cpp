@@ -27,7 +27,7 @@ using namespace fsp;
 
 extern "C" const char* fsp_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int fsp_abi_version(void) { return 15; }
+extern "C" int fsp_abi_version(void) { return 16; }
 
 extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }
@@ -37,7 +37,7 @@ extern "C" int64_t fsp_xcs_item_cap(void) { return kXcsItemCap; }
 extern "C" int64_t fsp_xcs_rows_cap(void) { return kXcsRowsCap; }
 extern "C" int64_t fsp_stage_window_cap(void) { return kStageWinCap; }
 extern "C" int64_t fsp_stage_window_rows_cap(void) { return kStageWinRows; }
-extern "C" int64_t fsp_stage_panels_cap(void) { return kStagePanelsCap; }
+extern "C" int64_t fsp_stage_chunk(void) { return kStageChunkEntries; }
 extern "C" int64_t fsp_xcs_window_slots_cap(void) { return kXcsWinSlotsCap; }
 extern "C" int64_t fsp_xcs_window_rows_cap(void) { return kXcsWinRowsCap; }
 extern "C" int64_t fsp_xcs_item_runs_cap(void) { return kXcsItemRunsCap; }

@@ -29,9 +29,9 @@ constexpr int64_t kXcsSortedColBits = 19;                // column bits of a sor
 constexpr int64_t kPanelBytes = 131072;                  // x panel copied to LDS (panel SpMV)
 constexpr int64_t kPanelChunk = 512;                     // entries per wave chunk (panel SpMV)
 constexpr int64_t kPanelChunkRunsCap = 64;               // runs (rows) of one chunk, at most
-constexpr int64_t kStageWinCap = 4096;                   // entries of one staged-x window
-constexpr int64_t kStageWinRows = 2048;                  // rows of one staged-x window
-constexpr int64_t kStagePanelsCap = 1024;                // x panels of the staged-x layout
+constexpr int64_t kStageWinCap = 8192;                   // entries of one staged-x window
+constexpr int64_t kStageWinRows = 4096;                  // rows of one staged-x window
+constexpr int64_t kStageChunkEntries = 512;             // staged entries per wave chunk
 
 // Zero y[0, n) on stream st (used before row-mapped launches that leave rows untouched).
 int fill_zero_f32(float* y, int64_t n, hipStream_t st);

@@ -721,56 +721,81 @@ static_assert(kPanelChunkRunsCap == kWave, "a chunk's runs are staged one per la
 
 constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
 
-// Rounds of 8-entry groups a thread of spmv_panel_kernel has in flight while staging.
-constexpr int kStageRounds = 4;
+// The staged-x pass of a job (see the file comment): chunks [c0, c1) of kStageChunk staged
+// entries, one wave per chunk, lane l taking entries 64k + l, so that each load of columns
+// and each store of staged values covers 64 consecutive entries.  Entry e of chunk c (in use:
+// below info.y) stores x[its column] at xs[e + sdelta[s]], s its segment: info.x for the
+// chunk's first entry, one more at every later entry whose column has the segment bit (a
+// layout rule: a chunk holds at most kWave segments).  The chunk's segment offsets are loaded
+// a lane each and handed round with ds_bpermute.  A chunk's columns are requested two chunks
+// ahead and its offsets one chunk ahead, so no wait of the loop is for a load issued in the
+// same round; every store is issued (entries not in use store past the buffer's range, which
+// the hardware drops), so the compiler keeps its count of the operations in flight.
+constexpr int kStageChunk = (int)kStageChunkEntries;
+constexpr uint32_t kSegStart = 0x8000u;  // scol: the entry opens a segment
 
-// The staged-x pass of a job (see the file comment): xs[e] = sx[scol[e]] for e in [s0, s1)
-// (multiples of 8), 8 consecutive entries per thread per group, the next round's column
-// loads issued before this round's values are stored.
 template <typename T>
-__device__ __forceinline__ void stage_panel_entries(const T* sx, uint32_t cmask,
-                                                    const uint16_t* __restrict__ scol, int s0,
-                                                    int s1, T* __restrict__ xs) {
-  constexpr int kRound = 8 * kPanelBlock;
-  constexpr int U = kStageRounds;
-  int e = s0 + 8 * (int)threadIdx.x;
-  i32x4 c[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int ee = e + u * kRound;
-    c[u] = ee < s1 ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(scol + ee))
-                   : i32x4{0, 0, 0, 0};
+__device__ __forceinline__ void store_staged(__amdgpu_buffer_rsrc_t r, unsigned off, T v) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(T) == 8) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, off, 0, 0);
   }
-  for (; e < s1; e += U * kRound) {
-    T v[U][8];
+}
+
+template <typename T>
+__device__ __forceinline__ void stage_panel_chunks(const T* sx, uint32_t cmask,
+                                                   const uint16_t* __restrict__ scol,
+                                                   const i32x2* __restrict__ sinfo,
+                                                   const int* __restrict__ sdelta, int c0,
+                                                   int c1, __amdgpu_buffer_rsrc_t xs) {
+  constexpr int kPer = kStageChunk / kWave;
+  constexpr int kStride = kPanelBlock / kWave;
+  const int lane = (int)threadIdx.x & (kWave - 1);
+  const int wid = (int)threadIdx.x / kWave;
+  struct Chunk {
+    uint32_t col[kPer];
+    i32x2 info;
+    int dl;
+  };
+  // past the job's last chunk: its last chunk again (loads only; never processed)
+  auto load_cols = [&](int c, Chunk& k) {
+    const int cc = c < c1 ? c : c1 - 1;
+    const int e0 = cc * kStageChunk;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t w[4] = {(uint32_t)c[u].x, (uint32_t)c[u].y, (uint32_t)c[u].z,
-                             (uint32_t)c[u].w};
+    for (int q = 0; q < kPer; ++q) k.col[q] = __builtin_nontemporal_load(scol + e0 + q * kWave + lane);
+    k.info = sinfo[cc];
+  };
+  auto load_dl = [&](Chunk& k) { k.dl = sdelta[k.info.x + lane]; };
+  int c = c0 + wid;
+  if (c >= c1) return;  // the whole wave
+  Chunk cur, nxt, nn;
+  load_cols(c, cur);
+  load_cols(c + kStride, nxt);
+  load_dl(cur);
+  for (; c < c1; c += kStride) {
+    load_dl(nxt);
+    load_cols(c + 2 * kStride, nn);
+    const unsigned base = (unsigned)(c * kStageChunk + lane);
+    int seen = 0;  // segment starts after the chunk's first entry, in the rounds before
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        v[u][q] = sx[((q & 1) ? (w[q >> 1] >> 16) : w[q >> 1]) & cmask];
+    for (int q = 0; q < kPer; ++q) {
+      const uint32_t w = cur.col[q];
+      const bool start = (w & kSegStart) != 0 && (q > 0 || lane > 0);
+      const uint64_t bal = __builtin_amdgcn_ballot_w64(start);
+      const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+      const int off = seen + below + (start ? 1 : 0);
+      seen += __builtin_popcountll(bal);
+      const int delta = __builtin_amdgcn_ds_bpermute(off << 2, cur.dl);
+      const T xv = sx[w & cmask];
+      const unsigned e = base + (unsigned)(q * kWave);
+      store_staged<T>(xs, q * kWave + lane < cur.info.y ? (e + (unsigned)delta) * (unsigned)sizeof(T)
+                                                        : kDropOffset, xv);
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int ee = e + (U + u) * kRound;
-      c[u] = ee < s1 ? __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(scol + ee))
-                     : i32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int ee = e + u * kRound;
-      if (ee < s1) {
-        if constexpr (sizeof(T) == 4) {
-          *reinterpret_cast<f32x4*>(xs + ee) = f32x4{v[u][0], v[u][1], v[u][2], v[u][3]};
-          *reinterpret_cast<f32x4*>(xs + ee + 4) = f32x4{v[u][4], v[u][5], v[u][6], v[u][7]};
-        } else {
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            *reinterpret_cast<f64x2*>(xs + ee + 2 * h) = f64x2{v[u][2 * h], v[u][2 * h + 1]};
-        }
-      }
-    }
+    cur = nxt;
+    nxt = nn;
   }
 }
 
@@ -780,7 +805,8 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     const T* __restrict__ x, int64_t x_len, const int* __restrict__ jobs,
     const int* __restrict__ job_panel, const i32x2* __restrict__ chunk_info,
     A* __restrict__ partials, int64_t n_partials, const uint16_t* __restrict__ scol,
-    const int* __restrict__ stage_jobs, T* __restrict__ xs) {
+    const int* __restrict__ stage_jobs, const i32x2* __restrict__ sinfo,
+    const int* __restrict__ sdelta, T* __restrict__ xs, int64_t n_xs) {
   extern __shared__ __align__(16) unsigned char s_dyn[];
   // Each wave's run sums of its current chunk in slot order (at most kWave: a layout rule),
   // then one slot per lane for the stores of lanes where no run ends.
@@ -960,7 +986,12 @@ __global__ __launch_bounds__(kPanelBlock) void spmv_panel_kernel(
     }
   }
   // the staged-x entries of the job, from the same LDS panel
-  if (scol != nullptr) stage_panel_entries<T>(sx, cmask, scol, stage_jobs[job], stage_jobs[job + 1], xs);
+  if (scol != nullptr) {
+    const __amdgpu_buffer_rsrc_t xs_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        xs, 0, (int)(n_xs * (int64_t)sizeof(T)), kBufferRsrcWord3);
+    stage_panel_chunks<T>(sx, cmask, scol, sinfo, sdelta, stage_jobs[job], stage_jobs[job + 1],
+                          xs_rsrc);
+  }
 }
 
 template <typename T, typename A>
@@ -1072,64 +1103,42 @@ __global__ __launch_bounds__(NB) void hybrid_combine_kernel(
                            win_cap);
 }
 
-// Staged-x windows (see the file comment).  Entries of a row summed inline by the thread that
-// holds the row; rows of more than kStageMed entries take a wave each.
-constexpr int kStageInline = 4;
-constexpr int kStageMed = 16;
+// Staged-x windows (see the file comment).
 constexpr uint16_t kStageSkip = 0xFFFFu;  // row_count: a row the window leaves alone
 
-// Window w of the staged-x layout, NB threads: the window's entries f < L are, in order, the
-// segments of panels 0, 1, ... (panel p's staged entries of the window's rows, in row order):
-// vals / dest at first + f (window-major), the staged x value at seg[w][p] + f - (the
-// segment's start in the window).  Products go to LDS position dest (the entry's rank in
-// (row, panel) order), then row r of the window gets the sum of its row_count[r] positions in
-// that order.
+// Window w of the staged-x layout, NB threads: the window's entries f < L (its segments, one
+// per panel with entries of the window's rows) are at first + f in vals, dest and xs (the
+// staged x values, written there by the panel jobs).  Products go to LDS position dest (the
+// entry's rank in (row, panel) order); a segmented scan over the positions (thread t:
+// positions 8t .. 8t + 7 in order, then the threads in a fixed DPP tree and the waves in
+// order) leaves each row's sum at its last position, and row r of the window (row_count[r]
+// positions) writes it to y.
 template <typename T, typename A, int NB>
 __device__ __forceinline__ void stage_combine_window(
-    int w, const i32x4* __restrict__ windows, const int* __restrict__ seg, int n_panels,
-    const T* __restrict__ vals, const int16_t* __restrict__ dest, const T* __restrict__ xs,
-    unsigned n_xs, const uint16_t* __restrict__ row_count, T* __restrict__ y,
-    const int* __restrict__ row_map) {
+    int w, const i32x4* __restrict__ windows, const T* __restrict__ vals,
+    const int16_t* __restrict__ dest, const T* __restrict__ xs,
+    const uint16_t* __restrict__ row_count, T* __restrict__ y, const int* __restrict__ row_map) {
   constexpr int kWaves = NB / kWave;
-  constexpr int kCap = (int)kStageWinCap;
-  constexpr int kPer = kCap / NB;                   // entries per thread
-  constexpr int kRowsPer = (int)kStageWinRows / NB;  // rows per thread
-  constexpr int kPanelsPer = (int)kStagePanelsCap / NB;
-  constexpr int kLongCap = kCap / (kStageInline + 1);
-  constexpr int kHugeCap = kCap / (kStageMed + 1);
+  constexpr int kPer = 8;                  // entries per thread
+  constexpr int kCap = kPer * NB;          // entries of a window
+  constexpr int kRowsPer = 4;              // rows per thread
+  static_assert(kCap <= (int)kStageWinCap && kRowsPer * NB <= (int)kStageWinRows, "caps");
+  static_assert(kPer == 8, "a thread scans one byte of row starts");
   static_assert(kRowsPer * kWaves <= kWave, "one lane per wave total of the row counts");
-  static_assert(kCap * 2 + (int)kStagePanelsCap * 4 <= kCap * (int)sizeof(A),
-                "the panel map and the segment offsets fit the product slots");
-  static_assert(kStageMed < 32 && kCap <= 8192 && kStageWinRows <= 8192, "row list packing");
-  // The products; before them (the same LDS) the panel of every window entry and the offset
-  // from window entry to staged entry of every panel.
-  __shared__ A s_val[kCap];
-  uint16_t* const s_map = reinterpret_cast<uint16_t*>(s_val);
-  int* const s_delta = reinterpret_cast<int*>(s_map + kCap);
-  __shared__ int s_wt[kWaves];
+  // The products, position p at slot p + p / 8 (a thread's 8 positions then start 9 slots
+  // after the previous thread's: its scan's LDS accesses do not all fall on the same banks).
+  __shared__ A s_val[kCap + kCap / kPer];
+  auto slot = [](int p) { return p + (p >> 3); };
+  __shared__ unsigned s_head[kCap / 32];  // a bit per position: a row starts there
   __shared__ int s_wtot[kRowsPer][kWaves];
-  __shared__ int s_nlong, s_nhuge;
-  // rows of kStageInline + 1 .. kStageMed entries: (row << 18) | (first position << 5) | count
-  __shared__ int s_long[kLongCap];
-  // rows of more: (row << 13) | first position, and the count
-  __shared__ int s_huge[kHugeCap];
-  __shared__ uint16_t s_hcnt[kHugeCap];
+  __shared__ int s_wh[kWaves];
+  __shared__ A s_wv[kWaves];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
-  if (tid == 0) s_nlong = 0, s_nhuge = 0;  // read after the barriers below
   const i32x4 win = windows[w];
   const int row0 = win.x, nr = win.y, L = win.z, first = win.w;
-  if (nr > (int)kStageWinRows || L > kCap) return;  // not a layout window (uniform)
-  // the window's segments (thread t: panels kPanelsPer t ..): their lengths and starts
-  int gs[kPanelsPer], len[kPanelsPer], own = 0;
-#pragma unroll
-  for (int u = 0; u < kPanelsPer; ++u) {
-    const int p = kPanelsPer * tid + u;
-    gs[u] = p < n_panels ? seg[(int64_t)w * n_panels + p] : 0;
-    len[u] = p < n_panels ? seg[(int64_t)(w + 1) * n_panels + p] - gs[u] : 0;
-    own += len[u];
-  }
-  // values and positions: window-major, contiguous
-  T v[kPer];
+  if (nr > kRowsPer * NB || L > kCap) return;  // not a layout window (uniform)
+  // values, positions and staged x values: window-major, contiguous
+  T v[kPer], xv[kPer];
   int d[kPer];
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
@@ -1137,6 +1146,7 @@ __device__ __forceinline__ void stage_combine_window(
     const int ff = f < L ? f : 0;  // past the end: the first entry again, dropped below
     v[k] = vals[first + ff];
     d[k] = dest[first + ff];
+    xv[k] = xs[first + ff];
   }
   int craw[kRowsPer];  // row counts, used after the products are in place
 #pragma unroll
@@ -1144,40 +1154,14 @@ __device__ __forceinline__ void stage_combine_window(
     const int r = tid + m * NB;
     craw[m] = r < nr ? (int)row_count[row0 + r] : 0;
   }
-  // segment starts in the window (a block scan of the lengths in panel order), the map of
-  // window entries to panels, and every panel's offset
-  const int incl = wave_incl_scan(own);
-  if (lane == kWave - 1) s_wt[wid] = incl;
-  __syncthreads();
-  int ls = incl - own;
-  for (int j = 0; j < wid; ++j) ls += s_wt[j];
-#pragma unroll
-  for (int u = 0; u < kPanelsPer; ++u) {
-    const int p = kPanelsPer * tid + u;
-    if (p < n_panels) {
-      s_delta[p] = gs[u] - ls;
-      for (int j = 0; j < len[u]; ++j) s_map[ls + j] = (uint16_t)p;
-    }
-    ls += len[u];
-  }
-  __syncthreads();
-  T xv[kPer];
+  if (tid < kCap / 32) s_head[tid] = 0u;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int f = tid + k * NB;
-    // past the end: staged entry 0, dropped below; an index outside the staged entries (a
-    // table that breaks the layout's rules) is clamped into them
-    const unsigned g = f < L ? (unsigned)(s_delta[s_map[f]] + f) : 0u;
-    xv[k] = xs[g < n_xs ? g : n_xs - 1u];
-  }
-  __syncthreads();  // every map read done: the products overwrite it
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int f = tid + k * NB;
-    if (f < L && (unsigned)d[k] < (unsigned)kCap) s_val[d[k]] = A(v[k]) * A(xv[k]);
+    if (f < L && (unsigned)d[k] < (unsigned)kCap) s_val[slot(d[k])] = A(v[k]) * A(xv[k]);
   }
   // first positions: an exclusive scan of the row counts in row order (thread t holds rows
-  // t, t + NB, ...; the wave totals scanned by wave 0)
+  // t, t + NB, ...; the wave totals scanned by wave 0); each row marks its first position
   int cnt[kRowsPer], rs[kRowsPer];
   bool skip[kRowsPer];
 #pragma unroll
@@ -1195,63 +1179,52 @@ __device__ __forceinline__ void stage_combine_window(
     const int ex = wave_incl_scan(t) - t;
     if (in) s_wtot[lane / kWaves][lane % kWaves] = ex;
   }
-  __syncthreads();  // products and wave offsets in place
+  __syncthreads();
 #pragma unroll
-  for (int m = 0; m < kRowsPer; ++m) rs[m] += s_wtot[m][wid];
-  // rows of up to kStageInline entries here; longer ones listed
+  for (int m = 0; m < kRowsPer; ++m) {
+    rs[m] += s_wtot[m][wid];
+    if (cnt[m] > 0 && rs[m] < kCap) atomicOr(&s_head[rs[m] >> 5], 1u << (rs[m] & 31));
+  }
+  __syncthreads();  // products and row starts in place
+  // the segmented scan: positions past L start rows of their own (and add nothing).  Each
+  // thread scans its positions in place; only the last position before its first row start
+  // (k0) then needs what the threads before carry in - a row that ends later has its sum
+  // complete from its own start.
+  const int p0 = kPer * tid;
+  const unsigned hb = (s_head[p0 >> 5] >> (p0 & 31)) & 0xFFu;
+  const unsigned hv = hb | (p0 + kPer > L ? ~0u << (L > p0 ? L - p0 : 0) : 0u);
+  const int k0 = hv ? __builtin_ctz(hv) : kPer;
+  A run = A(0), pre = A(0);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    if (p0 + q < L) {
+      const A vq = s_val[slot(p0) + q];
+      run = ((hv >> q) & 1u) ? vq : run + vq;
+      if (q + 1 == k0) pre = run;
+      s_val[slot(p0) + q] = run;
+    }
+  }
+  int h_in = hv ? 1 : 0, dummy = 0;
+  A v_in = run;
+  wave_seg_scan(h_in, v_in, dummy);
+  if (lane == kWave - 1) {
+    s_wh[wid] = h_in;
+    s_wv[wid] = v_in;
+  }
+  const A lane_c = dpp_bc<kDppWaveShr1, 0xF>(v_in);  // lane 0: 0
+  const int lane_h = dpp_bc<kDppWaveShr1, 0xF>(h_in);
+  __syncthreads();
+  A wave_c = A(0);  // what the waves before carry into this one, in wave order
+  for (int j = 0; j < wid; ++j) wave_c = s_wh[j] ? s_wv[j] : wave_c + s_wv[j];
+  const A cin = lane_h ? lane_c : wave_c + lane_c;
+  if (k0 > 0 && p0 + k0 - 1 < L) s_val[slot(p0) + k0 - 1] = cin + pre;
+  __syncthreads();  // every row's sum at its last position
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
     const int i = tid + m * NB;
     if (i >= nr || skip[m]) continue;
-    if (cnt[m] > kStageMed) {
-      const int at = atomicAdd(&s_nhuge, 1);
-      if (at < kHugeCap) {  // always, in a layout window
-        s_huge[at] = (i << 13) | rs[m];
-        s_hcnt[at] = (uint16_t)cnt[m];
-      }
-    } else if (cnt[m] > kStageInline) {
-      const int at = atomicAdd(&s_nlong, 1);
-      if (at < kLongCap) s_long[at] = (i << 18) | (rs[m] << 5) | cnt[m];
-    } else {
-      A t[kStageInline];
-#pragma unroll
-      for (int u = 0; u < kStageInline; ++u) t[u] = cnt[m] > u ? s_val[rs[m] + u] : A(0);
-      A acc = A(0);
-#pragma unroll
-      for (int u = 0; u < kStageInline; ++u)
-        if (cnt[m] > u) acc += t[u];
-      const int row = row0 + i;
-      y[row_map ? row_map[row] : row] = T(acc);
-    }
-  }
-  __syncthreads();
-  const int n_long = s_nlong < kLongCap ? s_nlong : kLongCap;
-  for (int j = tid; j < n_long; j += NB) {
-    const unsigned e = (unsigned)s_long[j];
-    const int i = (int)(e >> 18), a = (int)((e >> 5) & 0x1fffu), b = a + (int)(e & 0x1fu);
-    A r = A(0);  // 0 + s[a] + s[a + 1] + ..., in order
-    for (int k = a; k < b; k += 4) {
-      A t[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) t[u] = k + u < b ? s_val[k + u] : A(0);
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (k + u < b) r += t[u];
-    }
     const int row = row0 + i;
-    y[row_map ? row_map[row] : row] = T(r);
-  }
-  const int n_huge = s_nhuge < kHugeCap ? s_nhuge : kHugeCap;
-  for (int j = wid; j < n_huge; j += kWaves) {  // a wave per row: strided lanes, fixed tree
-    const int e = s_huge[j];
-    const int i = e >> 13, a = e & 0x1fff, b = a + (int)s_hcnt[j];
-    A r = A(0);
-    for (int k = a + lane; k < b; k += kWave) r += s_val[k];
-    r = wave_sum(r);
-    if (lane == 0) {
-      const int row = row0 + i;
-      y[row_map ? row_map[row] : row] = T(r);
-    }
+    y[row_map ? row_map[row] : row] = cnt[m] > 0 ? T(s_val[slot(rs[m] + cnt[m] - 1)]) : T(0);
   }
 }
 
@@ -1259,9 +1232,9 @@ __device__ __forceinline__ void stage_combine_window(
 // long rows (as in hybrid_combine_kernel), the rest the windows.
 template <typename T, typename A, int NB>
 __global__ __launch_bounds__(NB) void stage_combine_kernel(
-    const i32x4* __restrict__ windows, const int* __restrict__ seg, int n_panels,
-    const T* __restrict__ vals, const int16_t* __restrict__ dest, const T* __restrict__ xs,
-    unsigned n_xs, const uint16_t* __restrict__ row_count, const int* __restrict__ rows,
+    const i32x4* __restrict__ windows, const T* __restrict__ vals,
+    const int16_t* __restrict__ dest, const T* __restrict__ xs,
+    const uint16_t* __restrict__ row_count, const int* __restrict__ rows,
     const int* __restrict__ row_ptr, const int* __restrict__ slots,
     const A* __restrict__ panel_partials, int n_rows, int n_pblocks, T* __restrict__ y,
     const int* __restrict__ row_map) {
@@ -1273,8 +1246,8 @@ __global__ __launch_bounds__(NB) void stage_combine_kernel(
     return;
   }
   const int nw = (int)gridDim.x - n_pblocks;
-  stage_combine_window<T, A, NB>(xcd_logical_block(b - n_pblocks, nw), windows, seg, n_panels,
-                                 vals, dest, xs, n_xs, row_count, y, row_map);
+  stage_combine_window<T, A, NB>(xcd_logical_block(b - n_pblocks, nw), windows, vals, dest, xs,
+                                 row_count, y, row_map);
 }
 
 template <typename T, typename A>
@@ -1283,13 +1256,15 @@ int launch_panels(const void* vals, const uint16_t* pcol, int col_bits, const vo
                   const int32_t* job_panel, int64_t n_jobs, const int32_t* chunk_info,
                   void* partials, int64_t n_partials, const int32_t* rows,
                   const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
-                  const uint16_t* scol, const int32_t* stage_jobs, void* xs, hipStream_t st) {
+                  const uint16_t* scol, const int32_t* stage_jobs, const int32_t* sinfo,
+                  const int32_t* sdelta, void* xs, int64_t n_xs, hipStream_t st) {
   if (n_jobs > 0) {
     hipLaunchKernelGGL((spmv_panel_kernel<T, A>), dim3((unsigned)n_jobs), dim3(kPanelBlock),
                        ((size_t)1 << col_bits) * sizeof(T), st, static_cast<const T*>(vals),
                        pcol, col_bits, static_cast<const T*>(x), x_len, jobs, job_panel,
                        reinterpret_cast<const i32x2*>(chunk_info), static_cast<A*>(partials),
-                       n_partials, scol, stage_jobs, static_cast<T*>(xs));
+                       n_partials, scol, stage_jobs, reinterpret_cast<const i32x2*>(sinfo),
+                       sdelta, static_cast<T*>(xs), n_xs);
     int rc = check_hip(hipGetLastError(), "spmv_panel_kernel launch");
     if (rc) return rc;
   }
@@ -1321,24 +1296,41 @@ int launch_hybrid_combine(void* y, const int32_t* row_map, const void* xcs_parti
   return check_hip(hipGetLastError(), "hybrid_combine_kernel launch");
 }
 
-template <typename T, typename A>
-int launch_stage_combine(void* y, const int32_t* row_map, const int32_t* windows,
-                         int64_t n_windows, const int32_t* seg, int64_t n_panels,
-                         const void* vals, const int16_t* dest, const void* xs, int64_t n_xs,
-                         const uint16_t* row_count, const void* panel_partials,
-                         const int32_t* rows, const int32_t* row_ptr, const int32_t* slots,
-                         int64_t n_rows, hipStream_t st) {
-  constexpr int kRowsPerBlock = kCombBlock / kWave;
+// The staged-x combine's workgroup: 512 threads for windows of up to 4096 entries and 2048
+// rows (four workgroups per CU), 1024 for twice that (two per CU).
+template <typename T, typename A, int NB>
+int launch_stage_combine_nb(void* y, const int32_t* row_map, const int32_t* windows,
+                            int64_t n_windows, const void* vals, const int16_t* dest,
+                            const void* xs, const uint16_t* row_count,
+                            const void* panel_partials, const int32_t* rows,
+                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                            hipStream_t st) {
+  constexpr int kRowsPerBlock = NB / kWave;
   const int64_t n_pblocks = (n_rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int64_t grid = n_pblocks + n_windows;
   if (grid == 0) return FSP_OK;
-  hipLaunchKernelGGL((stage_combine_kernel<T, A, kCombBlock>), dim3((unsigned)grid),
-                     dim3(kCombBlock), 0, st, reinterpret_cast<const i32x4*>(windows), seg,
-                     (int)n_panels, static_cast<const T*>(vals), dest,
-                     static_cast<const T*>(xs), (unsigned)n_xs, row_count, rows, row_ptr,
-                     slots, static_cast<const A*>(panel_partials), (int)n_rows,
-                     (int)n_pblocks, static_cast<T*>(y), row_map);
+  hipLaunchKernelGGL((stage_combine_kernel<T, A, NB>), dim3((unsigned)grid), dim3(NB), 0, st,
+                     reinterpret_cast<const i32x4*>(windows), static_cast<const T*>(vals), dest,
+                     static_cast<const T*>(xs), row_count, rows, row_ptr, slots,
+                     static_cast<const A*>(panel_partials), (int)n_rows, (int)n_pblocks,
+                     static_cast<T*>(y), row_map);
   return check_hip(hipGetLastError(), "stage_combine_kernel launch");
+}
+
+template <typename T, typename A>
+int launch_stage_combine(void* y, const int32_t* row_map, const int32_t* windows,
+                         int64_t n_windows, int64_t window_cap, const void* vals,
+                         const int16_t* dest, const void* xs, const uint16_t* row_count,
+                         const void* panel_partials, const int32_t* rows,
+                         const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
+                         hipStream_t st) {
+  if (window_cap <= kStageWinCap / 2)
+    return launch_stage_combine_nb<T, A, 512>(y, row_map, windows, n_windows, vals, dest, xs,
+                                              row_count, panel_partials, rows, row_ptr, slots,
+                                              n_rows, st);
+  return launch_stage_combine_nb<T, A, 1024>(y, row_map, windows, n_windows, vals, dest, xs,
+                                             row_count, panel_partials, rows, row_ptr, slots,
+                                             n_rows, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1403,12 +1395,14 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
                                const int32_t* chunk_info, void* partials, int64_t n_partials,
                                const int32_t* rows, const int32_t* row_ptr,
                                const int32_t* slots, int64_t n_rows, const uint16_t* scol,
-                               const int32_t* stage_jobs, void* xs, int64_t n_staged,
-                               void* stream) {
+                               int64_t n_staged, const int32_t* stage_jobs,
+                               const int32_t* stage_info, const int32_t* seg_delta, void* xs,
+                               int64_t n_xs, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
     return set_error(FSP_ENOTSUP, "fsp_spmv_panels: dtype");
   const int64_t vsize = dtype == FSP_F32 ? 4 : 8;
-  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0 || n_partials < 0 || n_staged < 0)
+  if (n_entries < 0 || n_jobs < 0 || n_rows < 0 || x_len < 0 || n_partials < 0 ||
+      n_staged < 0 || n_xs < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: negative size");
   if (n_partials * 8 > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: more partial slots than 2^31 bytes hold");
@@ -1416,8 +1410,11 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
       n_jobs > 0x7fffffffLL || n_rows > 0x7fffffffLL - kBlock)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: n_entries must be a multiple of " +
                                      std::to_string(kPanelChunk) + " and sizes within int32");
-  if (n_staged % 8 != 0 || n_staged > 0x7fffffffLL - 8 * kPanelBlock * kStageRounds)
-    return set_error(FSP_EINVAL, "fsp_spmv_panels: n_staged must be a multiple of 8 below 2^31");
+  if (n_staged % kStageChunk != 0 || n_staged > 0x3fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: n_staged must be a multiple of " +
+                                     std::to_string(kStageChunk) + " below 2^30");
+  if (n_xs * vsize > 0x7fffffffLL)
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: staged values beyond 2^31 bytes");
   if (col_bits < 1 || col_bits > 15 || (vsize << col_bits) > kPanelBytes)
     return set_error(FSP_EINVAL, "fsp_spmv_panels: col_bits must be <= 15 and a panel of "
                                  "2^col_bits values must fit " +
@@ -1426,21 +1423,22 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null pointer");
   if (n_jobs > 0 && n_entries > 0 && (!vals || !pcol || !chunk_info || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null entry pointer");
-  if (n_jobs > 0 && n_staged > 0 && (!scol || !stage_jobs || !xs))
+  if (n_jobs > 0 && n_staged > 0 && (!scol || !stage_jobs || !stage_info || !seg_delta || !xs))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null staging pointer");
-  if ((reinterpret_cast<uintptr_t>(chunk_info) & 7u) != 0)
-    return set_error(FSP_EINVAL, "fsp_spmv_panels: chunk_info must be 8-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(chunk_info) & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(stage_info) & 7u) != 0)
+    return set_error(FSP_EINVAL,
+                     "fsp_spmv_panels: chunk_info and stage_info must be 8-byte aligned");
   if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !partials))
     return set_error(FSP_EINVAL, "fsp_spmv_panels: null row pointer");
-  if (!aligned16(vals) || !aligned16(pcol) || !aligned16(scol) || !aligned16(xs))
-    return set_error(FSP_EINVAL,
-                     "fsp_spmv_panels: vals, pcol, scol and xs must be 16-byte aligned");
+  if (!aligned16(vals) || !aligned16(pcol))
+    return set_error(FSP_EINVAL, "fsp_spmv_panels: vals and pcol must be 16-byte aligned");
   if (n_jobs == 0 && n_rows == 0) return FSP_OK;
   if (n_staged == 0) scol = nullptr;  // the kernel stages nothing
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define FSP_PANEL_ARGS vals, pcol, col_bits, x, x_len, y, row_map, jobs, job_panel, n_jobs, \
                        chunk_info, partials, n_partials, rows, row_ptr, slots, n_rows, scol, \
-                       stage_jobs, xs, st
+                       stage_jobs, stage_info, seg_delta, xs, n_xs, st
   if (dtype == FSP_F32) {
     if (acc_f64) return launch_panels<float, double>(FSP_PANEL_ARGS);
     return launch_panels<float, float>(FSP_PANEL_ARGS);
@@ -1451,25 +1449,24 @@ extern "C" int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const u
 
 extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
                                       int64_t n_out, const int32_t* windows, int64_t n_windows,
-                                      const int32_t* seg, int64_t n_panels, const void* vals,
-                                      const int16_t* dest, int64_t n_entries, const void* xs,
-                                      int64_t n_staged, const uint16_t* row_count,
+                                      int64_t window_cap, const void* vals,
+                                      const int16_t* dest, const void* xs,
+                                      int64_t n_entries, const uint16_t* row_count,
                                       const void* panel_partials, const int32_t* rows,
                                       const int32_t* row_ptr, const int32_t* slots,
                                       int64_t n_rows, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
     return set_error(FSP_ENOTSUP, "fsp_spmv_stage_combine: dtype");
-  if (n_windows < 0 || n_rows < 0 || n_panels < 0 || n_entries < 0 || n_staged < 0 || n_out < 0)
+  if (n_windows < 0 || n_rows < 0 || n_entries < 0 || n_out < 0)
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: negative size");
-  if (n_windows > 0x3fffffffLL || n_rows > 0x3fffffffLL || n_entries > 0x7fffffffLL ||
-      n_staged > 0x7fffffffLL)
+  if (n_windows > 0x3fffffffLL || n_rows > 0x3fffffffLL || n_entries > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: sizes beyond int32");
-  if (n_windows > 0 && (n_panels < 1 || n_panels > kStagePanelsCap))
-    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: n_panels outside [1, " +
-                                     std::to_string(kStagePanelsCap) + "]");
-  if (n_windows > 0 && (!y || !windows || !seg || !vals || !dest || !xs || !row_count ||
-                        n_staged < 1))
+  if (n_windows > 0 && (!y || !windows || !vals || !dest || !xs || !row_count))
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null window-table pointer");
+  if (n_windows > 0 && window_cap != kStageWinCap / 2 && window_cap != kStageWinCap)
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: window_cap must be " +
+                                     std::to_string(kStageWinCap / 2) + " or " +
+                                     std::to_string(kStageWinCap));
   if (n_rows > 0 && (!y || !rows || !row_ptr || !slots || !panel_partials))
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null panel-row pointer");
   if (!aligned16(windows))
@@ -1480,8 +1477,8 @@ extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int
                                 : fill_zero<double>(static_cast<double*>(y), n_out, st);
     if (rc) return rc;
   }
-#define FSP_STAGE_ARGS y, row_map, windows, n_windows, seg, n_panels, vals, dest, xs, n_staged, \
-                       row_count, panel_partials, rows, row_ptr, slots, n_rows, st
+#define FSP_STAGE_ARGS y, row_map, windows, n_windows, window_cap, vals, dest, xs, row_count, \
+                       panel_partials, rows, row_ptr, slots, n_rows, st
   if (dtype == FSP_F32) {
     if (acc_f64) return launch_stage_combine<float, double>(FSP_STAGE_ARGS);
     return launch_stage_combine<float, float>(FSP_STAGE_ARGS);

@@ -92,7 +92,7 @@ int64_t fsp_panel_chunk(void);           /* entries per chunk (panel SpMV)      
 int64_t fsp_panel_chunk_runs_cap(void);  /* runs (rows) per chunk, at most (panel SpMV) */
 int64_t fsp_stage_window_cap(void);      /* max entries of one staged-x window          */
 int64_t fsp_stage_window_rows_cap(void); /* max rows of one staged-x window             */
-int64_t fsp_stage_panels_cap(void);      /* max x panels of the staged-x layout         */
+int64_t fsp_stage_chunk(void);           /* staged entries per chunk (staged-x layout)  */
 
 /*
  * Host-side planner.  rowptr: host array of n_rows+1 int64 offsets (CSR indptr, or the
@@ -299,39 +299,43 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pc
                     int64_t n_jobs, const int32_t* chunk_info, void* partials,
                     int64_t n_partials, const int32_t* rows, const int32_t* row_ptr,
                     const int32_t* slots, int64_t n_rows, const uint16_t* scol,
-                    const int32_t* stage_jobs, void* xs, int64_t n_staged, void* stream);
+                    int64_t n_staged, const int32_t* stage_jobs, const int32_t* stage_info,
+                    const int32_t* seg_delta, void* xs, int64_t n_xs, void* stream);
 
 /*
- * The second pass of the staged-x layout (the short rows of power-law and uniform-random
- * matrices whose x exceeds an L2): fsp_spmv_panels' jobs stage x for them, xs[e] = the x value
- * at column (panel << col_bits) + scol[e] of their panel (scol, stage_jobs, xs, n_staged
- * above: job j stages entries [stage_jobs[j], stage_jobs[j+1]) of its panel, multiples of 8,
- * 16-byte aligned arrays; n_staged = 0 stages nothing), and this launch sums the rows, one
- * workgroup per window, beside the panel part's long rows (rows .. n_rows, over
- * panel_partials, as fsp_spmv_panels' second pass; n_rows may be 0).  Same reference launches
- * as fsp_spmv_csr.
+ * The staged-x layout (the short rows of matrices whose columns are spread over an x larger
+ * than an L2).  Its first pass is fsp_spmv_panels' jobs: job j, beside its chunks of long
+ * rows, stages x for chunks [stage_jobs[j], stage_jobs[j+1]) of fsp_stage_chunk() entries of
+ * its panel: scol (16 bits each, n_staged of them, a multiple of the chunk) = column -
+ * panel * 2^col_bits, | 0x8000 where the entry opens a segment (the entries of one panel for
+ * one window of rows); stage_info per chunk two int32 (8-byte aligned) {the segment of its
+ * first entry, its entries in use (the rest padding)}, a chunk holding at most 64 segments
+ * (counting the one its first entry continues); seg_delta per segment an int32 (and 64 more,
+ * any value, readable after the last): entry e of segment s stores its x value at xs[e +
+ * seg_delta[s]], inside xs[0 .. n_xs) (n_xs values of 2^31 bytes at most; a store outside is
+ * dropped).  n_staged = 0 stages nothing.
+ * fsp_spmv_stage_combine is the second pass: one workgroup per window of rows, beside the
+ * panel part's long rows (rows .. n_rows, over panel_partials, as fsp_spmv_panels' second
+ * pass; n_rows may be 0).  Same reference launches as fsp_spmv_csr.
  *   windows      n_windows int32 quadruples {row0, rows, entries L, first}: rows [row0, row0 +
- *                rows) (<= fsp_stage_window_rows_cap()), L <= fsp_stage_window_cap() entries
- *                vals[first .. first + L), dest[...] in window order: panel 0's staged entries
- *                of the window's rows (in row order), then panel 1's, ...
- *   seg          (n_windows + 1) x n_panels int32 (n_panels <= fsp_stage_panels_cap()):
- *                panel p's staged entries of window w are xs[seg[w][p] .. seg[w+1][p]), the
- *                lengths summing to L
- *   dest         int16 per entry: its rank in the window's (row, panel) order; entry f adds
- *                vals[first + f] * xs[...] (in the accumulation type) at that position
+ *                rows) (<= window_cap / 2), L <= window_cap entries at [first, first + L) of
+ *                vals, dest and xs (n_entries in all, the arrays readable 8 past the end)
+ *   window_cap   fsp_stage_window_cap() or half of it: workgroups of 1024 or 512 threads
+ *   dest         int16 per entry: its rank in the window's (row, panel) order; the product
+ *                vals[i] * xs[i] (in the accumulation type) goes to that position
  *   row_count    uint16 per row: the row's entries in its window (0xFFFF: a row the window
  *                leaves alone - y written by the panel rows); row r gets the sum of its
- *                positions in order (a fixed order for up to 16 entries, then lanes of a wave
- *                in order and a fixed tree)
+ *                positions (a segmented scan over the window's positions: 8 consecutive
+ *                positions per thread in order, then the threads in a fixed tree)
  *   row_map      NULL: layout row r is y[r]; else y[row_map[r]], and y[0..n_out) is zeroed
  *                first
  * Calls sharing xs or panel_partials must not overlap.
  */
 int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int32_t* row_map,
                            int64_t n_out, const int32_t* windows, int64_t n_windows,
-                           const int32_t* seg, int64_t n_panels, const void* vals,
-                           const int16_t* dest, int64_t n_entries, const void* xs,
-                           int64_t n_staged, const uint16_t* row_count,
+                           int64_t window_cap, const void* vals, const int16_t* dest,
+                           const void* xs,
+                           int64_t n_entries, const uint16_t* row_count,
                            const void* panel_partials, const int32_t* rows,
                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
                            void* stream);

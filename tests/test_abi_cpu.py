@@ -249,7 +249,7 @@ def test_kernel_entry_points_reject_before_any_hip_call():
                n_staged=0):
         return L.fsp_spmv_panels(dtype, 0, None, None, n_entries, col_bits, None, 1, None, None,
                                  None, None, n_jobs, None, None, n_partials, None, None, None,
-                                 n_rows, None, None, None, n_staged, None)
+                                 n_rows, None, n_staged, None, None, None, None, 0, None)
 
     assert panels() == 0                          # nothing to run
     assert panels(dtype=5) == -3
@@ -267,37 +267,41 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     # launch (the other pointers are never dereferenced on the host)
     fake = 1 << 20
     assert L.fsp_spmv_panels(0, 0, fake, fake, 512, 10, fake, 1024, None, None, fake, fake, 1,
-                             fake + 4, fake, 64, None, None, None, 0, None, None, None, 0,
-                             None) == -1
+                             fake + 4, fake, 64, None, None, None, 0, None, 0, None, None, None,
+                             None, 0, None) == -1
     assert b"chunk_info" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
-    # staging (the staged-x layout's first pass): whole groups of 8, arrays given
-    assert panels(n_staged=12) == -1
-    assert b"multiple of 8" in L.fsp_last_error()
+    # staging (the staged-x layout's first pass): whole chunks, its arrays given
+    chunk = L.fsp_stage_chunk()
+    assert chunk == 512
+    assert panels(n_staged=100) == -1
+    assert b"multiple" in L.fsp_last_error()
     assert L.fsp_spmv_panels(0, 0, None, None, 0, 10, fake, 1024, None, None, fake, fake, 1,
-                             None, None, 0, None, None, None, 0, None, None, None, 64,
-                             None) == -1
+                             None, None, 0, None, None, None, 0, None, chunk, None, None, None,
+                             None, 4, None) == -1
     assert b"staging" in L.fsp_last_error()
     assert L.fsp_spmv_panels(0, 0, None, None, 0, 10, fake, 1024, None, None, fake, fake, 1,
-                             None, None, 0, None, None, None, 0, fake + 8, fake, fake, 64,
-                             None) == -1
-    assert b"aligned" in L.fsp_last_error()
+                             None, None, 0, None, None, None, 0, fake, chunk, fake, fake + 4,
+                             fake, fake, 4, None) == -1
+    assert b"stage_info" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
 
-    def stage(dtype=0, n_windows=0, n_panels=1, n_rows=0, n_staged=8, tables=False):
+    def stage(dtype=0, n_windows=0, n_rows=0, tables=False):
         t = fake if tables else None
-        return L.fsp_spmv_stage_combine(dtype, 1, t, None, 0, t, n_windows, t, n_panels, t, t,
-                                        64, t, n_staged, t, None, None, None, None, n_rows,
-                                        None)
+        return L.fsp_spmv_stage_combine(dtype, 1, t, None, 0, t, n_windows, 4096, t, t, t, 64,
+                                        t, None, None, None, None, n_rows, None)
 
     assert stage() == 0                           # nothing to run
     assert stage(dtype=7) == -3
     assert stage(n_windows=2) == -1               # windows without their tables
     assert b"null" in L.fsp_last_error()
-    assert stage(n_windows=2, n_panels=L.fsp_stage_panels_cap() + 1, tables=True) == -1
-    assert b"n_panels" in L.fsp_last_error()
-    assert stage(n_windows=2, n_staged=0, tables=True) == -1  # nothing staged to read
     assert stage(n_rows=4) == -1                  # panel rows without their arrays
     assert b"panel-row" in L.fsp_last_error()
-    assert L.fsp_stage_window_cap() == 4096 and L.fsp_stage_window_rows_cap() == 2048
+    assert L.fsp_spmv_stage_combine(0, 1, fake, None, 0, fake + 4, 2, 4096, fake, fake, fake,
+                                    64, fake, None, None, None, None, 0, None) == -1
+    assert b"windows" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
+    assert L.fsp_spmv_stage_combine(0, 1, fake, None, 0, fake, 2, 1000, fake, fake, fake, 64,
+                                    fake, None, None, None, None, 0, None) == -1
+    assert b"window_cap" in L.fsp_last_error()
+    assert L.fsp_stage_window_cap() == 8192 and L.fsp_stage_window_rows_cap() == 4096
 
 
 def test_build_flags_kernels_with_scratch():

@@ -20,8 +20,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture(params=[("xcs-l2", 0), ("xcs-l2", 1), ("xcs-hybrid", 0), ("xcs-hybrid", 1),
-                        ("xstage", 0)],
-                ids=["xcs-rows", "xcs-sorted", "hybrid-rows", "hybrid-sorted", "xstage"])
+                        ("xstage", 0), ("xstage", 8192)],
+                ids=["xcs-rows", "xcs-sorted", "hybrid-rows", "hybrid-sorted", "xstage",
+                     "xstage-8192"])
 def force_xcs(request, monkeypatch):
     # the hybrid with rows of >= 32 entries in the panel part, so that these small matrices
     # have long rows in every case that checks the layout kind; the XCS items in row order
@@ -32,6 +33,8 @@ def force_xcs(request, monkeypatch):
     monkeypatch.setattr(_spmv_layouts, "SORTED_MIN_RUN", 0.0)
     if mode in ("xcs-hybrid", "xstage"):
         monkeypatch.setattr(_spmv_layouts, "FORCE_PANEL_ROW_MIN", 32)
+    if mode == "xstage":  # the staged-x windows: the size the layout picks, or the largest
+        monkeypatch.setattr(_spmv_layouts, "FORCE_STAGE_WINDOW", fmt or None)
     return mode
 
 
@@ -179,9 +182,10 @@ def test_xstage_marks_every_array(dev, monkeypatch):
         y = fs.flagsparse_spmv_csr(x=x.to(dev), prepared=p)
     torch.cuda.synchronize()
     lg = layout.long
-    wanted = (layout.scol, layout.xs, layout.seg, layout.vals, layout.dest, layout.row_count,
-              layout.windows, layout.jobs, layout.job_panel, layout.stage_jobs, lg.partials,
-              lg.vals, lg.pcol, lg.chunk_info, lg.rows, lg.row_ptr, lg.slots)
+    wanted = (layout.scol, layout.stage_info, layout.seg_delta, layout.xs, layout.vals,
+              layout.dest, layout.row_count, layout.windows, layout.jobs, layout.job_panel,
+              layout.stage_jobs, lg.partials, lg.vals, lg.pcol, lg.chunk_info, lg.rows,
+              lg.row_ptr, lg.slots)
     got = [ts for order, ts in seen if order is layout._order]
     assert got, "the layout's stream order was not consulted"
     for t in wanted:

@@ -1,10 +1,10 @@
 """The staged-x SpMV layout (flagsparse_amd/_spmv_layouts.py, XstageLayout), built on the CPU and
 checked without a GPU: the structure the kernels rely on (every short entry staged exactly once
-and placed exactly once in its window, windows of consecutive rows within their caps, segment
-tables that tile each window, LDS positions in (row, panel) order, staging ranges of whole
-groups of 8 inside their panel, one job per panel at least), and a step-by-step emulation of
-spmv_panel_kernel's staging and stage_combine_kernel's sums (with the panel part's long rows
-through the panel emulation) against the fp64 oracle."""
+and placed exactly once in its window, windows of consecutive rows within their caps, staged
+chunks inside one panel whose segment marks, first segments and offsets send every entry to
+its window position, LDS positions in (row, panel) order, one job per panel at least), and a
+step-by-step emulation of spmv_panel_kernel's staging and stage_combine_kernel's sums (with
+the panel part's long rows through the panel emulation) against the fp64 oracle."""
 
 import numpy as np
 import pytest
@@ -17,48 +17,49 @@ from test_xcs_layout_cpu import _case, _check_panels, _emulate_panels, _long_par
 
 
 def _stage(layout, x):
-    """spmv_panel_kernel's staging: job j stages entries [stage_jobs[j], stage_jobs[j+1]) of
-    its panel, xs[e] = x[(panel << col_bits) + scol[e]]."""
+    """spmv_panel_kernel's staging: job j stages chunks [stage_jobs[j], stage_jobs[j+1]) of its
+    panel; entry e of a chunk (below the chunk's count in use) has segment s = the chunk's first
+    segment plus the segment marks after the chunk's first entry up to e, and stores
+    x[(panel << col_bits) + its column] at xs[e + seg_delta[s]].  Returns xs and, per window
+    position, the staged entry stored there."""
+    chunk = _abi.caps()["stage_chunk"]
     cb = layout.col_bits
-    scol = layout.scol.numpy().view(np.uint16).astype(np.int64)
+    sc = layout.scol.numpy().view(np.uint16).astype(np.int64)
+    col, mark = sc & 0x7FFF, (sc >> 15) & 1
+    info = layout.stage_info.numpy().astype(np.int64)
+    delta = layout.seg_delta.numpy().astype(np.int64)
     sj = layout.stage_jobs.numpy().astype(np.int64)
     jp = layout.job_panel.numpy().astype(np.int64)
-    xs = np.zeros(layout.xs.numel(), dtype=np.float64)
+    xs = np.full(layout.xs.numel(), np.nan)
+    src = np.full(layout.xs.numel(), -1)
     for j in range(layout.n_jobs):
-        e = np.arange(sj[j], sj[j + 1])
-        col = (jp[j] << cb) + scol[e]
-        xs[e] = x[np.minimum(col, x.size - 1)]
-    return xs
-
-
-def _windows(layout):
-    """Per window: (row0, rows, entries, first, [(panel, staged start, staged end)])."""
-    w = layout.windows.numpy().astype(np.int64)
-    seg = layout.seg.numpy().astype(np.int64)
-    out = []
-    for k in range(layout.n_windows):
-        segs = [(p, seg[k, p], seg[k + 1, p]) for p in range(layout.n_panels)
-                if seg[k + 1, p] > seg[k, p]]
-        out.append((*w[k].tolist(), segs))
-    return out
+        for c in range(sj[j], sj[j + 1]):
+            e0 = c * chunk
+            seg = info[c, 0]
+            for q in range(info[c, 1]):
+                e = e0 + q
+                if q > 0 and mark[e]:
+                    seg += 1
+                out = e + delta[seg]
+                assert 0 <= out < layout.n_entries and src[out] == -1
+                src[out] = e
+                xs[out] = x[min((jp[j] << cb) + col[e], x.size - 1)]
+    return xs, src
 
 
 def _emulate(layout, x, y, row_map=None, acc=np.float64):
-    """stage_combine_kernel's windows: entry f of window k (its segments in panel order) adds
-    vals[first + f] * xs[segment position] at LDS position dest[first + f]; row r of the window
-    gets its row_count[r] positions summed in order (count 0xFFFF: left alone)."""
-    xs = _stage(layout, x).astype(acc)
+    """stage_combine_kernel's windows: entry i of the window adds vals[i] * xs[i] at LDS
+    position dest[i]; row r of the window gets its row_count[r] positions summed in order
+    (count 0xFFFF: left alone)."""
+    xs, _ = _stage(layout, x)
+    xs = xs.astype(acc)
     vals = layout.vals.numpy().astype(acc)
     dest = layout.dest.numpy().astype(np.int64)
     rc = layout.row_count.numpy().view(np.uint16).astype(np.int64)
-    for row0, nr, L, first, segs in _windows(layout):
-        s = np.full(_abi.caps()["stage_window"], np.nan)
-        f = 0
-        for _, g0, g1 in segs:
-            for g in range(g0, g1):
-                s[dest[first + f]] = acc(vals[first + f] * xs[g])
-                f += 1
-        assert f == L
+    for row0, nr, L, first in layout.windows.numpy().astype(np.int64):
+        s = np.full(layout.window_cap, np.nan)
+        for i in range(first, first + L):
+            s[dest[i]] = acc(vals[i] * xs[i])
         pos = 0
         for i in range(nr):
             c = rc[row0 + i]
@@ -85,40 +86,36 @@ def _check(layout, vals, cols, ip, long_mask):
     w = layout.windows.numpy().astype(np.int64)
     assert w[0, 0] == 0 and w[-1, 0] + w[-1, 1] == n_rows
     assert np.all(w[1:, 0] == w[:-1, 0] + w[:-1, 1])
-    assert np.all(w[:, 1] <= caps["stage_window_rows"]) and np.all(w[:, 2] <= caps["stage_window"])
+    assert np.all(w[:, 1] <= layout.window_cap // 2) and np.all(w[:, 2] <= layout.window_cap)
     assert np.all(w[1:, 3] == w[:-1, 3] + w[:-1, 2]) and w[0, 3] == 0
     rc = layout.row_count.numpy().view(np.uint16).astype(np.int64)
     assert np.all(rc[long_mask] == 0xFFFF)
     assert np.array_equal(rc[short], lengths[short])
-    # staging ranges: whole groups of 8, inside the job's panel, covering the staged entries
+    # staged chunks: each job's inside its panel, every panel with a job, chunks covering
+    # the staged entries; every window position written by exactly one staged entry
+    chunk = caps["stage_chunk"]
     sj = layout.stage_jobs.numpy().astype(np.int64)
     jp = layout.job_panel.numpy().astype(np.int64)
-    assert sj[0] == 0 and sj[-1] == layout.n_staged and np.all(sj % 8 == 0)
+    assert sj[0] == 0 and sj[-1] * chunk == layout.n_staged
     assert np.all(np.diff(sj) >= 0) and np.all(np.diff(jp) >= 0)
     assert np.array_equal(np.unique(jp), np.arange(P))  # every panel has a job
-    seg = layout.seg.numpy().astype(np.int64)
-    for p in range(P):
-        js = np.nonzero(jp == p)[0]
-        lo, hi = sj[js[0]], sj[js[-1] + 1]
-        assert lo <= seg[:, p].min() and seg[:, p].max() <= hi and hi - seg[-1, p] < 8
-        assert np.all(np.diff(seg[:, p]) >= 0)
+    x_probe = np.arange(layout.n_cols, dtype=np.float64)  # x[c] = c names the column
+    xs, src = _stage(layout, x_probe)
+    assert np.all(src[:layout.n_entries] >= 0)
     # every short entry once, its LDS position its rank in (row, panel) order
-    scol = layout.scol.numpy().view(np.uint16).astype(np.int64)
     v = layout.vals.numpy()
     dest = layout.dest.numpy().astype(np.int64)
     got = []
-    for row0, nr, L, first, segs in _windows(layout):
+    for row0, nr, L, first in layout.windows.numpy().astype(np.int64):
         counts = np.where(rc[row0:row0 + nr] == 0xFFFF, 0, rc[row0:row0 + nr])
         row_of_pos = np.repeat(np.arange(row0, row0 + nr), counts)
         panel_at = np.full(L, -1)
-        f = 0
-        for p, g0, g1 in segs:
-            for g in range(g0, g1):
-                d = dest[first + f]
-                assert 0 <= d < L and panel_at[d] == -1
-                panel_at[d] = p
-                got.append((int(row_of_pos[d]), int((p << cb) + scol[g]), float(v[first + f])))
-                f += 1
+        for i in range(first, first + L):
+            d = dest[i]
+            assert 0 <= d < L and panel_at[d] == -1
+            col = int(xs[i])
+            panel_at[d] = col >> cb
+            got.append((int(row_of_pos[d]), col, float(v[i])))
         # inside each row, positions in panel order
         for r in range(nr):
             a = counts[:r].sum()
@@ -138,8 +135,16 @@ def _run(layout, x, n_rows, row_map=None, n_out=None):
     return y
 
 
+@pytest.fixture(params=[None, 8192], ids=["auto-window", "window8192"])
+def window(request, monkeypatch):
+    """Each test with the window size the layout picks, and with the largest (1024-thread
+    combine workgroups)."""
+    monkeypatch.setattr(_spmv_layouts, "FORCE_STAGE_WINDOW", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
-def test_xstage_power_law_with_long_rows(seed):
+def test_xstage_power_law_with_long_rows(seed, window):
     rng = np.random.default_rng(seed)
     n_cols = 300000  # 10 panels of 2^15 columns
     lengths = rng.zipf(1.6, 5000).clip(max=40000)
@@ -149,7 +154,7 @@ def test_xstage_power_law_with_long_rows(seed):
     assert 0 < long_mask.sum() < 5000
     lay = XstageLayout(vals, cols, ip, n_cols, torch.as_tensor(long_mask))
     assert lay.long is not None and lay.n_panels == 10
-    # rows longer than a quarter window are in the panel part too
+    # rows longer than an eighth of the largest window are in the panel part too
     assert lay.long.n_rows == int((long_mask | (lengths > 1024)).sum())
     _check(lay, vals.numpy(), cols.numpy(), ip, long_mask | (lengths > 1024))
     y = _run(lay, x.numpy(), lengths.size)
@@ -161,7 +166,7 @@ def test_xstage_power_law_with_long_rows(seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
-def test_xstage_short_rows_only(dtype):
+def test_xstage_short_rows_only(dtype, window):
     rng = np.random.default_rng(7)
     lengths = rng.integers(0, 40, 9000)
     n_cols = 70000
@@ -176,22 +181,40 @@ def test_xstage_short_rows_only(dtype):
     assert np.all(y[lengths == 0] == 0.0)
 
 
-def test_xstage_window_row_cap_and_small_x():
+def test_xstage_window_row_cap_and_small_x(window):
     # mostly empty rows: windows are cut by their row cap; x of one panel
-    lengths = np.zeros(7000, dtype=np.int64)
+    lengths = np.zeros(17000, dtype=np.int64)
     lengths[::97] = 3
     vals, cols, ip, x = _case(lengths, 5000, 5)
-    lay = XstageLayout(vals, cols, ip, 5000, torch.zeros(7000, dtype=torch.bool))
+    lay = XstageLayout(vals, cols, ip, 5000, torch.zeros(17000, dtype=torch.bool))
     assert lay.n_panels == 1 and lay.n_windows >= 4
-    _check(lay, vals.numpy(), cols.numpy(), ip, np.zeros(7000, dtype=bool))
-    y = _run(lay, x.numpy(), 7000)
+    assert int(lay.windows[:, 1].max()) == lay.window_cap // 2  # windows cut by rows
+    _check(lay, vals.numpy(), cols.numpy(), ip, np.zeros(17000, dtype=bool))
+    y = _run(lay, x.numpy(), 17000)
     np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
 
 
-def test_xstage_too_many_panels():
-    vals, cols, ip, x = _case([2] * 10, 1 << 26, 1)  # 2048 panels of 2^15 columns
-    with pytest.raises(ValueError):
-        XstageLayout(vals, cols, ip, 1 << 26, torch.zeros(10, dtype=torch.bool))
+def test_xstage_chunks_of_many_segments(window):
+    # sparse rows: windows cut by their row cap, each panel's entries spread over ~150 windows
+    # in segments of one or two entries, so that chunks close at the kernel's 64 segments and
+    # end in padding
+    n = 600000
+    lengths = np.zeros(n, dtype=np.int64)
+    lengths[::40] = 1
+    lengths[5::200] = 3
+    vals, cols, ip, x = _case(lengths, 1 << 21, 1)
+    lay = XstageLayout(vals, cols, ip, 1 << 21, torch.zeros(n, dtype=torch.bool))
+    assert lay.n_panels == 64
+    info = lay.stage_info.numpy().astype(np.int64)
+    segs_in_chunk = np.diff(np.append(info[:, 0], lay.n_segments))
+    # a chunk's segments: those starting in it, plus the one its first entry continues
+    sc = lay.scol.numpy().view(np.uint16).astype(np.int64)[:lay.n_staged].reshape(-1, 512)
+    pieces = (sc[:, 1:] >> 15).sum(1) + 1
+    assert pieces.max() == 64 and (info[:, 1] < 512).sum() > lay.n_panels
+    assert np.all(segs_in_chunk <= pieces)
+    _check(lay, vals.numpy(), cols.numpy(), ip, np.zeros(n, dtype=bool))
+    y = _run(lay, x.numpy(), n)
+    np.testing.assert_allclose(y, oracle.spmv_csr(ip, cols, vals, x), rtol=1e-12, atol=1e-12)
 
 
 def test_xstage_is_the_default_for_spread_columns(monkeypatch):

@@ -4,7 +4,8 @@ The prepared objects keep their partial-sum workspaces across calls (no per-call
 unlike the reference's spmm_csr.py:979-983); a call from another stream than the previous one
 is ordered after the work queued on that stream (_plan.StreamOrder).  Every layout with a
 workspace is driven from two same-priority streams in alternation - the row-block SpMV with
-split rows, the XCS + panel hybrid, and SpMM with split rows - and each result must match the
+split rows, the XCS + panel hybrid, the staged-x layout (its staged values are a workspace
+too), and SpMM with split rows - and each result must match the
 fp64 oracle.
 """
 
@@ -41,7 +42,7 @@ def _alternate(dev, call, inputs, rounds=4):
     return outs
 
 
-@pytest.mark.parametrize("layout", ["rowblock", "xcs-hybrid"])
+@pytest.mark.parametrize("layout", ["rowblock", "xcs-hybrid", "xstage"])
 def test_spmv_two_streams(dev, layout, monkeypatch):
     monkeypatch.setattr(_spmv_layouts, "FORCE", layout)
     rng = np.random.default_rng(7)

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 
 FSP_F32 = 0
 FSP_F64 = 1
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 _lib = None
 
@@ -59,7 +59,7 @@ SIGNATURES = {
                                _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64,
                                _p]),
     "fsp_spmv_stage_combine": (_i32, [_i32, _i32, _p, _p, _i64, _p, _i64, _i64, _p, _p, _p,
-                                      _i64, _p, _p, _p, _p, _p, _i64, _p]),
+                                      _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "fsp_spmv_hybrid_combine": (_i32, [_i32, _i32, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
                                        _p, _p, _i64, _p]),
     "fsp_spmv_coo_atomic": (_i32, [_i32, _p, _p, _p, _i64, _p, _p, _i64, _i64, _p]),

@@ -1205,7 +1205,14 @@ class XstageLayout:
         ordered_len = seg_len[seg_order]
         seg_wpos = torch.empty_like(seg_len)
         seg_wpos[seg_order] = torch.cumsum(ordered_len, 0) - ordered_len  # window-major start
-        del seg_key, seg_order, ordered_len, seg_chunk, seg_job, s_lo
+        # each window starts at a multiple of 8 entries (the combine's 16-byte loads)
+        win_pad = (win_len + 7) // 8 * 8
+        win_start = torch.cumsum(win_pad, 0) - win_pad
+        n_pos = int((win_start[-1] + win_pad[-1]).item()) if W else 0
+        if n_pos > _INDEX_LIMIT_INT32 - 64:
+            raise ValueError("too many entries for the staged-x layout")
+        seg_wpos += (win_start - win_first)[ks[first_e] % Wk]
+        del seg_key, seg_order, ordered_len, seg_chunk, seg_job, s_lo, win_pad
         sdelta = torch.zeros(n_seg + 64, dtype=torch.int64, device=dev)
         sdelta[:n_seg] = seg_wpos - seg_pos
         self.seg_delta = sdelta.to(torch.int32).contiguous()
@@ -1219,20 +1226,33 @@ class XstageLayout:
         del order2, ar
         slot = rank - win_first[ew]
         del rank
-        self.vals = torch.zeros(n_short + 8, dtype=data.dtype, device=dev)
+        self.n_positions = n_pos
+        self.vals = torch.zeros(n_pos + 8, dtype=data.dtype, device=dev)
         self.vals[wpos] = data[pick][perm]
-        dest = torch.zeros(n_short + 8, dtype=torch.int32, device=dev)
+        dest = torch.zeros(n_pos + 8, dtype=torch.int32, device=dev)
         dest[wpos] = slot[perm].to(torch.int32)
         self.dest = dest.to(torch.int16)
-        self.xs = torch.zeros(n_short + 8, dtype=data.dtype, device=dev)
+        self.xs = torch.zeros(n_pos + 8, dtype=data.dtype, device=dev)
         del dest, slot, wpos, perm, pick, ec, pan, ew, er, ks
-        rc = torch.where(long_mask, 0xFFFF, short_len).to(torch.int32)
-        self.row_count = torch.where(rc >= (1 << 15), rc - (1 << 16), rc).to(torch.int16)
-        del rc
-        self.windows = torch.stack([win_row0, win_rows_n, win_len, win_first], 1).to(
+        # per row the end of its positions in its window (| 0x8000: a row left to the panel
+        # part); per window a bit per position where a row starts
+        rstart = torch.cumsum(short_len, 0) - short_len
+        if n_rows:
+            rstart -= win_first[win_of_row]
+        re = (rstart + short_len) | torch.where(long_mask, 0x8000, 0)
+        self.row_end = torch.where(re >= (1 << 15), re - (1 << 16), re).to(torch.int16)
+        del re
+        opens = torch.nonzero(short_len > 0).flatten()
+        hpos = rstart[opens] + win_of_row[opens] * win_cap
+        heads = torch.zeros(W * win_cap // 8 + 1, dtype=torch.int32, device=dev)
+        heads.index_add_(0, hpos >> 3, (1 << (hpos & 7)).to(torch.int32))
+        self.heads = heads.to(torch.uint8)
+        del heads, hpos, opens, rstart
+        self.windows = torch.stack([win_row0, win_rows_n, win_len, win_start], 1).to(
             torch.int32).contiguous()
         self._keep = (self.scol, self.stage_info, self.seg_delta, self.xs, self.vals, self.dest,
-                      self.row_count, self.windows, self.jobs, self.job_panel, self.stage_jobs)
+                      self.row_end, self.heads, self.windows, self.jobs, self.job_panel,
+                      self.stage_jobs)
         if self.long is not None:
             self._keep = self._keep + self.long._keep
         self._args = {}
@@ -1242,7 +1262,7 @@ class XstageLayout:
         return "spmv_panel_kernel+stage_combine_kernel"
 
     def held_bytes(self, caller=()):
-        own = tensor_bytes(*self._keep[:11])
+        own = tensor_bytes(*self._keep[:12])
         return own + (self.long.held_bytes(caller) if self.long is not None else 0)
 
     def describe(self):
@@ -1272,8 +1292,9 @@ class XstageLayout:
                      self.n_staged, p(self.stage_jobs), p(self.stage_info), p(self.seg_delta),
                      p(self.xs), int(self.xs.numel()), None]
             second = [dt, int(acc_f64), None, None, 0, p(self.windows), self.n_windows,
-                      self.window_cap, p(self.vals), p(self.dest), p(self.xs), self.n_entries,
-                      p(self.row_count), p(lg.partials) if lg else None,
+                      self.window_cap, p(self.vals), p(self.dest), p(self.xs),
+                      int(self.vals.numel()),
+                      p(self.row_end), p(self.heads), p(lg.partials) if lg else None,
                       p(lg.rows) if lg else None, p(lg.row_ptr) if lg else None,
                       p(lg.slots) if lg else None, lg.n_rows if lg else 0, None]
             args = (first, second)
@@ -1290,7 +1311,7 @@ class XstageLayout:
             a[2] = y.data_ptr()
             a[3] = None if row_map is None else row_map.data_ptr()
             a[4] = n_out
-            a[18] = st
+            a[19] = st
             _abi.check(L.fsp_spmv_stage_combine(*a), "fsp_spmv_stage_combine")
         return y
 

@@ -27,7 +27,7 @@ using namespace fsp;
 
 extern "C" const char* fsp_last_error(void) { return g_last_error.c_str(); }
 
-extern "C" int fsp_abi_version(void) { return 16; }
+extern "C" int fsp_abi_version(void) { return 17; }
 
 extern "C" int64_t fsp_spmv_stream_nnz_cap(void) { return kSpmvStreamNnzCap; }
 extern "C" int64_t fsp_spmv_stream_rows_cap(void) { return kSpmvStreamRowsCap; }

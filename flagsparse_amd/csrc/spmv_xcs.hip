@@ -1103,95 +1103,93 @@ __global__ __launch_bounds__(NB) void hybrid_combine_kernel(
                            win_cap);
 }
 
+// N consecutive values from p (16-byte aligned) by 16-byte loads.
+template <int N, typename T>
+__device__ __forceinline__ void load16x(const T* __restrict__ p, T (&out)[N]) {
+  constexpr int kPerLoad = 16 / sizeof(T);
+  static_assert(N % kPerLoad == 0, "whole 16-byte loads");
+  const i32x4* q = reinterpret_cast<const i32x4*>(p);
+#pragma unroll
+  for (int j = 0; j < N / kPerLoad; ++j) {
+    const i32x4 w = q[j];
+    __builtin_memcpy(&out[j * kPerLoad], &w, 16);
+  }
+}
+
 // Staged-x windows (see the file comment).
-constexpr uint16_t kStageSkip = 0xFFFFu;  // row_count: a row the window leaves alone
+constexpr uint32_t kStageSkip = 0x8000u;  // row_end: a row the window leaves alone
 
 // Window w of the staged-x layout, NB threads: the window's entries f < L (its segments, one
 // per panel with entries of the window's rows) are at first + f in vals, dest and xs (the
-// staged x values, written there by the panel jobs).  Products go to LDS position dest (the
+// staged x values, written there by the panel jobs), first a multiple of 8 and the arrays
+// readable up to the next multiple of 8 past first + L.  Products go to LDS position dest (the
 // entry's rank in (row, panel) order); a segmented scan over the positions (thread t:
-// positions 8t .. 8t + 7 in order, then the threads in a fixed DPP tree and the waves in
-// order) leaves each row's sum at its last position, and row r of the window (row_count[r]
-// positions) writes it to y.
+// positions 8t .. 8t + 7 in order, marked where a row starts by the bits of heads[w * NB + t],
+// then the threads in a fixed DPP tree and the waves in order) leaves each row's sum at its
+// last position, and row r of the window, positions [row_end[r - 1], row_end[r]) (0 for the
+// first row), writes it to y.
 template <typename T, typename A, int NB>
 __device__ __forceinline__ void stage_combine_window(
     int w, const i32x4* __restrict__ windows, const T* __restrict__ vals,
     const int16_t* __restrict__ dest, const T* __restrict__ xs,
-    const uint16_t* __restrict__ row_count, T* __restrict__ y, const int* __restrict__ row_map) {
+    const uint16_t* __restrict__ row_end, const uint8_t* __restrict__ heads,
+    T* __restrict__ y, const int* __restrict__ row_map) {
   constexpr int kWaves = NB / kWave;
   constexpr int kPer = 8;                  // entries per thread
   constexpr int kCap = kPer * NB;          // entries of a window
   constexpr int kRowsPer = 4;              // rows per thread
   static_assert(kCap <= (int)kStageWinCap && kRowsPer * NB <= (int)kStageWinRows, "caps");
   static_assert(kPer == 8, "a thread scans one byte of row starts");
-  static_assert(kRowsPer * kWaves <= kWave, "one lane per wave total of the row counts");
   // The products, position p at slot p + p / 8 (a thread's 8 positions then start 9 slots
   // after the previous thread's: its scan's LDS accesses do not all fall on the same banks).
   __shared__ A s_val[kCap + kCap / kPer];
   auto slot = [](int p) { return p + (p >> 3); };
-  __shared__ unsigned s_head[kCap / 32];  // a bit per position: a row starts there
-  __shared__ int s_wtot[kRowsPer][kWaves];
   __shared__ int s_wh[kWaves];
   __shared__ A s_wv[kWaves];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const i32x4 win = windows[w];
   const int row0 = win.x, nr = win.y, L = win.z, first = win.w;
-  if (nr > kRowsPer * NB || L > kCap) return;  // not a layout window (uniform)
-  // values, positions and staged x values: window-major, contiguous
+  if (nr > kRowsPer * NB || L > kCap || (first & (kPer - 1))) return;  // not a layout window
+  // values, positions and staged x values: window-major, entries f0 .. f0 + 7 of the window
+  // by 16-byte loads (the window starts at a multiple of 8 entries, the arrays are padded to
+  // the next window); a thread past the end loads the first entries again, dropped below
+  const int f0 = kPer * tid;
+  const int64_t g = first + (f0 < L ? f0 : 0);
   T v[kPer], xv[kPer];
   int d[kPer];
+  load16x<kPer>(vals + g, v);
+  load16x<kPer>(xs + g, xv);
+  {
+    const i32x4 dw = *reinterpret_cast<const i32x4*>(dest + g);
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int f = tid + k * NB;
-    const int ff = f < L ? f : 0;  // past the end: the first entry again, dropped below
-    v[k] = vals[first + ff];
-    d[k] = dest[first + ff];
-    xv[k] = xs[first + ff];
+    for (int j = 0; j < 4; ++j) {
+      d[2 * j] = (int)(int16_t)(dw[j] & 0xFFFF);
+      d[2 * j + 1] = dw[j] >> 16;
+    }
   }
-  int craw[kRowsPer];  // row counts, used after the products are in place
-#pragma unroll
-  for (int m = 0; m < kRowsPer; ++m) {
-    const int r = tid + m * NB;
-    craw[m] = r < nr ? (int)row_count[row0 + r] : 0;
-  }
-  if (tid < kCap / 32) s_head[tid] = 0u;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int f = tid + k * NB;
-    if (f < L && (unsigned)d[k] < (unsigned)kCap) s_val[slot(d[k])] = A(v[k]) * A(xv[k]);
-  }
-  // first positions: an exclusive scan of the row counts in row order (thread t holds rows
-  // t, t + NB, ...; the wave totals scanned by wave 0); each row marks its first position
-  int cnt[kRowsPer], rs[kRowsPer];
+  const unsigned hb = heads[(int64_t)w * NB + tid];
+  // the rows' positions: [start, end) (both 0 past the window's rows)
+  int start[kRowsPer], end[kRowsPer];
   bool skip[kRowsPer];
 #pragma unroll
   for (int m = 0; m < kRowsPer; ++m) {
-    skip[m] = craw[m] == (int)kStageSkip;
-    cnt[m] = skip[m] ? 0 : craw[m];
-    rs[m] = wave_incl_scan(cnt[m]);
-    if (lane == kWave - 1) s_wtot[m][wid] = rs[m];
-    rs[m] -= cnt[m];
+    const int r = tid + m * NB;
+    const unsigned e = r < nr ? row_end[row0 + r] : 0u;
+    const unsigned e0 = (r > 0 && r < nr) ? row_end[row0 + r - 1] : 0u;
+    skip[m] = (e & kStageSkip) != 0;
+    end[m] = (int)(e & (kStageSkip - 1u));
+    start[m] = (int)(e0 & (kStageSkip - 1u));
   }
-  __syncthreads();
-  if (wid == 0) {
-    const bool in = lane < kRowsPer * kWaves;
-    const int t = in ? s_wtot[lane / kWaves][lane % kWaves] : 0;
-    const int ex = wave_incl_scan(t) - t;
-    if (in) s_wtot[lane / kWaves][lane % kWaves] = ex;
-  }
-  __syncthreads();
 #pragma unroll
-  for (int m = 0; m < kRowsPer; ++m) {
-    rs[m] += s_wtot[m][wid];
-    if (cnt[m] > 0 && rs[m] < kCap) atomicOr(&s_head[rs[m] >> 5], 1u << (rs[m] & 31));
+  for (int k = 0; k < kPer; ++k) {
+    if (f0 + k < L && (unsigned)d[k] < (unsigned)kCap) s_val[slot(d[k])] = A(v[k]) * A(xv[k]);
   }
-  __syncthreads();  // products and row starts in place
+  __syncthreads();  // the products in place
   // the segmented scan: positions past L start rows of their own (and add nothing).  Each
   // thread scans its positions in place; only the last position before its first row start
   // (k0) then needs what the threads before carry in - a row that ends later has its sum
   // complete from its own start.
   const int p0 = kPer * tid;
-  const unsigned hb = (s_head[p0 >> 5] >> (p0 & 31)) & 0xFFu;
   const unsigned hv = hb | (p0 + kPer > L ? ~0u << (L > p0 ? L - p0 : 0) : 0u);
   const int k0 = hv ? __builtin_ctz(hv) : kPer;
   A run = A(0), pre = A(0);
@@ -1224,7 +1222,8 @@ __device__ __forceinline__ void stage_combine_window(
     const int i = tid + m * NB;
     if (i >= nr || skip[m]) continue;
     const int row = row0 + i;
-    y[row_map ? row_map[row] : row] = cnt[m] > 0 ? T(s_val[slot(rs[m] + cnt[m] - 1)]) : T(0);
+    const bool any = end[m] > start[m] && end[m] <= L;
+    y[row_map ? row_map[row] : row] = any ? T(s_val[slot(end[m] - 1)]) : T(0);
   }
 }
 
@@ -1234,7 +1233,8 @@ template <typename T, typename A, int NB>
 __global__ __launch_bounds__(NB) void stage_combine_kernel(
     const i32x4* __restrict__ windows, const T* __restrict__ vals,
     const int16_t* __restrict__ dest, const T* __restrict__ xs,
-    const uint16_t* __restrict__ row_count, const int* __restrict__ rows,
+    const uint16_t* __restrict__ row_end, const uint8_t* __restrict__ heads,
+    const int* __restrict__ rows,
     const int* __restrict__ row_ptr, const int* __restrict__ slots,
     const A* __restrict__ panel_partials, int n_rows, int n_pblocks, T* __restrict__ y,
     const int* __restrict__ row_map) {
@@ -1247,7 +1247,7 @@ __global__ __launch_bounds__(NB) void stage_combine_kernel(
   }
   const int nw = (int)gridDim.x - n_pblocks;
   stage_combine_window<T, A, NB>(xcd_logical_block(b - n_pblocks, nw), windows, vals, dest, xs,
-                                 row_count, y, row_map);
+                                 row_end, heads, y, row_map);
 }
 
 template <typename T, typename A>
@@ -1301,7 +1301,7 @@ int launch_hybrid_combine(void* y, const int32_t* row_map, const void* xcs_parti
 template <typename T, typename A, int NB>
 int launch_stage_combine_nb(void* y, const int32_t* row_map, const int32_t* windows,
                             int64_t n_windows, const void* vals, const int16_t* dest,
-                            const void* xs, const uint16_t* row_count,
+                            const void* xs, const uint16_t* row_end, const uint8_t* heads,
                             const void* panel_partials, const int32_t* rows,
                             const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
                             hipStream_t st) {
@@ -1311,7 +1311,7 @@ int launch_stage_combine_nb(void* y, const int32_t* row_map, const int32_t* wind
   if (grid == 0) return FSP_OK;
   hipLaunchKernelGGL((stage_combine_kernel<T, A, NB>), dim3((unsigned)grid), dim3(NB), 0, st,
                      reinterpret_cast<const i32x4*>(windows), static_cast<const T*>(vals), dest,
-                     static_cast<const T*>(xs), row_count, rows, row_ptr, slots,
+                     static_cast<const T*>(xs), row_end, heads, rows, row_ptr, slots,
                      static_cast<const A*>(panel_partials), (int)n_rows, (int)n_pblocks,
                      static_cast<T*>(y), row_map);
   return check_hip(hipGetLastError(), "stage_combine_kernel launch");
@@ -1320,17 +1320,17 @@ int launch_stage_combine_nb(void* y, const int32_t* row_map, const int32_t* wind
 template <typename T, typename A>
 int launch_stage_combine(void* y, const int32_t* row_map, const int32_t* windows,
                          int64_t n_windows, int64_t window_cap, const void* vals,
-                         const int16_t* dest, const void* xs, const uint16_t* row_count,
-                         const void* panel_partials, const int32_t* rows,
+                         const int16_t* dest, const void* xs, const uint16_t* row_end,
+                         const uint8_t* heads, const void* panel_partials, const int32_t* rows,
                          const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
                          hipStream_t st) {
   if (window_cap <= kStageWinCap / 2)
     return launch_stage_combine_nb<T, A, 512>(y, row_map, windows, n_windows, vals, dest, xs,
-                                              row_count, panel_partials, rows, row_ptr, slots,
-                                              n_rows, st);
+                                              row_end, heads, panel_partials, rows, row_ptr,
+                                              slots, n_rows, st);
   return launch_stage_combine_nb<T, A, 1024>(y, row_map, windows, n_windows, vals, dest, xs,
-                                             row_count, panel_partials, rows, row_ptr, slots,
-                                             n_rows, st);
+                                             row_end, heads, panel_partials, rows, row_ptr,
+                                             slots, n_rows, st);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1451,8 +1451,9 @@ extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int
                                       int64_t n_out, const int32_t* windows, int64_t n_windows,
                                       int64_t window_cap, const void* vals,
                                       const int16_t* dest, const void* xs,
-                                      int64_t n_entries, const uint16_t* row_count,
-                                      const void* panel_partials, const int32_t* rows,
+                                      int64_t n_entries, const uint16_t* row_end,
+                                      const uint8_t* heads, const void* panel_partials,
+                                      const int32_t* rows,
                                       const int32_t* row_ptr, const int32_t* slots,
                                       int64_t n_rows, void* stream) {
   if (dtype != FSP_F32 && dtype != FSP_F64)
@@ -1461,7 +1462,7 @@ extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: negative size");
   if (n_windows > 0x3fffffffLL || n_rows > 0x3fffffffLL || n_entries > 0x7fffffffLL)
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: sizes beyond int32");
-  if (n_windows > 0 && (!y || !windows || !vals || !dest || !xs || !row_count))
+  if (n_windows > 0 && (!y || !windows || !vals || !dest || !xs || !row_end || !heads))
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null window-table pointer");
   if (n_windows > 0 && window_cap != kStageWinCap / 2 && window_cap != kStageWinCap)
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: window_cap must be " +
@@ -1471,13 +1472,16 @@ extern "C" int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: null panel-row pointer");
   if (!aligned16(windows))
     return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: windows must be 16-byte aligned");
+  if (n_windows > 0 && (!aligned16(vals) || !aligned16(dest) || !aligned16(xs)))
+    return set_error(FSP_EINVAL, "fsp_spmv_stage_combine: vals, dest and xs must be 16-byte "
+                                 "aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (row_map && n_out > 0) {
     int rc = (dtype == FSP_F32) ? fill_zero<float>(static_cast<float*>(y), n_out, st)
                                 : fill_zero<double>(static_cast<double*>(y), n_out, st);
     if (rc) return rc;
   }
-#define FSP_STAGE_ARGS y, row_map, windows, n_windows, window_cap, vals, dest, xs, row_count, \
+#define FSP_STAGE_ARGS y, row_map, windows, n_windows, window_cap, vals, dest, xs, row_end, heads, \
                        panel_partials, rows, row_ptr, slots, n_rows, st
   if (dtype == FSP_F32) {
     if (acc_f64) return launch_stage_combine<float, double>(FSP_STAGE_ARGS);

@@ -319,14 +319,19 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pc
  * pass; n_rows may be 0).  Same reference launches as fsp_spmv_csr.
  *   windows      n_windows int32 quadruples {row0, rows, entries L, first}: rows [row0, row0 +
  *                rows) (<= window_cap / 2), L <= window_cap entries at [first, first + L) of
- *                vals, dest and xs (n_entries in all, the arrays readable 8 past the end)
+ *                vals, dest and xs, first a multiple of 8 (a window otherwise is skipped);
+ *                the arrays (n_entries long, 16-byte aligned) readable up to the next
+ *                multiple of 8 past first + L
  *   window_cap   fsp_stage_window_cap() or half of it: workgroups of 1024 or 512 threads
  *   dest         int16 per entry: its rank in the window's (row, panel) order; the product
  *                vals[i] * xs[i] (in the accumulation type) goes to that position
- *   row_count    uint16 per row: the row's entries in its window (0xFFFF: a row the window
- *                leaves alone - y written by the panel rows); row r gets the sum of its
- *                positions (a segmented scan over the window's positions: 8 consecutive
+ *   row_end      uint16 per row: the end of the row's positions in its window (it starts
+ *                where the window's previous row ends, the first at 0), | 0x8000 for a row
+ *                the window leaves alone (y written by the panel rows); row r gets the sum of
+ *                its positions (a segmented scan over the window's positions: 8 consecutive
  *                positions per thread in order, then the threads in a fixed tree)
+ *   heads        window_cap / 8 bytes per window: bit q of byte t set where position 8t + q
+ *                starts a row (a row of the window with entries)
  *   row_map      NULL: layout row r is y[r]; else y[row_map[r]], and y[0..n_out) is zeroed
  *                first
  * Calls sharing xs or panel_partials must not overlap.
@@ -335,7 +340,7 @@ int fsp_spmv_stage_combine(int dtype, int acc_f64, void* y, const int32_t* row_m
                            int64_t n_out, const int32_t* windows, int64_t n_windows,
                            int64_t window_cap, const void* vals, const int16_t* dest,
                            const void* xs,
-                           int64_t n_entries, const uint16_t* row_count,
+                           int64_t n_entries, const uint16_t* row_end, const uint8_t* heads,
                            const void* panel_partials, const int32_t* rows,
                            const int32_t* row_ptr, const int32_t* slots, int64_t n_rows,
                            void* stream);

@@ -287,7 +287,7 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     def stage(dtype=0, n_windows=0, n_rows=0, tables=False):
         t = fake if tables else None
         return L.fsp_spmv_stage_combine(dtype, 1, t, None, 0, t, n_windows, 4096, t, t, t, 64,
-                                        t, None, None, None, None, n_rows, None)
+                                        t, t, None, None, None, None, n_rows, None)
 
     assert stage() == 0                           # nothing to run
     assert stage(dtype=7) == -3
@@ -296,11 +296,16 @@ def test_kernel_entry_points_reject_before_any_hip_call():
     assert stage(n_rows=4) == -1                  # panel rows without their arrays
     assert b"panel-row" in L.fsp_last_error()
     assert L.fsp_spmv_stage_combine(0, 1, fake, None, 0, fake + 4, 2, 4096, fake, fake, fake,
-                                    64, fake, None, None, None, None, 0, None) == -1
+                                    64, fake, fake, None, None, None, None, 0, None) == -1
     assert b"windows" in L.fsp_last_error() and b"aligned" in L.fsp_last_error()
     assert L.fsp_spmv_stage_combine(0, 1, fake, None, 0, fake, 2, 1000, fake, fake, fake, 64,
-                                    fake, None, None, None, None, 0, None) == -1
+                                    fake, fake, None, None, None, None, 0, None) == -1
     assert b"window_cap" in L.fsp_last_error()
+    for k in range(3):  # vals, dest, xs: 16-byte loads
+        tabs = [fake + 8 if j == k else fake for j in range(3)]
+        assert L.fsp_spmv_stage_combine(0, 1, fake, None, 0, fake, 2, 4096, *tabs, 64, fake,
+                                        fake, None, None, None, None, 0, None) == -1
+        assert b"16-byte" in L.fsp_last_error()
     assert L.fsp_stage_window_cap() == 8192 and L.fsp_stage_window_rows_cap() == 4096
 
 

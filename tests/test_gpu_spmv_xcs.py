@@ -183,8 +183,8 @@ def test_xstage_marks_every_array(dev, monkeypatch):
     torch.cuda.synchronize()
     lg = layout.long
     wanted = (layout.scol, layout.stage_info, layout.seg_delta, layout.xs, layout.vals,
-              layout.dest, layout.row_count, layout.windows, layout.jobs, layout.job_panel,
-              layout.stage_jobs, lg.partials, lg.vals, lg.pcol, lg.chunk_info, lg.rows,
+              layout.dest, layout.row_end, layout.heads, layout.windows, layout.jobs,
+              layout.job_panel, layout.stage_jobs, lg.partials, lg.vals, lg.pcol, lg.chunk_info, lg.rows,
               lg.row_ptr, lg.slots)
     got = [ts for order, ts in seen if order is layout._order]
     assert got, "the layout's stream order was not consulted"

@@ -41,37 +41,43 @@ def _stage(layout, x):
                 if q > 0 and mark[e]:
                     seg += 1
                 out = e + delta[seg]
-                assert 0 <= out < layout.n_entries and src[out] == -1
+                assert 0 <= out < layout.xs.numel() - 8 and src[out] == -1
                 src[out] = e
                 xs[out] = x[min((jp[j] << cb) + col[e], x.size - 1)]
     return xs, src
 
 
+def _row_spans(layout, row0, nr):
+    """The window's rows' positions [start, end) from row_end (a row starts where the one
+    before ends, the first at 0) and which of them the window leaves alone (bit 15)."""
+    re = layout.row_end.numpy().view(np.uint16).astype(np.int64)[row0:row0 + nr]
+    end = re & 0x7FFF
+    start = np.concatenate([[0], end[:-1]])
+    return start, end, (re & 0x8000) != 0
+
+
 def _emulate(layout, x, y, row_map=None, acc=np.float64):
     """stage_combine_kernel's windows: entry i of the window adds vals[i] * xs[i] at LDS
-    position dest[i]; row r of the window gets its row_count[r] positions summed in order
-    (count 0xFFFF: left alone)."""
+    position dest[i]; row r of the window gets its positions [row_end[r-1], row_end[r]) summed
+    in order (bit 15: left alone)."""
     xs, _ = _stage(layout, x)
     xs = xs.astype(acc)
     vals = layout.vals.numpy().astype(acc)
     dest = layout.dest.numpy().astype(np.int64)
-    rc = layout.row_count.numpy().view(np.uint16).astype(np.int64)
     for row0, nr, L, first in layout.windows.numpy().astype(np.int64):
         s = np.full(layout.window_cap, np.nan)
         for i in range(first, first + L):
             s[dest[i]] = acc(vals[i] * xs[i])
-        pos = 0
+        start, end, skip = _row_spans(layout, row0, nr)
         for i in range(nr):
-            c = rc[row0 + i]
-            if c == 0xFFFF:
+            if skip[i]:
                 continue
             acc_v = acc(0)
-            for u in range(c):
-                acc_v = acc(acc_v + s[pos + u])
+            for u in range(start[i], end[i]):
+                acc_v = acc(acc_v + s[u])
             out = row0 + i if row_map is None else row_map[row0 + i]
             y[out] = acc_v
-            pos += c
-        assert pos == L
+        assert end[-1] == L
     return y
 
 
@@ -87,10 +93,25 @@ def _check(layout, vals, cols, ip, long_mask):
     assert w[0, 0] == 0 and w[-1, 0] + w[-1, 1] == n_rows
     assert np.all(w[1:, 0] == w[:-1, 0] + w[:-1, 1])
     assert np.all(w[:, 1] <= layout.window_cap // 2) and np.all(w[:, 2] <= layout.window_cap)
-    assert np.all(w[1:, 3] == w[:-1, 3] + w[:-1, 2]) and w[0, 3] == 0
-    rc = layout.row_count.numpy().view(np.uint16).astype(np.int64)
-    assert np.all(rc[long_mask] == 0xFFFF)
-    assert np.array_equal(rc[short], lengths[short])
+    # window starts: packed at multiples of 8 entries
+    assert np.all(w[1:, 3] == w[:-1, 3] + (w[:-1, 2] + 7) // 8 * 8) and w[0, 3] == 0
+    assert layout.vals.numel() == layout.n_positions + 8 == layout.xs.numel()
+    assert layout.n_positions == w[-1, 3] + (w[-1, 2] + 7) // 8 * 8
+    # row ends: the rows' lengths (none for the long rows, marked), and the row-start bits
+    # exactly where a row with entries starts
+    heads = layout.heads.numpy()
+    hb = layout.window_cap // 8
+    counts_all = np.zeros(n_rows, dtype=np.int64)
+    for k, (row0, nr, L, first) in enumerate(w):
+        start, end, skip = _row_spans(layout, row0, nr)
+        assert np.array_equal(skip, long_mask[row0:row0 + nr]) and end[-1] == L
+        counts_all[row0:row0 + nr] = end - start
+        bits = np.unpackbits(heads[k * hb:(k + 1) * hb], bitorder="little")
+        want_bits = np.zeros(layout.window_cap, dtype=np.uint8)
+        want_bits[start[end > start]] = 1
+        assert np.array_equal(bits, want_bits)
+    assert np.all(counts_all[long_mask] == 0)
+    assert np.array_equal(counts_all[short], lengths[short])
     # staged chunks: each job's inside its panel, every panel with a job, chunks covering
     # the staged entries; every window position written by exactly one staged entry
     chunk = caps["stage_chunk"]
@@ -101,13 +122,17 @@ def _check(layout, vals, cols, ip, long_mask):
     assert np.array_equal(np.unique(jp), np.arange(P))  # every panel has a job
     x_probe = np.arange(layout.n_cols, dtype=np.float64)  # x[c] = c names the column
     xs, src = _stage(layout, x_probe)
-    assert np.all(src[:layout.n_entries] >= 0)
+    written = np.zeros(src.size, dtype=bool)
+    for row0, nr, L, first in w:
+        written[first:first + L] = True
+    assert np.all(src[written] >= 0) and np.all(src[~written] == -1)
+    assert int(written.sum()) == layout.n_entries
     # every short entry once, its LDS position its rank in (row, panel) order
     v = layout.vals.numpy()
     dest = layout.dest.numpy().astype(np.int64)
     got = []
     for row0, nr, L, first in layout.windows.numpy().astype(np.int64):
-        counts = np.where(rc[row0:row0 + nr] == 0xFFFF, 0, rc[row0:row0 + nr])
+        counts = counts_all[row0:row0 + nr]
         row_of_pos = np.repeat(np.arange(row0, row0 + nr), counts)
         panel_at = np.full(L, -1)
         for i in range(first, first + L):

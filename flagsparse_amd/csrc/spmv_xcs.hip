@@ -732,6 +732,10 @@ constexpr uint32_t kRunStart = 0x8000u;  // pcol: the entry starts a run
 // same round; every store is issued (entries not in use store past the buffer's range, which
 // the hardware drops), so the compiler keeps its count of the operations in flight.
 constexpr int kStageChunk = (int)kStageChunkEntries;
+// Chunk buffers of the staging loop (columns two chunks ahead).  Measured on MI355X: 3 / 4 / 6
+// buffers, cfg3's panel pass 128.4 / 129.4 / 131.8 us, cfg4's 59.2 / 62.4 / 64.5 us.
+constexpr int kStageBuffers = 3;
+static_assert(kStageBuffers >= 3, "a chunk's offsets are loaded a round after its columns");
 constexpr uint32_t kSegStart = 0x8000u;  // scol: the entry opens a segment
 
 template <typename T>
@@ -768,16 +772,8 @@ __device__ __forceinline__ void stage_panel_chunks(const T* sx, uint32_t cmask,
     k.info = sinfo[cc];
   };
   auto load_dl = [&](Chunk& k) { k.dl = sdelta[k.info.x + lane]; };
-  int c = c0 + wid;
-  if (c >= c1) return;  // the whole wave
-  Chunk cur, nxt, nn;
-  load_cols(c, cur);
-  load_cols(c + kStride, nxt);
-  load_dl(cur);
-  for (; c < c1; c += kStride) {
-    load_dl(nxt);
-    load_cols(c + 2 * kStride, nn);
-    const unsigned base = (unsigned)(c * kStageChunk + lane);
+  auto process = [&](const Chunk& cur, int cc) {
+    const unsigned base = (unsigned)(cc * kStageChunk + lane);
     int seen = 0;  // segment starts after the chunk's first entry, in the rounds before
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
@@ -794,8 +790,26 @@ __device__ __forceinline__ void stage_panel_chunks(const T* sx, uint32_t cmask,
       store_staged<T>(xs, q * kWave + lane < cur.info.y ? (e + (unsigned)delta) * (unsigned)sizeof(T)
                                                         : kDropOffset, xv);
     }
-    cur = nxt;
-    nxt = nn;
+  };
+  int c = c0 + wid;
+  if (c >= c1) return;  // the whole wave
+  // kStageBuffers chunk buffers: buffer b of a round holds the chunk b strides on; before one
+  // is processed, the next one's offsets and the columns of the chunk kStageBuffers - 1
+  // strides ahead are requested.
+  constexpr int kSB = kStageBuffers;
+  Chunk buf[kSB];
+#pragma unroll
+  for (int b = 0; b + 1 < kSB; ++b) load_cols(c + b * kStride, buf[b]);
+  load_dl(buf[0]);
+  for (; c < c1; c += kSB * kStride) {
+#pragma unroll
+    for (int b = 0; b < kSB; ++b) {
+      const int cur = c + b * kStride;
+      if (cur >= c1) break;
+      load_dl(buf[(b + 1) % kSB]);
+      load_cols(cur + (kSB - 1) * kStride, buf[(b + kSB - 1) % kSB]);
+      process(buf[b], cur);
+    }
   }
 }
 

@@ -1069,9 +1069,6 @@ class XstageLayout:
         # panel part whatever their length per panel, so that windows stay nearly full.
         long_mask = long_mask | (lengths > caps["stage_window"] // 8)
         short_len = torch.where(long_mask, 0, lengths)
-        entry_row = torch.repeat_interleave(torch.arange(n_rows, device=dev), lengths,
-                                            output_size=self.nnz)
-        entry_long = long_mask[entry_row]
 
         # 1. Windows: consecutive rows whose short entries start in [kC, (k + 1) C), so that
         #    a window holds at most C - 1 + (the longest short row) <= win_cap entries, cut
@@ -1088,10 +1085,11 @@ class XstageLayout:
         del key, sub, w0, w0_first, start
         W = int(win_of_row[-1].item()) + 1 if n_rows else 0
         win_row0 = torch.searchsorted(win_of_row, torch.arange(W, device=dev))
-        win_rows_n = torch.bincount(win_of_row, minlength=W)
-        win_len = torch.zeros(W, dtype=torch.int64, device=dev).index_add_(0, win_of_row,
-                                                                           short_len)
-        win_first = torch.cumsum(win_len, 0) - win_len
+        win_rows_n = torch.diff(win_row0, append=win_row0.new_full((1,), n_rows))
+        short_end = torch.cumsum(short_len, 0)  # entries of the rows up to each one
+        sstart = short_end - short_len
+        win_first = sstart[win_row0] if W else sstart[:0]
+        win_len = torch.diff(win_first, append=short_end[-1:]) if W else win_first
         if W and (int(win_len.max().item()) > win_cap or int(win_rows_n.max().item()) > win_rows):
             raise AssertionError("staged-x windows: a window past its caps")
         self.n_windows = W
@@ -1101,19 +1099,22 @@ class XstageLayout:
         #    column.  Each panel's segments fill chunks of `chunk` entries, a chunk closing
         #    early rather than hold more than 64 segments (the kernel's offsets per chunk, the
         #    panel layout's chunk planner with segments for runs); the rest is padding.
-        pick = torch.nonzero(~entry_long).flatten()
-        er = entry_row[pick]
-        del entry_row, entry_long
-        ec = cols[pick].to(torch.int64)
-        n_short = int(pick.numel())
+        n_short = int(short_end[-1].item()) if n_rows else 0
         self.n_entries = n_short
+        ar = torch.arange(n_short, device=dev)
+        short_rows = torch.nonzero(short_len).flatten()
+        er = torch.repeat_interleave(short_rows, short_len[short_rows], output_size=n_short)
+        del short_rows
+        pick = rp[er] + (ar - sstart[er])  # the short entries' CSR positions, in order
+        ec = cols[pick].to(torch.int64)
         pan = ec >> cb
         ew = win_of_row[er]
         Wk = max(W, 1)
         key = pan * Wk + ew
+        if P * Wk < (1 << 31):
+            key = key.to(torch.int32)  # half the radix passes
         ks, perm = torch.sort(key, stable=True)  # stable: row order inside a segment
         del key
-        ar = torch.arange(n_short, device=dev)
         seg_start = torch.ones(n_short, dtype=torch.bool, device=dev)
         if n_short > 1:
             seg_start[1:] = ks[1:] != ks[:-1]
@@ -1122,7 +1123,8 @@ class XstageLayout:
         n_seg = int(first_e.numel())
         self.n_segments = n_seg
         seg_len = torch.diff(first_e, append=torch.tensor([n_short], device=dev))
-        seg_panel = ks[first_e] // Wk
+        seg_ks = ks[first_e].to(torch.int64)  # each segment's (panel, window) key
+        seg_panel = seg_ks // Wk
         panel_segs = torch.zeros(P + 1, dtype=torch.int64, device=dev)
         torch.cumsum(torch.bincount(seg_panel, minlength=P), 0, out=panel_segs[1:])
         seg_pos, panel_end = plan_panel_chunks(panel_segs, seg_len, chunk, 64)
@@ -1164,10 +1166,13 @@ class XstageLayout:
         self.long = None
         chunk0 = torch.zeros(P + 1, dtype=torch.int64, device=dev)
         if long_rows.numel():
-            lpick = torch.nonzero(long_mask[torch.repeat_interleave(
-                torch.arange(n_rows, device=dev), lengths, output_size=self.nnz)]).flatten()
             long_ptr = torch.zeros(long_rows.numel() + 1, dtype=torch.int64, device=dev)
             torch.cumsum(lengths[long_rows], 0, out=long_ptr[1:])
+            n_long = self.nnz - n_short
+            lr = torch.repeat_interleave(torch.arange(long_rows.numel(), device=dev),
+                                         lengths[long_rows], output_size=n_long)
+            lpick = rp[long_rows][lr] + (torch.arange(n_long, device=dev) - long_ptr[lr])
+            del lr
             self.long = PanelLayout(data[lpick], cols[lpick], long_ptr, n_cols, long_rows)
             del lpick
             lg = self.long
@@ -1199,8 +1204,8 @@ class XstageLayout:
         #    positions to its window positions.
         seg_chunk = seg_pos // chunk
         seg_job = torch.searchsorted(s_lo, seg_chunk, right=True) - 1
-        seg_key = (ks[first_e] % Wk) * (XCD_COUNT * P) + \
-            (seg_job % XCD_COUNT) * P * int(STAGE_XCD_ORDER) + ks[first_e] // Wk
+        seg_key = (seg_ks % Wk) * (XCD_COUNT * P) + \
+            (seg_job % XCD_COUNT) * P * int(STAGE_XCD_ORDER) + seg_ks // Wk
         seg_order = torch.sort(seg_key)[1]
         ordered_len = seg_len[seg_order]
         seg_wpos = torch.empty_like(seg_len)
@@ -1211,19 +1216,24 @@ class XstageLayout:
         n_pos = int((win_start[-1] + win_pad[-1]).item()) if W else 0
         if n_pos > _INDEX_LIMIT_INT32 - 64:
             raise ValueError("too many entries for the staged-x layout")
-        seg_wpos += (win_start - win_first)[ks[first_e] % Wk]
+        seg_wpos += (win_start - win_first)[seg_ks % Wk]
         del seg_key, seg_order, ordered_len, seg_chunk, seg_job, s_lo, win_pad
         sdelta = torch.zeros(n_seg + 64, dtype=torch.int64, device=dev)
         sdelta[:n_seg] = seg_wpos - seg_pos
         self.seg_delta = sdelta.to(torch.int32).contiguous()
         wpos = seg_wpos[seg_id] + ar - first_e[seg_id]
         del seg_len, seg_wpos, first_e, seg_start, seg_id, spos, seg_pos
-        rank_key = er * P + pan  # CSR order is row order: a stable sort by (row, panel)
-        order2 = torch.sort(rank_key, stable=True)[1]
-        del rank_key
-        rank = torch.empty_like(order2)
-        rank[order2] = ar
-        del order2, ar
+        # rank in (row, panel) order: CSR order is row order, and where each row's panels
+        # already rise (sorted columns) it is the CSR order itself; else a stable sort
+        unordered = n_short > 1 and bool(((er[1:] == er[:-1]) & (pan[1:] < pan[:-1])).any())
+        if unordered:
+            order2 = torch.sort(er * P + pan, stable=True)[1]
+            rank = torch.empty_like(order2)
+            rank[order2] = ar
+            del order2
+        else:
+            rank = ar
+        del ar
         slot = rank - win_first[ew]
         del rank
         self.n_positions = n_pos
@@ -1236,18 +1246,16 @@ class XstageLayout:
         del dest, slot, wpos, perm, pick, ec, pan, ew, er, ks
         # per row the end of its positions in its window (| 0x8000: a row left to the panel
         # part); per window a bit per position where a row starts
-        rstart = torch.cumsum(short_len, 0) - short_len
-        if n_rows:
-            rstart -= win_first[win_of_row]
+        rstart = sstart - win_first[win_of_row] if n_rows else sstart
         re = (rstart + short_len) | torch.where(long_mask, 0x8000, 0)
         self.row_end = torch.where(re >= (1 << 15), re - (1 << 16), re).to(torch.int16)
         del re
         opens = torch.nonzero(short_len > 0).flatten()
-        hpos = rstart[opens] + win_of_row[opens] * win_cap
-        heads = torch.zeros(W * win_cap // 8 + 1, dtype=torch.int32, device=dev)
-        heads.index_add_(0, hpos >> 3, (1 << (hpos & 7)).to(torch.int32))
-        self.heads = heads.to(torch.uint8)
-        del heads, hpos, opens, rstart
+        bits = torch.zeros(W * win_cap + 8, dtype=torch.uint8, device=dev)
+        bits[rstart[opens] + win_of_row[opens] * win_cap] = 1
+        weight = torch.tensor([1, 2, 4, 8, 16, 32, 64, 128], dtype=torch.uint8, device=dev)
+        self.heads = (bits.view(-1, 8) * weight).sum(1, dtype=torch.uint8)
+        del bits, opens, rstart
         self.windows = torch.stack([win_row0, win_rows_n, win_len, win_start], 1).to(
             torch.int32).contiguous()
         self._keep = (self.scol, self.stage_info, self.seg_delta, self.xs, self.vals, self.dest,

@@ -168,13 +168,14 @@ def window(request, monkeypatch):
     return request.param
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
-def test_xstage_power_law_with_long_rows(seed, window):
+@pytest.mark.parametrize("seed,unsorted", [(0, False), (1, False), (2, False), (0, True)])
+def test_xstage_power_law_with_long_rows(seed, unsorted, window):
+    # unsorted: each row's columns in falling order (the (row, panel) ranks then need a sort)
     rng = np.random.default_rng(seed)
     n_cols = 300000  # 10 panels of 2^15 columns
     lengths = rng.zipf(1.6, 5000).clip(max=40000)
     lengths[rng.integers(0, 5000, 300)] = 0
-    vals, cols, ip, x = _case(lengths, n_cols, seed)
+    vals, cols, ip, x = _case(lengths, n_cols, seed, unsorted=unsorted)
     long_mask = lengths >= panel_row_min(n_cols, 4)
     assert 0 < long_mask.sum() < 5000
     lay = XstageLayout(vals, cols, ip, n_cols, torch.as_tensor(long_mask))

@@ -7,7 +7,9 @@ size-independent properties that hold exactly:
   cfg3  8M power-law fp32, int64 indices (the default staged-x layout, and the XCS + panel
         hybrid): oracle bars incl. <= 1 ulp from float32(fp64 oracle) on the default path; two
         calls bit-identical
-  cfg4  COO 2M, 41.9M entries: oracle bars; A * 0 = 0
+  cfg3  the same in fp64 (staged-x): oracle bars, two calls bit-identical, linearity
+  cfg4  COO 2M, 41.9M entries (staged-x): oracle bars for x and x = 1; A * 0 = 0; two calls
+        bit-identical
   cfg5  SpMM N=64 fp32 (opt), N=16 fp32 (base and opt) and N=16 fp64 (base): oracle bars;
         column j of A B = A B[:, j] (the SpMV of the same matrix), within 1 ulp where both
         round an fp64 sum of the same products to float32 (the fp32 base path);
@@ -82,14 +84,38 @@ def test_cfg3_full(dev, monkeypatch, mode):
     _bars(fs.flagsparse_spmv_csr(x=x, prepared=p, use_opt=True), ref, torch.float32)
 
 
+def test_cfg3_full_fp64(dev):
+    # the staged-x layout with float64 entries (14-bit panel columns, fp64 staged values)
+    print("full size cfg3 fp64", flush=True)
+    data, idx, ptr, x, shape = synthetic.csr_powerlaw(dtype=torch.float64, device=dev)
+    p = fs.prepare_spmv_csr(data, idx, ptr, shape)
+    assert p._kernel(False).kind == "xstage"
+    ref = oracle.spmv_csr(ptr.cpu(), idx.cpu(), data.cpu(), x.cpu())
+    y = fs.flagsparse_spmv_csr(x=x, prepared=p)
+    _bars(y, ref, torch.float64)
+    assert torch.equal(y, fs.flagsparse_spmv_csr(x=x, prepared=p))
+    # linearity: A(2x - z) = 2Ax - Az to fp64 rounding
+    z = synthetic.uniform_values(5, 8, shape[1], torch.float64, dev)
+    lhs = fs.flagsparse_spmv_csr(x=2 * x - z, prepared=p).cpu().numpy()
+    rhs = 2 * ref - oracle.spmv_csr(ptr.cpu(), idx.cpu(), data.cpu(), z.cpu())
+    assert oracle.rel_l2(lhs, rhs) <= 1e-12
+
+
 def test_cfg4_full(dev):
     print("full size cfg4", flush=True)
     data, row, col, x, shape = synthetic.coo_uniform(device=dev)
     p = fs.prepare_spmv_coo(data, row, col, shape)
+    assert p._run_layout().kind == "xstage"
     ref = oracle.spmv_coo(row.cpu(), col.cpu(), data.cpu(), x.cpu(), shape[0])
-    _bars(fs.flagsparse_spmv_coo(x=x, prepared=p), ref, torch.float32)
+    y = fs.flagsparse_spmv_coo(x=x, prepared=p)
+    _bars(y, ref, torch.float32)
+    assert torch.equal(y, fs.flagsparse_spmv_coo(x=x, prepared=p))
     zero = torch.zeros_like(x)
     assert int(torch.count_nonzero(fs.flagsparse_spmv_coo(x=zero, prepared=p))) == 0
+    # x = 1: every row's sum of values, against the oracle's
+    ones = torch.ones_like(x)
+    ref1 = oracle.spmv_coo(row.cpu(), col.cpu(), data.cpu(), ones.cpu(), shape[0])
+    _bars(fs.flagsparse_spmv_coo(x=ones, prepared=p), ref1, torch.float32)
 
 
 @pytest.mark.parametrize("dtype,N,paths", [(torch.float32, 64, ("opt",)),

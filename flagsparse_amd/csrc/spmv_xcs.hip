@@ -80,6 +80,17 @@ __device__ __forceinline__ float dpp_bc(float v) {
   return __int_as_float(dpp_bc<CTRL, ROW_MASK>(__float_as_int(v)));
 }
 
+// Lane l's value of v (l wave-uniform).
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double lane_value(double v, int l) {
+  const int64_t b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffff), l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double(((int64_t)hi << 32) | (uint32_t)lo);
+}
+
 // One step of the wave scans of the XCS and panel kernels: (h, v) a segmented inclusive scan
 // (h: a run starts in this lane's part; combine(a, b) = (a.h | b.h, b.h ? b.v : a.v + b.v)), c
 // a plain one, with the source lane that the DPP control CTRL selects.  Lanes without a source
@@ -1139,7 +1150,7 @@ constexpr uint32_t kStageSkip = 0x8000u;  // row_end: a row the window leaves al
 // readable up to the next multiple of 8 past first + L.  Products go to LDS position dest (the
 // entry's rank in (row, panel) order); a segmented scan over the positions (thread t:
 // positions 8t .. 8t + 7 in order, marked where a row starts by the bits of heads[w * NB + t],
-// then the threads in a fixed DPP tree and the waves in order) leaves each row's sum at its
+// then the threads and the waves in fixed DPP trees) leaves each row's sum at its
 // last position, and row r of the window, positions [row_end[r - 1], row_end[r]) (0 for the
 // first row), writes it to y.
 template <typename T, typename A, int NB>
@@ -1226,8 +1237,17 @@ __device__ __forceinline__ void stage_combine_window(
   const A lane_c = dpp_bc<kDppWaveShr1, 0xF>(v_in);  // lane 0: 0
   const int lane_h = dpp_bc<kDppWaveShr1, 0xF>(h_in);
   __syncthreads();
-  A wave_c = A(0);  // what the waves before carry into this one, in wave order
-  for (int j = 0; j < wid; ++j) wave_c = s_wh[j] ? s_wv[j] : wave_c + s_wv[j];
+  // What the waves before carry into this one: lane j takes wave j's (start, carry-out), a
+  // segmented scan over lanes 0 .. kWaves - 1 (a fixed tree inside one 16-lane row), read at
+  // lane wid - 1 (a loop over the waves before, one LDS read after another, measured slower).
+  static_assert(kWaves <= 16, "the waves' carries are scanned inside one DPP row");
+  int hw = lane < kWaves ? s_wh[lane] : 0, cw = 0;
+  A vw = lane < kWaves ? s_wv[lane] : A(0);
+  seg_scan_step<kDppRowShr1, 0xF>(hw, vw, cw);
+  seg_scan_step<kDppRowShr1 + 1, 0xF>(hw, vw, cw);
+  seg_scan_step<kDppRowShr1 + 3, 0xF>(hw, vw, cw);
+  seg_scan_step<kDppRowShr1 + 7, 0xF>(hw, vw, cw);
+  const A wave_c = wid > 0 ? lane_value(vw, wid - 1) : A(0);
   const A cin = lane_h ? lane_c : wave_c + lane_c;
   if (k0 > 0 && p0 + k0 - 1 < L) s_val[slot(p0) + k0 - 1] = cin + pre;
   __syncthreads();  // every row's sum at its last position

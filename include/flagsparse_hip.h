@@ -329,7 +329,8 @@ int fsp_spmv_panels(int dtype, int acc_f64, const void* vals, const uint16_t* pc
  *                where the window's previous row ends, the first at 0), | 0x8000 for a row
  *                the window leaves alone (y written by the panel rows); row r gets the sum of
  *                its positions (a segmented scan over the window's positions: 8 consecutive
- *                positions per thread in order, then the threads in a fixed tree)
+ *                positions per thread in order, then the threads and the waves in fixed
+ *                trees)
  *   heads        window_cap / 8 bytes per window: bit q of byte t set where position 8t + q
  *                starts a row (a row of the window with entries)
  *   row_map      NULL: layout row r is y[r]; else y[row_map[r]], and y[0..n_out) is zeroed

@@ -1039,8 +1039,8 @@ class XcsHybridLayout:
 
 class XstageLayout:
     """Long rows in a PanelLayout (``self.long``, None when there are none), the other rows
-    staged (module docstring).  Built on the device.  ValueError when x needs more panels than
-    the combine takes (fsp_stage_panels_cap())."""
+    staged (module docstring).  Built on the device.  ValueError when the staged entries pass
+    the kernels' 32-bit offsets (or the long rows the panel layout's limits)."""
 
     kind = "xstage"
 

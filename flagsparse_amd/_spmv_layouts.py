@@ -1058,8 +1058,8 @@ class XstageLayout:
         # Windows of the larger size where the smaller would leave each panel's segment of a
         # window under STAGE_SEGMENT_MIN entries: the panel jobs write the segments of a window
         # from many CUs, and short segments share more lines (measured on MI355X, cfg3 - 256
-        # panels -: 8192 against 4096 entries 205 against 214 us a call; cfg4 - 64 panels -:
-        # 142 against 137 us).
+        # panels -: 8192 against 4096 entries 195.4 against 207.2 us a call; cfg4 - 64 panels
+        # -: 132.9 against 133.5 us, its panel pass 5.6 us faster and its combine 4.6 slower).
         win_cap, win_rows = caps["stage_window"], caps["stage_window_rows"]
         if FORCE_STAGE_WINDOW:
             win_cap = int(FORCE_STAGE_WINDOW)
